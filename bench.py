@@ -1,0 +1,160 @@
+"""Benchmark of the quantized dequant-GEMV hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: Q4_K GEMV, W 14336 x 4096 in GGUF Q4_K
+superblocks, f32 x ~ N(0,1), batch 1.  A step is one hip_gemv_async call over
+one of ROT weight copies (>= 768 MB in total, so the 256 MB MALL cannot serve
+repeats); weights and x are resident in HBM before the timed region.
+Prints ONE JSON line.  `value` = algorithmic bytes (weights + x + y) per step x K
+/ wall time of the K steps (HIP events on the launch stream).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+Q4K = 12
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def device_q4k(torch, out_dim, in_dim, seed):
+    """Synthetic Q4_K weights generated on the device (same distributions as
+    saient_quartz_amd.synth.weights, torch RNG stream)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    nb = out_dim * in_dim // 256
+    blk = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device="cuda", generator=g)
+    d = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.01).half()
+    dmin = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.005).half()
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:4] = dmin.view(torch.uint8).view(nb, 2)
+    return blk.reshape(-1)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
+                                   "(the GEMV shards by output rows, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    from saient_quartz_amd import lib, type_size
+    from saient_quartz_amd.api import check
+
+    L = lib()
+    out_dim, in_dim = 14336, 4096
+    wbytes = type_size(Q4K, out_dim * in_dim)
+    alg_bytes = wbytes + 4 * in_dim + 4 * out_dim
+    rot = max(3, -(-768 * 2**20 // wbytes))
+    Ws = [device_q4k(torch, out_dim, in_dim, seed=20261201 + 1 + i) for i in range(rot)]
+    x = torch.randn(in_dim, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7))
+    y = torch.empty(out_dim, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(i):
+        check("hip_gemv_async", L.hip_gemv_async(Q4K, Ws[i % rot].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                 in_dim, out_dim, sp))
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Timed region: K back-to-back steps, events on the launch stream.
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / args.steps
+
+    # Per-launch kernel duration: an event pair around each launch.
+    n_k = min(args.steps, 100)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_k)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(out_dim, in_dim, args.cpu_seconds)
+
+    rec = {
+        "metric": "Q4_K GEMV effective HBM GB/s (% of peak); 8B-shape decode tok/s at 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, f32 activations/accumulate",
+        "data": f"synthetic seeded GGUF Q4_K blocks, {rot} rotated copies ({rot * wbytes / 2**20:.0f} MiB)",
+        "config": {"workload": "Q4_K dequant-GEMV 14336x4096 (Llama-3-8B ffn_up), batch 1",
+                   "out_dim": out_dim, "in_dim": in_dim, "batch": 1, "bytes_per_step": alg_bytes},
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qh_gemv_unit<FmtQ4K, 4>", "kernel_us": round(kern_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def cpu_baseline(out_dim, in_dim, seconds):
+    """Quartz's CPU GEMV path (fused q4k_row, rayon-parallel rows) restated in C,
+    timed on this host's cores over a bounded number of repetitions."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import Oracle
+    from saient_quartz_amd import synth
+
+    o = Oracle.load()
+    cores = min(os.cpu_count() or 1, 16)
+    o.set_threads(cores)
+    data = synth.weights(Q4K, out_dim, in_dim, seed=20261202)
+    x = synth.activations(1, in_dim, seed=3)[0]
+    o.gemv(Q4K, x, data, in_dim, out_dim)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        o.gemv(Q4K, x, data, in_dim, out_dim)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    alg = data.nbytes + 4 * in_dim + 4 * out_dim
+    return {"value": round(alg / dt / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} x Q4_K 14336x4096 GEMV (C restatement of q4k_row, OpenMP over rows), "
+                      f"{dt * 1e3:.2f} ms each"}
+
+
+if __name__ == "__main__":
+    main()

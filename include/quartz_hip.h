@@ -1,0 +1,105 @@
+/*
+ * quartz_hip.h -- C ABI of libquartz_hip.so, the MI355X (gfx950) quantized
+ * dequant-GEMV backend for Quartz.
+ *
+ * Drop-in for the `cuda_*` extern block of Quartz's CUDA backend
+ * (src/cuda.rs:6-55, defined in src/cuda_kernels.cu:1025-1125): every symbol
+ * below with a `cuda_` twin takes the same arguments in the same order with the
+ * same meaning, with `hip_` in place of `cuda_`.  Differences, all additive:
+ *   - entry points return an int status (0 = ok, negative = error, see QH_ERR_*)
+ *     where the reference returns void;
+ *   - `_async` variants take a hipStream_t passed as `void*` (NULL = the legacy
+ *     default stream, which is what the synchronous forms use);
+ *   - hip_gemm / hip_gemm_async (batched tokens) and hip_dequant are new: the
+ *     reference has them only on the CPU (src/dequant.rs:143, :1239).
+ *
+ * Layouts: d_data points at out_dim contiguous GGUF rows of in_dim/QK blocks (no
+ * row padding; GGUF row j holds elements [j*in_dim, (j+1)*in_dim)).  x and y are
+ * f32.  Batched activations are token-major: x[n][in_dim], y[n][out_dim].
+ * y is overwritten, never accumulated.  Buffers are caller-owned device memory;
+ * no entry point allocates device memory.  Calls on one stream are ordered; the
+ * library keeps no per-call host state and is safe to call from several host
+ * threads on distinct streams.
+ */
+#ifndef QUARTZ_HIP_H
+#define QUARTZ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define QH_OK 0
+#define QH_ERR_TYPE (-1)  /* unsupported ggml_type (y is zero-filled, as the reference does) */
+#define QH_ERR_DIMS (-2)  /* in_dim <= 0, out_dim/n < 0, or in_dim not a multiple of the block size */
+#define QH_ERR_NULL (-3)  /* null device pointer with non-empty dims */
+#define QH_ERR_HIP (-4)   /* HIP runtime error; hip_last_error() has the message */
+#define QH_ERR_RANGE (-5) /* argument outside a documented limit */
+
+/* GGML type ids handled: 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0,
+ * 10 Q2_K, 12 Q4_K, 13 Q5_K, 14 Q6_K, 16 IQ2_XXS, 17 IQ2_XS, 20 IQ4_NL,
+ * 21 IQ3_S, 22 IQ2_S, 30 BF16  (src/gguf.rs:172-191; 2 and 3 are GGUF types the
+ * reference lacks). */
+
+/* y[j] = sum_k W[j,k] x[k].  Replaces cuda_gemv (src/cuda_kernels.cu:1046-1077,
+ * Rust decl src/cuda.rs:7-8). */
+int hip_gemv(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim, int out_dim);
+int hip_gemv_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
+                   int out_dim, void* stream);
+
+/* Y[t][j] = sum_k W[j,k] X[t][k] for t < n (token-major).  GPU counterpart of
+ * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv. */
+int hip_gemm(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim, int out_dim,
+             int n);
+int hip_gemm_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
+                   int out_dim, int n, void* stream);
+
+/* Up to 4 expert GEMVs in one call.  Replaces cuda_gemv_moe4
+ * (src/cuda_kernels.cu:1085-1106, Rust decl src/cuda.rs:39-45); any type. */
+int hip_gemv_moe4(uint32_t ggml_type, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,
+                  const uint8_t* w3, const float* xi0, const float* xi1, const float* xi2, const float* xi3,
+                  float* o0, float* o1, float* o2, float* o3, int n_act, int in_dim, int out_dim);
+
+/* Bit-exact decode of n_elems elements to f32 on the GPU.  GPU counterpart of
+ * dequant::dequant (src/dequant.rs:1239-1258); n_elems must be a multiple of
+ * the block size. */
+int hip_dequant(uint32_t ggml_type, const uint8_t* d_data, float* d_out, size_t n_elems);
+int hip_dequant_async(uint32_t ggml_type, const uint8_t* d_data, float* d_out, size_t n_elems, void* stream);
+
+/* Byte size of n_elems elements of ggml_type; 0 for an unsupported type.
+ * Mirrors ggml_type_size (src/gguf.rs:172-191), which panics instead. */
+size_t hip_type_size(uint32_t ggml_type, size_t n_elems);
+
+/* Memory.  Replace cuda_alloc / cuda_drop / cuda_h2d / cuda_d2h / cuda_sync /
+ * cuda_mem_info (src/cuda_kernels.cu:1042-1044, 1109-1125).  hip_alloc returns
+ * NULL on failure (256-byte aligned otherwise); h2d/d2h are blocking. */
+void* hip_alloc(size_t bytes);
+void hip_drop(void* ptr);
+int hip_h2d(void* dst, const void* src, size_t bytes);
+int hip_d2h(void* dst, const void* src, size_t bytes);
+int hip_sync(void);
+int hip_mem_info(size_t* free_b, size_t* total_b);
+
+/* IQ codebooks.  Replace cuda_set_iq3s_grid / _iq2s_grid / _iq2xxs_grid /
+ * _iq2xs_grid / cuda_set_ksigns (src/cuda_kernels.cu:1027-1041).  The library is
+ * built with ggml's codebooks already resident, so calling these is optional;
+ * they overwrite the device tables (idempotent for the standard tables).
+ * ksigns is a closed form (i | parity(i) << 7) in this library: hip_set_ksigns
+ * only checks that the table it is given is that one (QH_ERR_RANGE if not). */
+int hip_set_iq3s_grid(const uint32_t* host);
+int hip_set_iq2s_grid(const uint64_t* host);
+int hip_set_iq2xxs_grid(const uint64_t* host);
+int hip_set_iq2xs_grid(const uint64_t* host);
+int hip_set_ksigns(const uint8_t* host);
+
+/* Diagnostics. */
+const char* hip_status_string(int status);
+const char* hip_last_error(void); /* last HIP error seen on this host thread ("" if none) */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QUARTZ_HIP_H */

@@ -1,0 +1,185 @@
+// qh_api.hip -- the C ABI declared in include/quartz_hip.h.
+//
+// Argument checking, dispatch and status codes.  Reference: the `extern "C"`
+// block of src/cuda_kernels.cu:1025-1125.  Unlike the reference (void returns,
+// no error checks), every HIP call is checked and turned into a status code.
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/quartz_hip.h"
+#include "qh_internal.h"
+
+extern __device__ uint64_t qh_g_iq2xxs[256];
+extern __device__ uint64_t qh_g_iq2xs[512];
+extern __device__ uint64_t qh_g_iq2s[1024];
+extern __device__ uint32_t qh_g_iq3s[512];
+
+static thread_local char qh_errbuf[256];
+
+static int qh_fail(hipError_t e, const char* what) {
+    snprintf(qh_errbuf, sizeof qh_errbuf, "%s: %s", what, hipGetErrorString(e));
+    return QH_ERR_HIP;
+}
+#define QH_CHECK(call, what)                         \
+    do {                                             \
+        hipError_t qh_e_ = (call);                   \
+        if (qh_e_ != hipSuccess) return qh_fail(qh_e_, what); \
+    } while (0)
+
+static int qh_check_dims(uint32_t type, int in_dim, int out_dim) {
+    const int qk = qh_block_elems(type);
+    if (qk == 0) return QH_ERR_TYPE;
+    if (in_dim <= 0 || out_dim < 0 || in_dim % qk) return QH_ERR_DIMS;
+    return QH_OK;
+}
+
+// Unknown type: zero y and say so, as cuda_gemv does (src/cuda_kernels.cu:1070-1074).
+static int qh_unknown_type(const char* fn, uint32_t type, float* y, size_t n, hipStream_t st) {
+    fprintf(stderr, "%s: unsupported ggml_type %u\n", fn, type);
+    if (y && n) {
+        hipError_t e = hipMemsetAsync(y, 0, n * sizeof(float), st);
+        if (e != hipSuccess) qh_fail(e, fn);
+    }
+    return QH_ERR_TYPE;
+}
+
+extern "C" {
+
+const char* hip_status_string(int s) {
+    switch (s) {
+        case QH_OK: return "ok";
+        case QH_ERR_TYPE: return "unsupported ggml_type";
+        case QH_ERR_DIMS: return "bad dimensions (in_dim must be a positive multiple of the block size)";
+        case QH_ERR_NULL: return "null device pointer";
+        case QH_ERR_HIP: return "HIP runtime error";
+        case QH_ERR_RANGE: return "argument out of range";
+        default: return "unknown status";
+    }
+}
+
+const char* hip_last_error(void) { return qh_errbuf; }
+
+size_t hip_type_size(uint32_t type, size_t n) { return qh_type_size(type, n); }
+
+int hip_gemv_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                   void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    int rc = qh_check_dims(type, in_dim, out_dim);
+    if (rc == QH_ERR_TYPE) return qh_unknown_type("hip_gemv", type, out_dim > 0 ? y : nullptr, (size_t)(out_dim > 0 ? out_dim : 0), st);
+    if (rc) return rc;
+    if (out_dim == 0) return QH_OK;
+    if (!W || !x || !y) return QH_ERR_NULL;
+    QH_CHECK(qh_launch_gemv(type, W, x, y, in_dim, out_dim, st), "hip_gemv");
+    return QH_OK;
+}
+
+int hip_gemv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim) {
+    return hip_gemv_async(type, W, x, y, in_dim, out_dim, nullptr);
+}
+
+int hip_gemm_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
+                   void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    int rc = qh_check_dims(type, in_dim, out_dim);
+    if (rc == QH_ERR_TYPE) {
+        const size_t cnt = (out_dim > 0 && n > 0) ? (size_t)out_dim * (size_t)n : 0;
+        return qh_unknown_type("hip_gemm", type, cnt ? y : nullptr, cnt, st);
+    }
+    if (rc) return rc;
+    if (n < 0) return QH_ERR_DIMS;
+    if (out_dim == 0 || n == 0) return QH_OK;
+    if (!W || !x || !y) return QH_ERR_NULL;
+    QH_CHECK(qh_launch_gemm(type, W, x, y, in_dim, out_dim, n, st), "hip_gemm");
+    return QH_OK;
+}
+
+int hip_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n) {
+    return hip_gemm_async(type, W, x, y, in_dim, out_dim, n, nullptr);
+}
+
+int hip_gemv_moe4(uint32_t type, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2, const uint8_t* w3,
+                  const float* xi0, const float* xi1, const float* xi2, const float* xi3, float* o0, float* o1,
+                  float* o2, float* o3, int n_act, int in_dim, int out_dim) {
+    if (n_act < 0 || n_act > 4) return QH_ERR_RANGE;
+    const uint8_t* ws[4] = {w0, w1, w2, w3};
+    const float* xs[4] = {xi0, xi1, xi2, xi3};
+    float* os[4] = {o0, o1, o2, o3};
+    for (int e = 0; e < n_act; e++) {
+        int rc = hip_gemv_async(type, ws[e], xs[e], os[e], in_dim, out_dim, nullptr);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
+int hip_dequant_async(uint32_t type, const uint8_t* W, float* out, size_t n, void* stream) {
+    const int qk = qh_block_elems(type);
+    if (qk == 0) return QH_ERR_TYPE;
+    if (n % (size_t)qk) return QH_ERR_DIMS;
+    if (n == 0) return QH_OK;
+    if (!W || !out) return QH_ERR_NULL;
+    QH_CHECK(qh_launch_dequant(type, W, out, n, (hipStream_t)stream), "hip_dequant");
+    return QH_OK;
+}
+
+int hip_dequant(uint32_t type, const uint8_t* W, float* out, size_t n) {
+    return hip_dequant_async(type, W, out, n, nullptr);
+}
+
+void* hip_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    return p;
+}
+
+void hip_drop(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+int hip_h2d(void* dst, const void* src, size_t bytes) {
+    QH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hip_h2d");
+    return QH_OK;
+}
+
+int hip_d2h(void* dst, const void* src, size_t bytes) {
+    QH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hip_d2h");
+    return QH_OK;
+}
+
+int hip_sync(void) {
+    QH_CHECK(hipDeviceSynchronize(), "hip_sync");
+    return QH_OK;
+}
+
+int hip_mem_info(size_t* free_b, size_t* total_b) {
+    QH_CHECK(hipMemGetInfo(free_b, total_b), "hip_mem_info");
+    return QH_OK;
+}
+
+int hip_set_iq3s_grid(const uint32_t* host) {
+    if (!host) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(qh_g_iq3s), host, sizeof(qh_g_iq3s)), "hip_set_iq3s_grid");
+    return QH_OK;
+}
+int hip_set_iq2s_grid(const uint64_t* host) {
+    if (!host) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(qh_g_iq2s), host, sizeof(qh_g_iq2s)), "hip_set_iq2s_grid");
+    return QH_OK;
+}
+int hip_set_iq2xxs_grid(const uint64_t* host) {
+    if (!host) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(qh_g_iq2xxs), host, sizeof(qh_g_iq2xxs)), "hip_set_iq2xxs_grid");
+    return QH_OK;
+}
+int hip_set_iq2xs_grid(const uint64_t* host) {
+    if (!host) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(qh_g_iq2xs), host, sizeof(qh_g_iq2xs)), "hip_set_iq2xs_grid");
+    return QH_OK;
+}
+int hip_set_ksigns(const uint8_t* host) {
+    if (!host) return QH_ERR_NULL;
+    for (uint32_t i = 0; i < 128; i++)
+        if (host[i] != (uint8_t)(i | ((uint32_t)__builtin_parity(i) << 7))) return QH_ERR_RANGE;
+    return QH_OK;
+}
+
+}  // extern "C"

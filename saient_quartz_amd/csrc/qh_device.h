@@ -1,0 +1,140 @@
+// qh_device.h -- device-side helpers shared by every gfx950 kernel in this library.
+//
+// Conventions:
+//  * All weight bytes are read through a raw buffer resource (V#) whose record
+//    count is the byte size of the weight tensor.  Loads are 4-byte aligned
+//    buffer_load_dword{,x2,x4}; an out-of-range load returns 0 instead of
+//    faulting, so a window load that runs a few bytes past the end of a tensor
+//    is harmless.  Byte fields that sit at 2-byte alignment (GGUF blocks of 210,
+//    110, 66, 74, 82, 34, 22 or 18 bytes) are loaded as aligned dwords and
+//    re-aligned in registers with v_alignbyte_b32.
+//  * Wavefronts are 64 lanes; reductions use DPP row ops plus row_bcast.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QH_DEV __device__ __forceinline__
+
+typedef uint32_t qh_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t qh_u32x2 __attribute__((ext_vector_type(2)));
+
+// GGML type ids (src/gguf.rs:172-191; 2/3 from the public GGUF layout).
+enum : uint32_t {
+    QT_F32 = 0, QT_F16 = 1, QT_Q4_0 = 2, QT_Q4_1 = 3, QT_Q5_0 = 6, QT_Q5_1 = 7, QT_Q8_0 = 8,
+    QT_Q2_K = 10, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ2_XXS = 16, QT_IQ2_XS = 17,
+    QT_IQ4_NL = 20, QT_IQ3_S = 21, QT_IQ2_S = 22, QT_BF16 = 30,
+};
+
+// ---------------------------------------------------------------- buffer loads
+
+struct QhBuf {
+    __amdgpu_buffer_rsrc_t rs;
+};
+
+// dword3 of a raw (untyped, stride 0) gfx9 buffer descriptor: 32-bit data format.
+#define QH_RSRC_DW3 0x00020000
+
+QH_DEV QhBuf qh_buf(const void* base, uint32_t nbytes) {
+    QhBuf b;
+    b.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, QH_RSRC_DW3);
+    return b;
+}
+QH_DEV uint32_t qh_ld32(QhBuf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(b.rs, (int)off, 0, 0);
+}
+QH_DEV qh_u32x2 qh_ld64(QhBuf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(b.rs, (int)off, 0, 0);
+}
+QH_DEV qh_u32x4 qh_ld128(QhBuf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(b.rs, (int)off, 0, 0);
+}
+
+// Load N dwords starting at a 4-byte aligned offset.
+template <int N>
+QH_DEV void qh_ldn(QhBuf b, uint32_t off, uint32_t* r) {
+    int i = 0;
+#pragma unroll
+    for (; i + 4 <= N; i += 4) {
+        qh_u32x4 v = qh_ld128(b, off + 4 * i);
+        r[i] = v.x; r[i + 1] = v.y; r[i + 2] = v.z; r[i + 3] = v.w;
+    }
+    if constexpr (N % 4 >= 2) {
+        qh_u32x2 v = qh_ld64(b, off + 4 * i);
+        r[i] = v.x; r[i + 1] = v.y;
+        i += 2;
+    }
+    if constexpr (N % 2 == 1) r[i] = qh_ld32(b, off + 4 * i);
+}
+
+// Window of N dwords starting at a 2-byte aligned offset: loads N+1 aligned
+// dwords into raw[]; qh_fix() then shifts them into place.
+template <int N>
+QH_DEV void qh_ldwin(QhBuf b, uint32_t off, uint32_t* raw) {
+    qh_ldn<N + 1>(b, off & ~3u, raw);
+}
+template <int N>
+QH_DEV void qh_fix(const uint32_t* raw, uint32_t off, uint32_t* out) {
+    const uint32_t sh = off & 3u;
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+}
+
+// ---------------------------------------------------------------- scalars
+
+QH_DEV float qh_bits(uint32_t b) { return __uint_as_float(b); }
+
+// IEEE binary16 -> f32, bit-identical to src/dequant.rs:1329-1349 for every
+// pattern (subnormals exact, Inf/NaN keep their payload, no NaN quieting).
+QH_DEV float qh_f16(uint32_t h) {
+    h &= 0xFFFFu;
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t em = h & 0x7FFFu;
+    const uint32_t normal = (em << 13) + 0x38000000u;                       // rebias 15 -> 127
+    const uint32_t infnan = 0x7F800000u | ((em & 0x3FFu) << 13);
+    const uint32_t sub = __float_as_uint((float)em * 0x1p-24f);            // exact: em < 2^10
+    uint32_t r = em >= 0x7C00u ? infnan : (em >= 0x400u ? normal : sub);
+    return qh_bits(sign | r);
+}
+QH_DEV float qh_f16_lo(uint32_t w) { return qh_f16(w & 0xFFFFu); }
+QH_DEV float qh_f16_hi(uint32_t w) { return qh_f16(w >> 16); }
+
+// Unsigned byte k of w as float (v_cvt_f32_ubyte{0..3}).
+QH_DEV float qh_ub0(uint32_t w) { return (float)(w & 0xFFu); }
+QH_DEV float qh_ub1(uint32_t w) { return (float)((w >> 8) & 0xFFu); }
+QH_DEV float qh_ub2(uint32_t w) { return (float)((w >> 16) & 0xFFu); }
+QH_DEV float qh_ub3(uint32_t w) { return (float)(w >> 24); }
+
+// s += x[0..3] . bytes(w)
+QH_DEV float qh_dot4u(const float* xv, uint32_t w, float s) {
+    s = fmaf(xv[0], qh_ub0(w), s);
+    s = fmaf(xv[1], qh_ub1(w), s);
+    s = fmaf(xv[2], qh_ub2(w), s);
+    s = fmaf(xv[3], qh_ub3(w), s);
+    return s;
+}
+
+// Spread the low 4 bits of t (t < 16) to bit 0 of each byte.
+QH_DEV uint32_t qh_spread4(uint32_t t) { return (t * 0x00204081u) & 0x01010101u; }
+
+// Byte-wise conditional negation: bytes whose mask byte is 0xFF are negated
+// (g must have no zero bytes where negated, true for every IQ codebook entry).
+QH_DEV uint32_t qh_negbytes(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+
+// ksigns_iq2xs[i] = i | parity(i) << 7  (the closed form of KSIGNS_IQ2XS).
+QH_DEV uint32_t qh_ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
+
+// 0xFF in byte j of the result for every set bit j (j < 4) of s.
+QH_DEV uint32_t qh_signmask4(uint32_t s4) { return qh_spread4(s4 & 0xFu) * 0xFFu; }
+
+// ---------------------------------------------------------------- reductions
+
+// Full 64-lane sum; the result is valid in lane 63.
+QH_DEV float qh_wave_sum63(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false)); // row_bcast15
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false)); // row_bcast31
+    return v;
+}

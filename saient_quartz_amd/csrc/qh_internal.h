@@ -1,0 +1,49 @@
+// qh_internal.h -- declarations shared by the translation units of libquartz_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+// Block geometry, src/gguf.rs:172-191 (Q4_0/Q4_1 from the GGUF layout).
+__host__ __device__ inline int qh_block_elems(uint32_t t) {
+    switch (t) {
+        case 0: case 1: case 30: return 1;
+        case 2: case 3: case 6: case 7: case 8: case 20: return 32;
+        case 10: case 12: case 13: case 14: case 16: case 17: case 21: case 22: return 256;
+        default: return 0;
+    }
+}
+__host__ __device__ inline uint32_t qh_block_bytes(uint32_t t) {
+    switch (t) {
+        case 0: return 4;
+        case 1: case 30: return 2;
+        case 2: return 18;
+        case 3: return 20;
+        case 6: return 22;
+        case 7: return 24;
+        case 8: return 34;
+        case 10: return 84;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        case 16: return 66;
+        case 17: return 74;
+        case 20: return 18;
+        case 21: return 110;
+        case 22: return 82;
+        default: return 0;
+    }
+}
+__host__ __device__ inline size_t qh_type_size(uint32_t t, size_t n) {
+    const int qk = qh_block_elems(t);
+    return qk ? (n / (size_t)qk) * qh_block_bytes(t) : 0;
+}
+
+// Bit-exact decode of one block (qk elements) -- qh_dequant.hip.
+__device__ void qh_decode_block(uint32_t type, const uint8_t* blk, float* out);
+
+hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                          hipStream_t st);
+hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                          int n, hipStream_t st);
+hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

@@ -1,0 +1,7 @@
+// qh_lib.hip -- the single translation unit of libquartz_hip.so.
+// The IQ codebooks are device globals shared by the decode and GEMV kernels;
+// compiling everything as one unit keeps them visible without relocatable
+// device code.
+#include "qh_dequant.hip"
+#include "qh_gemv.hip"
+#include "qh_api.hip"

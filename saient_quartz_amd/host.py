@@ -1,0 +1,107 @@
+"""Host-side wrappers over the C ABI, mirroring Quartz's Rust FFI wrapper
+(src/cuda.rs:59-150, 250-281): GpuBuf (RAII device buffer), GpuScratch (reusable
+x/y buffers + gemv), gpu_expert_slice, ensure_iq_grids and verify_gemv_hip.
+Same names and argument meaning; failures raise instead of panicking.
+"""
+import ctypes as C
+
+import numpy as np
+
+from .api import check, lib, type_size
+
+
+class GpuBuf:
+    """Owned device buffer (src/cuda.rs:59-90).  Freed with hip_drop."""
+
+    def __init__(self, ptr: int, nbytes: int):
+        self.ptr = ptr
+        self.bytes = nbytes
+
+    @classmethod
+    def alloc(cls, nbytes: int) -> "GpuBuf":
+        p = lib().hip_alloc(max(nbytes, 1))
+        if not p:
+            raise MemoryError(f"hipMalloc failed for {nbytes} bytes")
+        return cls(p, nbytes)
+
+    @classmethod
+    def upload(cls, data: np.ndarray) -> "GpuBuf":
+        data = np.ascontiguousarray(data)
+        b = cls.alloc(data.nbytes)
+        check("hip_h2d", lib().hip_h2d(b.ptr, data.ctypes.data, data.nbytes))
+        return b
+
+    @classmethod
+    def alloc_f32(cls, n: int) -> "GpuBuf":
+        return cls.alloc(4 * n)
+
+    @classmethod
+    def upload_f32(cls, data) -> "GpuBuf":
+        return cls.upload(np.asarray(data, dtype=np.float32))
+
+    def download(self, dtype=np.uint8, count=None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.bytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        check("hip_d2h", lib().hip_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def drop(self):
+        if self.ptr:
+            lib().hip_drop(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.drop()
+        except Exception:
+            pass
+
+
+class GpuSlice:
+    """View into an uploaded stacked-expert tensor (src/cuda.rs:244-258)."""
+
+    def __init__(self, ptr: int, ggml_type: int):
+        self.ptr = ptr
+        self.ggml_type = ggml_type
+
+
+def gpu_expert_slice(buf: GpuBuf, ggml_type: int, expert: int, n_elems_per_expert: int) -> GpuSlice:
+    return GpuSlice(buf.ptr + expert * type_size(ggml_type, n_elems_per_expert), ggml_type)
+
+
+class GpuScratch:
+    """Reusable x / y device buffers (src/cuda.rs:94-128, 261-281)."""
+
+    def __init__(self, max_in: int, max_out: int):
+        self.d_x = GpuBuf.alloc_f32(max_in)
+        self.d_y = GpuBuf.alloc_f32(max_out)
+
+    def _run(self, x, ptr, ggml_type, in_dim, out_dim):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        L = lib()
+        check("hip_h2d", L.hip_h2d(self.d_x.ptr, x.ctypes.data, x.nbytes))
+        check("hip_gemv", L.hip_gemv(ggml_type, ptr, self.d_x.ptr, self.d_y.ptr, in_dim, out_dim))
+        out = np.empty(out_dim, dtype=np.float32)
+        check("hip_d2h", L.hip_d2h(out.ctypes.data, self.d_y.ptr, out.nbytes))
+        check("hip_sync", L.hip_sync())
+        return out
+
+    def gemv(self, x, data: GpuBuf, ggml_type: int, in_dim: int, out_dim: int) -> np.ndarray:
+        return self._run(x, data.ptr, ggml_type, in_dim, out_dim)
+
+    def gemv_slice(self, x, sl: GpuSlice, in_dim: int, out_dim: int) -> np.ndarray:
+        return self._run(x, sl.ptr, sl.ggml_type, in_dim, out_dim)
+
+
+def ensure_iq_grids():
+    """src/cuda.rs:131-140.  The codebooks are resident from load time; nothing to do."""
+    return None
+
+
+def verify_gemv_hip(x, data: np.ndarray, ggml_type: int, in_dim: int, out_dim: int) -> np.ndarray:
+    """src/cuda.rs:144-150: upload the raw tensor fresh, run one GEMV, return y."""
+    ensure_iq_grids()
+    buf = GpuBuf.upload(data)
+    sc = GpuScratch(in_dim, out_dim)
+    return sc.gemv(x, buf, ggml_type, in_dim, out_dim)

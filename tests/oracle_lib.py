@@ -1,0 +1,78 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).  Test infrastructure."""
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+SO = ROOT / "oracle" / "liboracle.so"
+
+
+class Oracle:
+    _inst = None
+
+    @classmethod
+    def load(cls):
+        if cls._inst is None:
+            if not SO.exists():
+                subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+            cls._inst = cls(C.CDLL(str(SO)))
+        return cls._inst
+
+    def __init__(self, L):
+        self.L = L
+        L.o_f16_to_f32.restype = C.c_float
+        L.o_f16_to_f32.argtypes = [C.c_uint16]
+        L.o_type_size.restype = C.c_size_t
+        L.o_type_size.argtypes = [C.c_uint32, C.c_size_t]
+        L.o_block_elems.restype = C.c_int
+        L.o_block_elems.argtypes = [C.c_uint32]
+        L.o_dequant.restype = C.c_int
+        L.o_dequant.argtypes = [C.c_uint32, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.o_gemv.restype = C.c_int
+        L.o_gemv.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+        L.o_gemm.restype = C.c_int
+        L.o_gemm.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
+        L.o_set_threads.argtypes = [C.c_int]
+        L.o_get_threads.restype = C.c_int
+        L.o_grid_sha256.restype = C.c_char_p
+        L.o_grid_sha256.argtypes = [C.c_int]
+
+    def f16(self, bits: int) -> float:
+        return self.L.o_f16_to_f32(bits)
+
+    def type_size(self, t, n):
+        return self.L.o_type_size(t, n)
+
+    def dequant(self, t, data: np.ndarray, n: int) -> np.ndarray:
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.empty(n, dtype=np.float32)
+        rc = self.L.o_dequant(t, data.ctypes.data, n, out.ctypes.data)
+        if rc:
+            raise ValueError(f"o_dequant rc={rc}")
+        return out
+
+    def gemv(self, t, x: np.ndarray, data: np.ndarray, in_dim: int, out_dim: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        y = np.empty(out_dim, dtype=np.float32)
+        rc = self.L.o_gemv(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, y.ctypes.data)
+        if rc:
+            raise ValueError(f"o_gemv rc={rc}")
+        return y
+
+    def gemm(self, t, x: np.ndarray, data: np.ndarray, in_dim: int, out_dim: int, n: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        y = np.empty((n, out_dim), dtype=np.float32)
+        rc = self.L.o_gemm(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, n, y.ctypes.data)
+        if rc:
+            raise ValueError(f"o_gemm rc={rc}")
+        return y
+
+    def set_threads(self, n):
+        self.L.o_set_threads(n)
+
+    def threads(self):
+        return self.L.o_get_threads()

@@ -1,0 +1,159 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle.
+
+Bars: dequant bit-exact; GEMV/GEMM within 1e-3 relative L2 of the oracle
+(f32 accumulate; observed ~1e-6); --verify-gemv criterion
+max|cpu-gpu| / max|cpu| < 1e-3 (src/main.rs:2653-2662).
+"""
+import numpy as np
+import pytest
+
+import closed_form as cf
+from saient_quartz_amd import GGML_TYPES, synth
+from saient_quartz_amd.host import GpuBuf, GpuScratch, gpu_expert_slice, verify_gemv_hip
+from saient_quartz_amd.api import check
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+ALL_TYPES = sorted(GGML_TYPES)
+
+
+def gpu_gemv(qh, t, x, data, in_dim, out_dim):
+    return verify_gemv_hip(x, data, t, in_dim, out_dim)
+
+
+def gpu_gemm(qh, t, x, data, in_dim, out_dim, n):
+    w = GpuBuf.upload(data)
+    dx = GpuBuf.upload_f32(x.reshape(-1))
+    dy = GpuBuf.alloc_f32(n * out_dim)
+    check("hip_gemm", qh.hip_gemm(t, w.ptr, dx.ptr, dy.ptr, in_dim, out_dim, n))
+    return dy.download(np.float32).reshape(n, out_dim)
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_dequant_bit_exact(qh, oracle, t):
+    _, qk, _ = GGML_TYPES[t]
+    out_dim, in_dim = 37, 1024
+    data = synth.weights(t, out_dim, in_dim, seed=100 + t)
+    n = out_dim * in_dim
+    w = GpuBuf.upload(data)
+    out = GpuBuf.alloc_f32(n)
+    check("hip_dequant", qh.hip_dequant(t, w.ptr, out.ptr, n))
+    got = out.download(np.float32)
+    ref = oracle.dequant(t, data, n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_f16_all_patterns(qh, oracle):
+    bits = np.arange(65536, dtype=np.uint16).view(np.uint8)
+    w = GpuBuf.upload(bits)
+    out = GpuBuf.alloc_f32(65536)
+    check("hip_dequant", qh.hip_dequant(1, w.ptr, out.ptr, 65536))
+    assert np.array_equal(out.download(np.uint32), oracle.dequant(1, bits, 65536).view(np.uint32))
+
+
+SHAPES = [(64, 4096), (37, 4096), (5, 256), (130, 512), (19, 14336), (3, 8192), (2, 12288), (1, 28672)]
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_vs_oracle(qh, oracle, t, shape):
+    out_dim, in_dim = shape
+    data = synth.weights(t, out_dim, in_dim, seed=7 * t + in_dim)
+    x = synth.activations(1, in_dim, seed=11 + in_dim)[0]
+    got = gpu_gemv(qh, t, x, data, in_dim, out_dim)
+    ref = oracle.gemv(t, x, data, in_dim, out_dim)
+    bad = np.nonzero(~np.isclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max()))[0]
+    assert cf.rel_l2(got, ref) < TOL, (t, shape, cf.rel_l2(got, ref), bad[:16])
+
+
+@pytest.mark.parametrize("t", [2, 3, 6, 7, 8, 20, 0, 1, 30])
+@pytest.mark.parametrize("in_dim", [32, 96, 4064])
+def test_gemv_fallback_shapes(qh, oracle, t, in_dim):
+    """in_dim % 64 != 0 takes the generic kernel (32-element formats, floats)."""
+    out_dim = 9
+    data = synth.weights(t, out_dim, in_dim, seed=5 + in_dim)
+    x = synth.activations(1, in_dim, seed=6)[0]
+    got = gpu_gemv(qh, t, x, data, in_dim, out_dim)
+    assert cf.rel_l2(got, oracle.gemv(t, x, data, in_dim, out_dim)) < TOL
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_verify_gemv_criterion(qh, oracle, t):
+    """Quartz's --verify-gemv check with its deterministic x (src/main.rs:2640-2662)."""
+    out_dim, in_dim = 96, 4096
+    data = synth.weights(t, out_dim, in_dim, seed=300 + t)
+    x = synth.verify_x(in_dim)
+    cpu = oracle.gemv(t, x, data, in_dim, out_dim)
+    gpu = gpu_gemv(qh, t, x, data, in_dim, out_dim)
+    maxdiff = float(np.max(np.abs(cpu - gpu)))
+    maxmag = max(float(np.max(np.abs(cpu))), 1e-6)
+    assert maxdiff / maxmag < 1e-3
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("n", [2, 4, 16])
+def test_gemm_vs_oracle(qh, oracle, t, n):
+    out_dim, in_dim = 40, 4096 if GGML_TYPES[t][1] > 1 else 1024
+    data = synth.weights(t, out_dim, in_dim, seed=900 + t)
+    x = synth.activations(n, in_dim, seed=901 + n)
+    got = gpu_gemm(qh, t, x, data, in_dim, out_dim, n)
+    ref = oracle.gemm(t, x, data, in_dim, out_dim, n)
+    assert cf.rel_l2(got, ref) < TOL
+
+
+def test_expert_slices_and_moe4(qh, oracle):
+    """Stacked experts addressed as base + e * type_size (src/cuda.rs:250-258)."""
+    t, in_dim, out_dim, n_exp = 21, 1024, 64, 4
+    per = out_dim * in_dim
+    data = np.concatenate([synth.weights(t, out_dim, in_dim, seed=40 + e) for e in range(n_exp)])
+    buf = GpuBuf.upload(data)
+    xs = synth.activations(n_exp, in_dim, seed=41)
+    sc = GpuScratch(in_dim, out_dim)
+    nbytes = per * GGML_TYPES[t][2] // GGML_TYPES[t][1]
+    for e in range(n_exp):
+        sl = gpu_expert_slice(buf, t, e, per)
+        got = sc.gemv_slice(xs[e], sl, in_dim, out_dim)
+        ref = oracle.gemv(t, xs[e], data[e * nbytes:(e + 1) * nbytes], in_dim, out_dim)
+        assert cf.rel_l2(got, ref) < TOL
+    dx = [GpuBuf.upload_f32(xs[e]) for e in range(n_exp)]
+    dy = [GpuBuf.alloc_f32(out_dim) for _ in range(n_exp)]
+    ws = [gpu_expert_slice(buf, t, e, per).ptr for e in range(n_exp)]
+    check("hip_gemv_moe4", qh.hip_gemv_moe4(t, *ws, *[b.ptr for b in dx], *[b.ptr for b in dy], 3, in_dim, out_dim))
+    check("hip_sync", qh.hip_sync())
+    for e in range(3):
+        ref = oracle.gemv(t, xs[e], data[e * nbytes:(e + 1) * nbytes], in_dim, out_dim)
+        assert cf.rel_l2(dy[e].download(np.float32), ref) < TOL
+
+
+def test_unknown_type_zero_fills(qh):
+    y = GpuBuf.upload_f32(np.full(16, 7.0, np.float32))
+    w = GpuBuf.alloc(64)
+    x = GpuBuf.alloc_f32(256)
+    assert qh.hip_gemv(5, w.ptr, x.ptr, y.ptr, 256, 16) == -1
+    check("hip_sync", qh.hip_sync())
+    assert np.all(y.download(np.float32) == 0.0)
+
+
+def test_iq_grid_upload_roundtrip(qh, oracle):
+    """hip_set_*_grid with the standard tables leaves results unchanged."""
+    # keep every host table referenced while the library copies it
+    t2xxs = np.ascontiguousarray(cf.GRIDS["IQ2XXS"][0], dtype=np.uint64)
+    t2xs = np.ascontiguousarray(cf.GRIDS["IQ2XS"][0], dtype=np.uint64)
+    t2s = np.ascontiguousarray(cf.GRIDS["IQ2S"][0], dtype=np.uint64)
+    t3s = np.ascontiguousarray(cf.GRIDS["IQ3S"][0], dtype=np.uint32)
+    check("set", qh.hip_set_iq2xxs_grid(t2xxs.ctypes.data))
+    check("set", qh.hip_set_iq2xs_grid(t2xs.ctypes.data))
+    check("set", qh.hip_set_iq2s_grid(t2s.ctypes.data))
+    check("set", qh.hip_set_iq3s_grid(t3s.ctypes.data))
+    for t in (16, 17, 21, 22):
+        data = synth.weights(t, 8, 512, seed=t)
+        x = synth.activations(1, 512, seed=1)[0]
+        assert cf.rel_l2(gpu_gemv(qh, t, x, data, 512, 8), oracle.gemv(t, x, data, 512, 8)) < TOL
+
+
+def test_mem_info(qh):
+    import ctypes as C
+    f, tot = C.c_size_t(), C.c_size_t()
+    check("hip_mem_info", qh.hip_mem_info(C.byref(f), C.byref(tot)))
+    assert 0 < f.value <= tot.value
