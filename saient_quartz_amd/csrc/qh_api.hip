@@ -4,6 +4,7 @@
 // block of src/cuda_kernels.cu:1025-1125.  Unlike the reference (void returns,
 // no error checks), every HIP call is checked and turned into a status code.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/quartz_hip.h"
@@ -15,6 +16,14 @@ extern __device__ uint64_t qh_g_iq2s[1024];
 extern __device__ uint32_t qh_g_iq3s[512];
 
 static thread_local char qh_errbuf[256];
+
+bool qh_force_valu() {
+    static const bool v = [] {
+        const char* e = getenv("QUARTZ_HIP_KERNEL");
+        return e && strcmp(e, "valu") == 0;
+    }();
+    return v;
+}
 
 static int qh_fail(hipError_t e, const char* what) {
     snprintf(qh_errbuf, sizeof qh_errbuf, "%s: %s", what, hipGetErrorString(e));

@@ -95,8 +95,12 @@ QH_DEV float qh_f16(uint32_t h) {
     uint32_t r = em >= 0x7C00u ? infnan : (em >= 0x400u ? normal : sub);
     return qh_bits(sign | r);
 }
-QH_DEV float qh_f16_lo(uint32_t w) { return qh_f16(w & 0xFFFFu); }
-QH_DEV float qh_f16_hi(uint32_t w) { return qh_f16(w >> 16); }
+// Hardware binary16 -> f32 (v_cvt_f32_f16): exact for every finite value
+// (subnormals included); NaN payloads may be quieted.  Used for the scales in the
+// GEMV kernels; the bit-exact qh_f16 is used where decoded values are returned.
+QH_DEV float qh_h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+QH_DEV float qh_f16_lo(uint32_t w) { return qh_h2f(w & 0xFFFFu); }
+QH_DEV float qh_f16_hi(uint32_t w) { return qh_h2f(w >> 16); }
 
 // Unsigned byte k of w as float (v_cvt_f32_ubyte{0..3}).
 QH_DEV float qh_ub0(uint32_t w) { return (float)(w & 0xFFu); }

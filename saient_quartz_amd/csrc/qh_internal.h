@@ -42,6 +42,11 @@ __host__ __device__ inline size_t qh_type_size(uint32_t t, size_t n) {
 // Bit-exact decode of one block (qk elements) -- qh_dequant.hip.
 __device__ void qh_decode_block(uint32_t type, const uint8_t* blk, float* out);
 
+hipError_t qh_launch_mmv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                         hipStream_t st);
+// QUARTZ_HIP_KERNEL=valu selects the lane-per-unit VALU kernels instead of the
+// matrix-core ones (for A/B measurement); read once per process.
+bool qh_force_valu();
 hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                           hipStream_t st);
 hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,

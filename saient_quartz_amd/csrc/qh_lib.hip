@@ -3,5 +3,6 @@
 // compiling everything as one unit keeps them visible without relocatable
 // device code.
 #include "qh_dequant.hip"
+#include "qh_mmv.hip"
 #include "qh_gemv.hip"
 #include "qh_api.hip"
