@@ -3,7 +3,7 @@
     python -m saient_quartz_amd.build        # or build() from Python
 
 The library is one translation unit (csrc/qh_lib.hip).  Flags: -O3, gfx950 only,
-and packed-FP32 code generation disabled (-packed-fp32-ops).
+packed-FP32 code generation disabled (-packed-fp32-ops), MFMA results in VGPRs.
 """
 import os
 import shutil
@@ -23,6 +23,9 @@ HIPCC_FLAGS = [
     "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the GEMV kernels consume every result
+    # immediately, so accumulation registers only add copies.
+    "-mllvm", "--amdgpu-mfma-vgpr-form",
 ]
 
 

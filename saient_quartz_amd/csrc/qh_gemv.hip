@@ -129,7 +129,9 @@ static hipError_t launch_unit(const uint8_t* W, const float* x, float* y, int in
 hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                           hipStream_t st) {
     if (!qh_force_valu()) {
-        hipError_t e = qh_launch_mmv(type, W, x, y, in_dim, out_dim, st);
+        hipError_t e = qh_launch_mmv16(type, W, x, y, in_dim, out_dim, st);
+        if (e != hipErrorNotSupported) return e;
+        e = qh_launch_mmv(type, W, x, y, in_dim, out_dim, st);
         if (e != hipErrorNotSupported) return e;
     }
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);

@@ -4,5 +4,6 @@
 // device code.
 #include "qh_dequant.hip"
 #include "qh_mmv.hip"
+#include "qh_mmv16.hip"
 #include "qh_gemv.hip"
 #include "qh_api.hip"
