@@ -9,14 +9,15 @@
 //   2. x is turned into three balanced int8 digit planes in LDS (the exponent is
 //      per wavefront and chunk, so the int32 MFMA sums are exact);
 //   3. per group, the wavefront writes its slices into a private LDS tile (one
-//      RS-byte line per row, 16-byte aligned whatever the block alignment in
+//      QH_RS-byte line per row, 16-byte aligned whatever the block alignment in
 //      memory) and reads them back transposed: lane (n = lane % 16, kg = lane / 16)
-//      takes the 16 weights k = 16 kg .. 16 kg + 15 of each 64-weight slice p of
-//      row n as the B operand (column n).  The A operand holds digit m of those x
-//      values in row 4 kg + m only, so result row 4 kg + m, column n (which the
-//      MFMA returns in lane 16 kg + n, register m) is the digit-m dot of exactly
-//      that lane's 16-weight group: every lane then applies its own group's
-//      integer scale, with no shuffles.
+//      owns two 16-byte chunks of row n's quants and turns their low and high
+//      nibbles into the B operands (column n) of the group's four MFMAs.  Every
+//      B operand is 16 weights that share one scale ("piece" = 16 consecutive x
+//      positions).  The A operand of MFMA s holds, in row 4 kg + m only, digit m of
+//      the x piece that lane kg's B operand multiplies, so result row 4 kg + m,
+//      column n (returned in lane 16 kg + n, register m) is the digit-m dot of that
+//      lane's own piece: each lane applies its piece's integer scale, no shuffles.
 //   4. sums over lanes and wavefronts finish through DPP/LDS.
 //
 // Reference counterpart: the warp-per-row cuda_gemv kernels of
@@ -26,21 +27,32 @@
 
 typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
 
-#define QH_XU 256   // LDS bytes per 64-element x slice
-#define QH_XU_SUM 192  // 4 f32 sums of 16 elements
-#define QH_XU_ZERO 208 // 16 zero bytes: the A operand of lanes that carry no digits
+// x of one group in LDS: digit plane m of piece q at 256m + 16q, the f32 sum of
+// piece q at 768 + 4q, and 16 zero bytes (the A operand of lanes that carry no
+// digits) at 832.
+#define QH_XG 1024
+#define QH_XG_SUM 768
+#define QH_XG_ZERO 832
 #define QH_RS 240   // LDS line per row: 15 x 16 bytes, conflict-free b128 reads over 16 rows
+#define QH_MAXT 32  // row tiles per workgroup (their results wait in LDS until the end)
+
+QH_DEV uint32_t qh_lo4(uint32_t q) { return q & 0x0F0F0F0Fu; }
+QH_DEV uint32_t qh_hi4(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
 
 // ---------------------------------------------------------------- formats
 // Each format gives: BYTES (per superblock), CH (16-byte slices loaded per row and
-// superblock), ROWS, a header decoded once per group (hdr), the B operand of
-// slice p for this lane (bop), the lane's integer scale (scl) and the integer
-// weight of its f32 x-sum (mn), and the two f32 factors of the group result:
-//   y += d * 2^-s * sum(scl * digit dots) - dm * sum(mn * x16).
+// superblock; slice c starts at block byte 16c, the last at LAST <= BYTES - 16),
+// ROWS, a header decoded once per group (hdr), the four B operands of lane kg
+// (bops), and per MFMA s: the x piece of lane kg (piece), its integer scale (scl)
+// and the integer weight of the piece's f32 x-sum (mn).  Group result:
+//   y += d * 2^-s * sum(scl * digit dots) - dm * sum(mn * xsum).
 
 // Q4_K: d, dmin, scales[12], qs[128] (src/dequant.rs:1471-1519).  Weight = d*sc*q - dmin*m.
+// Lane kg owns qs chunks c = kg (MFMAs 0, 1 = low, high nibbles) and c = kg + 4
+// (MFMAs 2, 3).  qs chunk c holds sub-blocks 2(c/2) (low) and 2(c/2)+1 (high),
+// positions 16(c%2) .. +15.
 struct M16Q4K {
-    static constexpr int BYTES = 144, CH = 9, ROWS = 14;
+    static constexpr int BYTES = 144, CH = 9, ROWS = 14, LAST = 128;
     struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
@@ -53,77 +65,99 @@ struct M16Q4K {
         o.dm = qh_f16_hi(h.x);
         return o;
     }
-    // Slice p covers sub-blocks 2p (k < 32) and 2p+1: qs[32p + 16(kg&1) + e], nibble kg>>1.
-    template <int P>
-    static QH_DEV qh_i32x4 bop(const unsigned char* r, int kg, const H&) {
-        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 16 + 32 * P + 16 * (kg & 1));
-        const uint32_t sh = 4u * (uint32_t)(kg >> 1);
-        return qh_i32x4{(int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu),
-                        (int)((q.z >> sh) & 0x0F0F0F0Fu), (int)((q.w >> sh) & 0x0F0F0F0Fu)};
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+        const qh_u32x4 q0 = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * kg);
+        const qh_u32x4 q1 = *reinterpret_cast<const qh_u32x4*>(r + 80 + 16 * kg);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            B[0][i] = (int)qh_lo4(q0[i]);
+            B[1][i] = (int)qh_hi4(q0[i]);
+            B[2][i] = (int)qh_lo4(q1[i]);
+            B[3][i] = (int)qh_hi4(q1[i]);
+        }
     }
-    template <int P>
+    // sub-block j = 2(kg/2) + 4(S/2) + S%2, piece = 2j + kg%2.
+    template <int S>
+    static QH_DEV int piece(int kg) { return 4 * (kg >> 1) + 8 * (S >> 1) + 2 * (S & 1) + (kg & 1); }
+    template <int S>
     static QH_DEV int scl(const H& h, int kg) {
-        return (int)(((P < 2 ? h.sc0 : h.sc1) >> (16 * (P & 1) + 8 * (kg >> 1))) & 0xFFu);
+        return (int)(((S < 2 ? h.sc0 : h.sc1) >> (16 * (kg >> 1) + 8 * (S & 1))) & 0xFFu);
     }
-    template <int P>
+    template <int S>
     static QH_DEV int mn(const H& h, int kg) {
-        return (int)(((P < 2 ? h.mn0 : h.mn1) >> (16 * (P & 1) + 8 * (kg >> 1))) & 0xFFu);
+        return (int)(((S < 2 ? h.mn0 : h.mn1) >> (16 * (kg >> 1) + 8 * (S & 1))) & 0xFFu);
     }
 };
 
 // Q5_K: d, dmin, scales[12], qh[32], qs[128] (src/dequant.rs:1146-1182).
 // Weight of sub-block j, position l: d*sc*(nibble + 16*bit_j(qh[l])) - dmin*m.
+// Chunks as Q4_K (qs at byte 48); both of lane kg's chunks use qh[16(kg%2) ..].
 struct M16Q5K {
-    static constexpr int BYTES = 176, CH = 11, ROWS = 11;
+    static constexpr int BYTES = 176, CH = 11, ROWS = 11, LAST = 160;
     using H = M16Q4K::H;
     static QH_DEV H hdr(const unsigned char* r) { return M16Q4K::hdr(r); }
-    template <int P>
-    static QH_DEV qh_i32x4 bop(const unsigned char* r, int kg, const H&) {
-        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 48 + 32 * P + 16 * (kg & 1));
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+        const qh_u32x4 q0 = *reinterpret_cast<const qh_u32x4*>(r + 48 + 16 * kg);
+        const qh_u32x4 q1 = *reinterpret_cast<const qh_u32x4*>(r + 112 + 16 * kg);
         const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * (kg & 1));
-        const uint32_t sh = 4u * (uint32_t)(kg >> 1), j = 2u * P + (uint32_t)(kg >> 1);
-        return qh_i32x4{(int)(((q.x >> sh) & 0x0F0F0F0Fu) | (((u.x >> j) & 0x01010101u) << 4)),
-                        (int)(((q.y >> sh) & 0x0F0F0F0Fu) | (((u.y >> j) & 0x01010101u) << 4)),
-                        (int)(((q.z >> sh) & 0x0F0F0F0Fu) | (((u.z >> j) & 0x01010101u) << 4)),
-                        (int)(((q.w >> sh) & 0x0F0F0F0Fu) | (((u.w >> j) & 0x01010101u) << 4))};
+        const uint32_t j = 2u * (uint32_t)(kg >> 1);  // sub-block of chunk kg's low nibbles
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = u[i] >> j;
+            B[0][i] = (int)(qh_lo4(q0[i]) | ((v & 0x01010101u) << 4));
+            B[1][i] = (int)(qh_hi4(q0[i]) | ((v & 0x02020202u) << 3));
+            B[2][i] = (int)(qh_lo4(q1[i]) | ((v & 0x10101010u)));
+            B[3][i] = (int)(qh_hi4(q1[i]) | ((v & 0x20202020u) >> 1));
+        }
     }
-    template <int P>
-    static QH_DEV int scl(const H& h, int kg) { return M16Q4K::scl<P>(h, kg); }
-    template <int P>
-    static QH_DEV int mn(const H& h, int kg) { return M16Q4K::mn<P>(h, kg); }
+    template <int S>
+    static QH_DEV int piece(int kg) { return M16Q4K::piece<S>(kg); }
+    template <int S>
+    static QH_DEV int scl(const H& h, int kg) { return M16Q4K::scl<S>(h, kg); }
+    template <int S>
+    static QH_DEV int mn(const H& h, int kg) { return M16Q4K::mn<S>(h, kg); }
 };
 
 // Q6_K: ql[128], qh[64], scales[16] (int8), d (src/dequant.rs:1583-1620).
-// Slice p = (half n = p/2, nibble p%2): position k = 16kg + e has
-// q = nibble(ql[64n + 16kg + e]) | bits(qh[32n + 16(kg&1) + e] >> (4(p%2) + 2(kg>>1))) << 4,
-// scale index 4p + kg and weight d*sc*(q - 32): the -32 goes through the x sums.
+// Half n, ql[64n + l] low nibble = position 128n + l, high = 128n + 64 + l;
+// qh[32n + l'] bits 2i..2i+1 = bits 4-5 of position 128n + 32i + l'.
+// Lane kg owns ql chunks kg (half 0) and kg + 4 (half 1): MFMA s = (half s/2,
+// nibble s%2) covers piece 8(s/2) + 4(s%2) + kg, whose scale is byte kg of
+// scales word s.  Weight = d*sc*(q - 32): the -32 goes through the x sums.
 struct M16Q6K {
     static constexpr int BYTES = 210, CH = 14, ROWS = 16;
+    // The 14th slice is loaded from block bytes 194-209 (not 208-223), so no load
+    // leaves the block: the LDS line then holds bytes 0-207 at 0-207 and d at 222.
+    static constexpr int LAST = 194;
     struct H { qh_u32x4 s; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         H o;
         o.s = *reinterpret_cast<const qh_u32x4*>(r + 192);
-        o.d = qh_f16_lo(*reinterpret_cast<const uint32_t*>(r + 208));
+        o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 222));
         o.dm = 32.0f * o.d;
         return o;
     }
-    template <int P>
-    static QH_DEV qh_i32x4 bop(const unsigned char* r, int kg, const H&) {
-        const qh_u32x4 l = *reinterpret_cast<const qh_u32x4*>(r + 64 * (P >> 1) + 16 * kg);
-        const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 128 + 32 * (P >> 1) + 16 * (kg & 1));
-        constexpr uint32_t ls = 4u * (P & 1);
-        const uint32_t us = ls + 2u * (uint32_t)(kg >> 1);
-        return qh_i32x4{(int)(((l.x >> ls) & 0x0F0F0F0Fu) | (((u.x >> us) & 0x03030303u) << 4)),
-                        (int)(((l.y >> ls) & 0x0F0F0F0Fu) | (((u.y >> us) & 0x03030303u) << 4)),
-                        (int)(((l.z >> ls) & 0x0F0F0F0Fu) | (((u.z >> us) & 0x03030303u) << 4)),
-                        (int)(((l.w >> ls) & 0x0F0F0F0Fu) | (((u.w >> us) & 0x03030303u) << 4))};
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+        const qh_u32x4 l0 = *reinterpret_cast<const qh_u32x4*>(r + 16 * kg);
+        const qh_u32x4 l1 = *reinterpret_cast<const qh_u32x4*>(r + 64 + 16 * kg);
+        const qh_u32x4 u0 = *reinterpret_cast<const qh_u32x4*>(r + 128 + 16 * (kg & 1));
+        const qh_u32x4 u1 = *reinterpret_cast<const qh_u32x4*>(r + 160 + 16 * (kg & 1));
+        const uint32_t sh = 2u * (uint32_t)(kg >> 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v0 = u0[i] >> sh, v1 = u1[i] >> sh;
+            B[0][i] = (int)(qh_lo4(l0[i]) | ((v0 & 0x03030303u) << 4));
+            B[1][i] = (int)(qh_hi4(l0[i]) | (v0 & 0x30303030u));
+            B[2][i] = (int)(qh_lo4(l1[i]) | ((v1 & 0x03030303u) << 4));
+            B[3][i] = (int)(qh_hi4(l1[i]) | (v1 & 0x30303030u));
+        }
     }
-    template <int P>
-    static QH_DEV int scl(const H& h, int kg) {
-        return ((int)(h.s[P] >> (8 * kg)) << 24) >> 24;
-    }
-    template <int P>
-    static QH_DEV int mn(const H& h, int kg) { return scl<P>(h, kg); }
+    template <int S>
+    static QH_DEV int piece(int kg) { return 8 * (S >> 1) + 4 * (S & 1) + kg; }
+    template <int S>
+    static QH_DEV int scl(const H& h, int kg) { return ((int)(h.s[S] >> (8 * kg)) << 24) >> 24; }
+    template <int S>
+    static QH_DEV int mn(const H& h, int kg) { return scl<S>(h, kg); }
 };
 
 // ---------------------------------------------------------------- kernel
@@ -138,66 +172,87 @@ QH_DEV float qh_dpp_max(float m) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
 }
 
-template <class F, int W, int GPW>
+// Persistent kernel: workgroup b handles row tiles b, b + gridDim.x, ... (ROWS
+// rows each).  A wavefront's work items are (tile, K chunk) pairs; the weight
+// loads of the next item are issued before the current one is computed, so every
+// wavefront keeps one item of loads in flight for the whole kernel.  When K fits
+// one chunk (X1: W * GPW >= in_dim / 256), x is digitised once per workgroup.
+template <class F, int W, int GPW, bool X1>
 __global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ Wt, uint32_t wbytes,
                                                    const float* __restrict__ x, float* __restrict__ y, int out_dim,
                                                    uint32_t row_bytes, int ngroups) {
     constexpr int ROWS = F::ROWS, CH = F::CH;
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
     static_assert(ROWS <= 16 && 16 * CH < QH_RS, "tile shape");
-    __shared__ __align__(16) unsigned char lds[W * ROWS * QH_RS + W * GPW * 4 * QH_XU];
+    constexpr int TILE = ROWS * QH_RS + 16;  // staging tile of one group + 16 spare bytes
+    __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * W * 16 * 4 + QH_MAXT * 16 * 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const QhBuf wb = qh_buf(Wt, wbytes);
-    const int row0 = blockIdx.x * ROWS;
-    unsigned char* wl = lds + w * (ROWS * QH_RS);
-    unsigned char* xl = lds + W * ROWS * QH_RS + w * (GPW * 4 * QH_XU);
+    const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
+    unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
+    unsigned char* xl = lds + W * GPW * TILE + w * (GPW * QH_XG);
+    float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
+    float* res = red + 2 * W * 16;  // finished rows of this workgroup's tiles
+    const int ntiles = (out_dim + ROWS - 1) / ROWS;
+    const int nch = (ngroups + W * GPW - 1) / (W * GPW);
 
+    // Slices of this lane in a tile: row rr[h], byte offset goff[h] from the
+    // tile's first row, LDS offset soff[h].
     uint32_t goff[NH], soff[NH];
-    bool sok[NH];
+    int rr[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) {
         const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
-        sok[h] = q < ROWS * CH;
-        goff[h] = (sok[h] && row0 + r < out_dim) ? (uint32_t)(row0 + r) * row_bytes + 16u * c : 0x80000000u;
-        soff[h] = (uint32_t)(r * QH_RS + 16 * c);
+        rr[h] = q < ROWS * CH ? r : 1 << 30;
+        goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
+        // Lanes past ROWS * CH store into the spare bytes after the tile's last line.
+        soff[h] = q < ROWS * CH ? (uint32_t)(r * QH_RS + 16 * c) : (uint32_t)(ROWS * QH_RS);
     }
     const int n = lane & 15, kg = lane >> 4;
     const unsigned char* wrow = wl + (n < ROWS ? n : 0) * QH_RS;
-    const uint32_t aoff = ((n >> 2) == kg && (n & 3) < 3) ? 64u * (n & 3) + 16u * kg : QH_XU_ZERO;
-    const uint32_t bias = 0x4B400000u - 0x808080u;
+    // A operand of MFMA s: digit plane n%4 of lane kg's piece in rows 4kg..4kg+2.
+    const bool arow = (n >> 2) == kg && (n & 3) < 3;
+    uint32_t aoff[4], xsoff[4];
+    aoff[0] = arow ? 256u * (n & 3) + 16u * F::template piece<0>(kg) : QH_XG_ZERO;
+    aoff[1] = arow ? 256u * (n & 3) + 16u * F::template piece<1>(kg) : QH_XG_ZERO;
+    aoff[2] = arow ? 256u * (n & 3) + 16u * F::template piece<2>(kg) : QH_XG_ZERO;
+    aoff[3] = arow ? 256u * (n & 3) + 16u * F::template piece<3>(kg) : QH_XG_ZERO;
+    xsoff[0] = QH_XG_SUM + 4u * F::template piece<0>(kg);
+    xsoff[1] = QH_XG_SUM + 4u * F::template piece<1>(kg);
+    xsoff[2] = QH_XG_SUM + 4u * F::template piece<2>(kg);
+    xsoff[3] = QH_XG_SUM + 4u * F::template piece<3>(kg);
 
-    float tot = 0.f, bad = 0.f;
-    for (int cg = w * GPW; cg < ngroups; cg += W * GPW) {
-        float4 xv[GPW];
-#pragma unroll
-        for (int t = 0; t < GPW; t++)
-            xv[t] = (cg + t < ngroups) ? *reinterpret_cast<const float4*>(x + 256 * (cg + t) + 4 * lane)
-                                       : float4{0.f, 0.f, 0.f, 0.f};
-        qh_u32x4 wr[GPW * NH];
+    // Weight loads of item (tile, ch).  Rows past out_dim and groups past in_dim
+    // get offsets beyond the buffer range and read as zeros, so the load stream
+    // has no branches.
+    auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
+        const int g0 = ch * (W * GPW) + w * GPW;
+        const uint32_t base = (uint32_t)(tile * ROWS) * row_bytes;
 #pragma unroll
         for (int t = 0; t < GPW; t++)
 #pragma unroll
             for (int h = 0; h < NH; h++) {
-                const uint32_t off = (cg + t < ngroups ? goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)(cg + t);
-                if (F::BYTES % 16 == 0 || off + 16u <= wbytes || off >= 0x80000000u) {
-                    wr[t * NH + h] = qh_ld128(wb, off);
-                } else {
-                    // A slice that runs past the end of the tensor (the last block of a
-                    // 210-byte format): a dword straddling the range end reads as zero,
-                    // so load aligned dwords and realign.
-                    uint32_t raw[5], v[4];
-                    qh_ldwin<4>(wb, off, raw);
-                    qh_fix<4>(raw, off, v);
-                    wr[t * NH + h] = qh_u32x4{v[0], v[1], v[2], v[3]};
-                }
+                const bool ok = tile * ROWS + rr[h] < out_dim && g0 + t < ngroups;
+                wo[t * NH + h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)(g0 + t));
             }
-
-        // x -> digits.  One exponent per wavefront and chunk: max|x| * 2^s < 2^22.
+    };
+    auto load_x = [&](int ch, float4* xo) {
+        const int g0 = ch * (W * GPW) + w * GPW;
+#pragma unroll
+        for (int t = 0; t < GPW; t++) {
+            const qh_u32x4 v = qh_ld128(xb, 1024u * (uint32_t)(g0 + t) + 16u * lane);
+            xo[t] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+        }
+    };
+    // x -> digit planes in LDS.  One exponent per wavefront and chunk:
+    // max|x| * 2^s < 2^22.  Returns 2^-s; `bad` turns NaN when x is not finite.
+    float bad = 0.f;
+    auto prep_x = [&](const float4* xv) -> float {
         float m = 0.f;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
             m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[t].x), fabsf(xv[t].y)), fmaxf(fabsf(xv[t].z), fabsf(xv[t].w))));
-            bad += ((xv[t].x * 0.f + xv[t].y * 0.f) + (xv[t].z * 0.f + xv[t].w * 0.f));  // NaN iff x not finite
+            bad += ((xv[t].x * 0.f + xv[t].y * 0.f) + (xv[t].z * 0.f + xv[t].w * 0.f));
         }
         m = qh_dpp_max(m);
         int e = 0;
@@ -205,6 +260,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ W
         int s = m > 0.f ? 22 - e : 0;
         s = s > 126 ? 126 : s;
         const float scx = ldexpf(1.0f, s);
+        const uint32_t bias = 0x4B400000u - 0x808080u;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
             const float4 v = xv[t];
@@ -216,90 +272,177 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ W
             const uint32_t t23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
             const uint32_t u01 = __builtin_amdgcn_perm(a1, a0, 0x06020602u);
             const uint32_t u23 = __builtin_amdgcn_perm(a3, a2, 0x06020602u);
-            // lane holds x[256t + 4 lane .. +3]: slice lane/16, 16-group (lane/4)%4.
-            unsigned char* ub = xl + (4 * t + (lane >> 4)) * QH_XU;
-            const int pos = 4 * (lane & 15);
-            *reinterpret_cast<uint32_t*>(ub + pos) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
-            *reinterpret_cast<uint32_t*>(ub + 64 + pos) = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
-            *reinterpret_cast<uint32_t*>(ub + 128 + pos) = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
+            // lane holds x[256t + 4 lane .. +3] = positions 4(lane%4).. of piece lane/4.
+            unsigned char* ub = xl + t * QH_XG + 4 * lane;
+            *reinterpret_cast<uint32_t*>(ub) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+            *reinterpret_cast<uint32_t*>(ub + 256) = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
+            *reinterpret_cast<uint32_t*>(ub + 512) = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
             float hs = (v.x + v.y) + (v.z + v.w);
             hs += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hs), 0xB1, 0xF, 0xF, false));
             hs += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hs), 0x4E, 0xF, 0xF, false));
-            if ((lane & 3) == 0) *reinterpret_cast<float*>(ub + QH_XU_SUM + (lane & 12)) = hs;
-            if ((lane & 15) == 0) *reinterpret_cast<qh_u32x4*>(ub + QH_XU_ZERO) = qh_u32x4{0, 0, 0, 0};
+            if ((lane & 3) == 0) *reinterpret_cast<float*>(xl + t * QH_XG + QH_XG_SUM + lane) = hs;
+            if (lane == 0) *reinterpret_cast<qh_u32x4*>(xl + t * QH_XG + QH_XG_ZERO) = qh_u32x4{0, 0, 0, 0};
         }
-
+        return ldexpf(1.0f, -s);
+    };
+    // Move an item's weights from registers into the GPW staging tiles.
+    auto stage = [&](const qh_u32x4* wr) {
+#pragma unroll
+        for (int t = 0; t < GPW; t++)
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+                *reinterpret_cast<qh_u32x4*>(wl + t * TILE + soff[h]) = wr[t * NH + h];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // One staged item: four MFMAs per group.
+    auto compute = [&](float rs) -> float {
         float acc = 0.f, accm = 0.f;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
-            // Stage group t.  The tile is reused per group: LDS operations of one
-            // wavefront complete in order, so these writes follow the previous reads.
-#pragma unroll
-            for (int h = 0; h < NH; h++)
-                if (sok[h]) *reinterpret_cast<qh_u32x4*>(wl + soff[h]) = wr[t * NH + h];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const unsigned char* wrow = wl + t * TILE + (n < ROWS ? n : 0) * QH_RS;
             const typename F::H hd = F::hdr(wrow);
+            qh_i32x4 B[4];
+            F::bops(wrow, kg, hd, B);
             int i0 = 0, i1 = 0, i2 = 0;
             float fm = 0.f;
-            const unsigned char* xt = xl + 4 * t * QH_XU;
-            auto slice = [&](auto PC) {
-                constexpr int P = decltype(PC)::value;
-                const qh_i32x4 B = F::template bop<P>(wrow, kg, hd);
-                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xt + P * QH_XU + aoff);
-                const qh_i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B, qh_i32x4{0, 0, 0, 0}, 0, 0, 0);
-                const int sc = F::template scl<P>(hd, kg);
+            const unsigned char* xt = xl + t * QH_XG;
+            auto mfma = [&](auto SC) {
+                constexpr int S = decltype(SC)::value;
+                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xt + aoff[S]);
+                const qh_i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[S], qh_i32x4{0, 0, 0, 0}, 0, 0, 0);
+                const int sc = F::template scl<S>(hd, kg);
                 i0 += __mul24(sc, D[0]);
                 i1 += __mul24(sc, D[1]);
                 i2 += __mul24(sc, D[2]);
-                const float xs = *reinterpret_cast<const float*>(xt + P * QH_XU + QH_XU_SUM + 4 * kg);
-                fm = fmaf((float)F::template mn<P>(hd, kg), xs, fm);
+                const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
+                fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
                 __builtin_amdgcn_sched_barrier(0);
             };
-            slice(std::integral_constant<int, 0>{});
-            slice(std::integral_constant<int, 1>{});
-            slice(std::integral_constant<int, 2>{});
-            slice(std::integral_constant<int, 3>{});
+            mfma(std::integral_constant<int, 0>{});
+            mfma(std::integral_constant<int, 1>{});
+            mfma(std::integral_constant<int, 2>{});
+            mfma(std::integral_constant<int, 3>{});
             const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
             acc = fmaf(hd.d, P, acc);
             accm = fmaf(hd.dm, fm, accm);
         }
-        tot += fmaf(acc, ldexpf(1.0f, -s), -accm);
-    }
-    float v = tot + bad;
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);
-    if (lane < 16) red[w * 16 + lane] = v;
-    __syncthreads();
-    if (w == 0 && lane < ROWS && row0 + lane < out_dim) {
-        float r = 0.f;
+        return fmaf(acc, rs, -accm);
+    };
+
+    int tile = blockIdx.x, ch = 0, done = 0;
+    if (tile >= ntiles) return;  // uniform over the workgroup
+    // Pipeline: the registers of an item are staged into LDS as soon as they
+    // arrive and then receive the next item's loads, which stay in flight while
+    // the staged item is computed.  No loaded value is carried around the loop
+    // in registers (a copy between register sets would make the compiler drain
+    // every load in flight); a deeper, two-set pipeline measured slower.
+    qh_u32x4 wr[GPW * NH];
+    float4 xv[GPW];
+    float rs = 0.f, tot = 0.f;
+    load_x(0, xv);
+    load_w(tile, 0, wr);
+    for (;;) {
+        if (!X1 || (tile == blockIdx.x && ch == 0)) rs = prep_x(xv);
+        stage(wr);
+        int ntile = tile, nc = ch + 1;
+        if (X1 || nc == nch) { nc = 0; ntile += gridDim.x; }
+        if (!X1) load_x(nc, xv);
+        load_w(ntile, nc, wr);
+        tot += compute(rs);
+        if (nc == 0) {
+            // Tile finished: sum the four lanes of each column, then the wavefronts.
+            float v = tot + bad;
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            float* rb = red + (done & 1) * (W * 16);
+            if (lane < 16) rb[w * 16 + lane] = v;
+            __syncthreads();
+            // y is written after the loop: a store inside it would make the
+            // compiler drain all loads in flight (stores and loads share vmcnt).
+            if (w == 0 && lane < 16) {
+                float r = 0.f;
 #pragma unroll
-        for (int i = 0; i < W; i++) r += red[i * 16 + lane];
-        y[row0 + lane] = r;
+                for (int i = 0; i < W; i++) r += rb[i * 16 + lane];
+                res[done * 16 + lane] = r;
+            }
+            tot = 0.f;
+            done++;
+        }
+        if (ntile >= ntiles) break;
+        tile = ntile;
+        ch = nc;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < done * 16; i += 64 * W) {
+        const int row = (blockIdx.x + (i >> 4) * gridDim.x) * ROWS + (i & 15);
+        if ((i & 15) < ROWS && row < out_dim) y[row] = res[i];
     }
 }
 
-template <class F, int W, int GPW>
+template <class F, int W, int GPW, bool X1>
 static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim,
                                uint32_t row_bytes, hipStream_t st) {
+    static int resident = 0;  // workgroups the device holds at once (per instantiation)
+    if (!resident) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, GPW, X1>, 64 * W, 0) != hipSuccess ||
+            per_cu < 1)
+            return hipErrorNotSupported;
+        resident = per_cu * prop.multiProcessorCount;
+    }
     const int ngroups = in_dim / 256;
     // Rows are processed in chunks whose weight bytes fit a 31-bit buffer range.
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / F::ROWS * F::ROWS;
     if (max_rows < F::ROWS) return hipErrorNotSupported;
     for (int64_t r0 = 0; r0 < out_dim; r0 += max_rows) {
         const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
-        // Record count rounded up to a dword (the last 2-byte field of a 210-byte
-        // block shares its dword with the byte after the tensor).
         const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
-        hipLaunchKernelGGL((qh_mmv16<F, W, GPW>), dim3((unsigned)((rows + F::ROWS - 1) / F::ROWS)), dim3(64 * W), 0,
-                           st, Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups);
+        const int ntiles = (rows + F::ROWS - 1) / F::ROWS;
+        // As many workgroups as fit at once, with the tiles spread evenly.
+        int rounds = (ntiles + resident - 1) / resident;
+        if (rounds > QH_MAXT) rounds = QH_MAXT;
+        const int grid = (ntiles + rounds - 1) / rounds;
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1>), dim3((unsigned)grid), dim3(64 * W), 0, st,
+                           Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+template <class F, int W, int GPW>
+static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim,
+                               uint32_t row_bytes, hipStream_t st) {
+    if (in_dim <= 256 * W * GPW) return launch_mmv16<F, W, GPW, true>(Wt, x, y, in_dim, out_dim, row_bytes, st);
+    return launch_mmv16<F, W, GPW, false>(Wt, x, y, in_dim, out_dim, row_bytes, st);
+}
+
+// Launch shape: waves per workgroup W and groups per wave and chunk GPW.
+// Measured on MI355X: 16 x 1 is fastest when K fits one chunk (in_dim <= 4096),
+// 8 x 1 above that.  QUARTZ_HIP_MMV16=4|10|2 forces 16x1 | 8x1 | 8x2 (tuning).
+static int qh_mmv16_variant_env() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_MMV16");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+
+template <class F>
+static hipError_t dispatch_mmv16(const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                                 uint32_t row_bytes, hipStream_t st) {
+    int v = qh_mmv16_variant_env();
+    if (v < 0) v = in_dim <= 4096 ? 4 : 10;
+    switch (v) {
+        case 2: return launch_mmv16<F, 8, 2>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case 4: return launch_mmv16<F, 16, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case 10: return launch_mmv16<F, 8, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 // Returns hipErrorNotSupported when the type/shape has no kernel here.
@@ -308,9 +451,9 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
     if (in_dim % 256 || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     switch (type) {
-        case QT_Q4_K: return launch_mmv16<M16Q4K, 4, 4>(W, x, y, in_dim, out_dim, row_bytes, st);
-        case QT_Q5_K: return launch_mmv16<M16Q5K, 4, 4>(W, x, y, in_dim, out_dim, row_bytes, st);
-        case QT_Q6_K: return launch_mmv16<M16Q6K, 4, 4>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q4_K: return dispatch_mmv16<M16Q4K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q5_K: return dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
         default: return hipErrorNotSupported;
     }
 }

@@ -78,6 +78,53 @@ def test_gemv_fallback_shapes(qh, oracle, t, in_dim):
     assert cf.rel_l2(got, oracle.gemv(t, x, data, in_dim, out_dim)) < TOL
 
 
+# Shapes that give the persistent matrix-core kernel several row tiles per
+# workgroup (14336 rows), the tiles-per-workgroup cap (200000 rows), a partial
+# last tile and multi-chunk K (14336).
+BIG_SHAPES = [(14336, 4096), (4101, 14336), (200003, 256)]
+
+
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("shape", BIG_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_many_tiles(qh, oracle, t, shape):
+    out_dim, in_dim = shape
+    data = synth.weights(t, out_dim, in_dim, seed=31 * t + out_dim)
+    x = synth.activations(1, in_dim, seed=5 + in_dim)[0]
+    got = gpu_gemv(qh, t, x, data, in_dim, out_dim)
+    ref = oracle.gemv(t, x, data, in_dim, out_dim)
+    assert cf.rel_l2(got, ref) < TOL, (t, shape, cf.rel_l2(got, ref))
+    # every row is written (no stale rows from a missed tile)
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref)) + 1e-6
+
+
+def test_gemv_launch_variant_8x2(qh):
+    """The tuning override QUARTZ_HIP_MMV16=2 (8 waves x 2 groups) selects a
+    launch shape the defaults do not use; it must give the same results.  Runs in
+    a child process because the override is read once per process."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    code = (
+        "import sys, numpy as np; sys.path.insert(0, %r); sys.path.insert(0, %r)\n"
+        "from saient_quartz_amd import synth\n"
+        "from saient_quartz_amd.host import verify_gemv_hip\n"
+        "from oracle_lib import Oracle\n"
+        "import closed_form as cf\n"
+        "o = Oracle.load()\n"
+        "for t, (od, idim) in [(12, (3000, 4096)), (14, (2000, 14336)), (13, (1000, 2048))]:\n"
+        "    d = synth.weights(t, od, idim, seed=t); x = synth.activations(1, idim, seed=2)[0]\n"
+        "    e = cf.rel_l2(verify_gemv_hip(x, d, t, idim, od), o.gemv(t, x, d, idim, od))\n"
+        "    assert e < 1e-3, (t, e)\n"
+        "print('ok')\n" % (str(root), str(root / "tests")))
+    env = dict(os.environ, QUARTZ_HIP_MMV16="2")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
 @pytest.mark.parametrize("t", ALL_TYPES)
 def test_verify_gemv_criterion(qh, oracle, t):
     """Quartz's --verify-gemv check with its deterministic x (src/main.rs:2640-2662)."""
