@@ -33,6 +33,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 device copies of 256 MiB (torch copy kernel), to calibrate the "
+                         "FETCH_SIZE / WRITE_SIZE counters against known bytes")
     return ap.parse_args()
 
 
@@ -57,6 +60,15 @@ def main():
                                    "(the GEMV shards by output rows, see DESIGN.md)"}))
         sys.exit(2)
     import torch
+
+    if args.copy_calibration:
+        src = torch.empty(256 * 2**20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel(), "copies": 5}))
+        return
 
     from saient_quartz_amd import lib, type_size
     from saient_quartz_amd.api import check
@@ -118,6 +130,8 @@ def main():
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
 
+    traffic = measured_traffic(ROOT / "profiles" / "mmv16_q4k_14336x4096_traffic.md")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(out_dim, in_dim, args.cpu_seconds)
@@ -139,11 +153,23 @@ def main():
                    "out_dim": out_dim, "in_dim": in_dim, "batch": 1, "bytes_per_step": alg_bytes},
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "qh_mmv16<M16Q4K, 16, 1, true>", "kernel_us": round(kern_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
+
+
+def measured_traffic(path):
+    """HBM bytes per launch of the GEMV kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated); None if absent."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(out_dim, in_dim, seconds):

@@ -402,10 +402,11 @@ static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int 
         const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
         const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
         const int ntiles = (rows + F::ROWS - 1) / F::ROWS;
-        // As many workgroups as fit at once, with the tiles spread evenly.
-        int rounds = (ntiles + resident - 1) / resident;
-        if (rounds > QH_MAXT) rounds = QH_MAXT;
-        const int grid = (ntiles + rounds - 1) / rounds;
+        // One workgroup per tile up to what the device holds at once (tiles go
+        // round-robin, so some workgroups take one more tile than others); more
+        // only when a workgroup would exceed QH_MAXT tiles.
+        int grid = ntiles < resident ? ntiles : resident;
+        if ((ntiles + grid - 1) / grid > QH_MAXT) grid = (ntiles + QH_MAXT - 1) / QH_MAXT;
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1>), dim3((unsigned)grid), dim3(64 * W), 0, st,
                            Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups);
         hipError_t e = hipGetLastError();
