@@ -17,6 +17,11 @@
  * Q4_0 / Q4_1 (GGML types 2, 3) do not exist in Quartz; they follow the public
  * GGUF block layout only (parity unpinned by the reference, pinned by the
  * closed-form tests in tests/test_oracle.py).
+ *
+ * Bit-identity of the f32 sums (o_gemv / o_gemm) with the Rust binary: parity
+ * unpinned -- rustc is not available to run the reference; the sums are pinned
+ * to the float64 dot of the exact dequantized values (relative L2 < 1e-5) and
+ * the summation order is restated from the cited lines.
  */
 #include "quartz_oracle.h"
 
