@@ -33,24 +33,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the 8B-shape decode-step leg")
+    ap.add_argument("--decode-reps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 256 MiB (torch copy kernel), to calibrate the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes")
     return ap.parse_args()
-
-
-def device_q4k(torch, out_dim, in_dim, seed):
-    """Synthetic Q4_K weights generated on the device (same distributions as
-    saient_quartz_amd.synth.weights, torch RNG stream)."""
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    nb = out_dim * in_dim // 256
-    blk = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device="cuda", generator=g)
-    d = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.01).half()
-    dmin = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.005).half()
-    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
-    blk[:, 2:4] = dmin.view(torch.uint8).view(nb, 2)
-    return blk.reshape(-1)
 
 
 def main():
@@ -70,7 +58,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel(), "copies": 5}))
         return
 
-    from saient_quartz_amd import lib, type_size
+    from saient_quartz_amd import lib, synth_device, type_size
     from saient_quartz_amd.api import check
 
     L = lib()
@@ -78,7 +66,7 @@ def main():
     wbytes = type_size(Q4K, out_dim * in_dim)
     alg_bytes = wbytes + 4 * in_dim + 4 * out_dim
     rot = max(3, -(-768 * 2**20 // wbytes))
-    Ws = [device_q4k(torch, out_dim, in_dim, seed=20261201 + 1 + i) for i in range(rot)]
+    Ws = [synth_device.q4k(out_dim, in_dim, seed=20261201 + 1 + i) for i in range(rot)]
     x = torch.randn(in_dim, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7))
     y = torch.empty(out_dim, device="cuda")
     stream = torch.cuda.current_stream()
@@ -131,6 +119,8 @@ def main():
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
 
     traffic = measured_traffic(ROOT / "profiles" / "mmv16_q4k_14336x4096_traffic.md")
+    del Ws
+    decode = None if args.no_decode else decode_leg(torch, args.decode_reps)
 
     cpu = None
     if not args.no_cpu:
@@ -156,8 +146,47 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "qh_mmv16<M16Q4K, 16, 1, true>", "kernel_us": round(kern_ms * 1e3, 3)},
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     print(json.dumps(rec), flush=True)
+
+
+def decode_leg(torch, reps):
+    """Llama-3-8B-shaped Q4_K_M decode step: the 225
+    weight GEMVs of one step (32 layers x 7 + head) captured in one HIP graph,
+    timed over `reps` replays, for N = 1, 4, 16 tokens.  Weight streaming only:
+    the glue kernels between GEMVs are not part of this library yet."""
+    from saient_quartz_amd.decode import DecodeStep, Shape
+
+    shape = Shape()
+    wbytes = shape.weight_bytes()
+    step = DecodeStep(shape, n_max=16)
+    out = {"workload": "Llama-3-8B-shaped Q4_K_M decode step, weight GEMVs only (32 layers x q,k,v,o,gate,up,down "
+                       "+ Q6_K head), random-init weights, synthetic activations",
+           "weight_bytes": wbytes, "roofline_tok_s_n1": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)}
+    for n in (1, 4, 16):
+        g = torch.cuda.CUDAGraph()
+        step.issue(n)  # eager warm-up (first-call device queries happen outside capture)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step.issue(n)
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / reps
+        out[f"n{n}"] = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
+                        "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                        "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+        del g
+    del step
+    torch.cuda.empty_cache()
+    return out
 
 
 def measured_traffic(path):

@@ -1,0 +1,84 @@
+"""Llama-3-8B-shaped Q4_K_M decode step: the weight GEMVs of one token.
+
+Per layer, in the order of forward_gpu_step (src/cuda.rs:556-562, :647, :773-788):
+  q 4096x4096 Q4_K, k 1024x4096 Q4_K, v 1024x4096 Q6_K, o 4096x4096 Q4_K,
+  gate 14336x4096 Q4_K, up 14336x4096 Q4_K, down 4096x14336 Q6_K;
+then the output head 128256x4096 Q6_K.  32 layers: 4,875,853,824 weight bytes.
+
+`DecodeStep` holds random-init weights (seeded, generated on the device) and
+issues the step's GEMVs (n tokens: hip_gemm, n = 1: hip_gemv) through the C ABI
+on a caller stream.  The glue between GEMVs (rms_norm, rope, attention, swiglu,
+residual adds) is not part of this library yet: activations are fixed buffers,
+so a step measures weight streaming, which is >99% of the bytes of a decode step
+at short context.
+"""
+from dataclasses import dataclass
+
+import torch
+
+from . import synth_device
+from .api import check, lib
+
+Q4_K, Q6_K = 12, 14
+
+
+@dataclass(frozen=True)
+class Shape:
+    hidden: int = 4096
+    kv_dim: int = 1024  # 8 kv heads x 128
+    ffn: int = 14336
+    vocab: int = 128256
+    layers: int = 32
+
+    def layer_mats(self):
+        """(name, ggml_type, out_dim, in_dim) in call order."""
+        h, kv, f = self.hidden, self.kv_dim, self.ffn
+        return [("q", Q4_K, h, h), ("k", Q4_K, kv, h), ("v", Q6_K, kv, h), ("o", Q4_K, h, h),
+                ("gate", Q4_K, f, h), ("up", Q4_K, f, h), ("down", Q6_K, h, f)]
+
+    def weight_bytes(self) -> int:
+        from . import type_size
+        per_layer = sum(type_size(t, o * i) for _, t, o, i in self.layer_mats())
+        return per_layer * self.layers + type_size(Q6_K, self.vocab * self.hidden)
+
+
+class DecodeStep:
+    def __init__(self, shape: Shape = Shape(), n_max: int = 16, seed: int = 20261204):
+        self.shape = shape
+        self.L = lib()
+        s = shape
+        self.layers = []
+        for l in range(s.layers):
+            mats = []
+            for j, (name, t, o, i) in enumerate(s.layer_mats()):
+                mats.append((t, synth_device.weights(t, o, i, seed + 16 * l + j), o, i))
+            self.layers.append(mats)
+        self.head = (Q6_K, synth_device.weights(Q6_K, s.vocab, s.hidden, seed - 1), s.vocab, s.hidden)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 7)
+        # token-major activations: x[n][hidden] for every GEMV but down, xf[n][ffn] for down
+        self.x = torch.randn(n_max, s.hidden, device="cuda", generator=g)
+        self.xf = torch.randn(n_max, s.ffn, device="cuda", generator=g)
+        self.y = {name: torch.empty(n_max, o, device="cuda") for name, _, o, _ in s.layer_mats()}
+        self.logits = torch.empty(n_max, s.vocab, device="cuda")
+        self.n_max = n_max
+
+    def _mm(self, t, w, out, o, i, n, sp):
+        x = self.x if i == self.shape.hidden else self.xf
+        if n == 1:
+            check("hip_gemv_async", self.L.hip_gemv_async(t, w.data_ptr(), x.data_ptr(), out.data_ptr(),
+                                                          i, o, sp))
+        else:
+            check("hip_gemm_async", self.L.hip_gemm_async(t, w.data_ptr(), x.data_ptr(), out.data_ptr(),
+                                                          i, o, n, sp))
+
+    def issue(self, n: int = 1, stream=None):
+        """Enqueue one decode step's GEMVs for n tokens on `stream` (torch stream)."""
+        assert 1 <= n <= self.n_max
+        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        names = [m[0] for m in self.shape.layer_mats()]
+        for mats in self.layers:
+            for name, (t, w, o, i) in zip(names, mats):
+                self._mm(t, w, self.y[name], o, i, n, sp)
+        t, w, o, i = self.head
+        self._mm(t, w, self.logits, o, i, n, sp)
