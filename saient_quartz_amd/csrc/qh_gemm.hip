@@ -1,0 +1,493 @@
+// qh_gemm.hip -- batched dequant-GEMM for n = 2..16 tokens on the int8 matrix
+// cores (v_mfma_i32_32x32x32_i8), Q4_K / Q5_K / Q6_K.
+//
+// Y[t][j] = sum_k W[j,k] X[t][k], X and Y token-major.  One pass over the weights
+// serves every token: the weights are the B operand (32 weight rows = the 32
+// MFMA columns), the tokens are the A operand (A row 2t + m = digit m of token
+// t's x), so a lane's 16 results all belong to one weight row and one scale.
+//   * x as two balanced int8 digits: per token and K chunk, s = 14 - exponent of
+//     max|x|, x * 2^s is rounded to an integer of at most 2^14 in magnitude (one
+//     FMA against a magic constant) and split into d0 + 256 d1.  The int32 MFMA
+//     sums are exact; x's rounding (<= 2^-15 of the chunk's largest |x| per token)
+//     is the only error added (measured ~3e-5 relative L2 against the oracle,
+//     against the 1e-3 bar).
+//   * Q4_K / Q5_K: one MFMA per 32-weight sub-block (one scale), 16 tokens each.
+//     Q6_K: 16-weight scale groups, so a 32-weight chunk carries two scales: A
+//     rows 0-15 hold tokens' digits for k < 16 and rows 16-31 for k >= 16, 8
+//     tokens per MFMA, and result registers 0-7 / 8-15 take the two scales.
+//   * mins (Q4_K/Q5_K dmin * m_j * sum(x)): one more MFMA per group whose B
+//     operand is the 8 mins and whose A operand is the per-token sums of x over
+//     the sub-blocks, digitised the same way.  Q6_K's -32 is in its B operand
+//     (q - 32 is a signed byte), so its sums are not needed.
+// Weights are read with the same coalesced, LDS-staged, persistent pipeline as
+// qh_mmv16.hip (tiles of 32 rows; the next item's loads are in flight while the
+// current one is computed).  Every item re-digitises x for its K chunk and all
+// tokens (4 NT elements per lane).
+//
+// Reference counterpart: dequant::gemm (src/dequant.rs:143-200) with
+// q4k_row_batched / q6k_row_batched (:38-122); the reference has no GPU
+// batched path.
+#include "qh_formats.h"
+#include "qh_internal.h"
+
+typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t qh_i32x16 __attribute__((ext_vector_type(16)));
+
+#define QG_MAXT 4  // row tiles per workgroup (their results wait in LDS until the end)
+
+// ---------------------------------------------------------------- formats
+
+// Q4_K (src/dequant.rs:1471-1519): sub-block sb = 2p + nibble uses qs[32p + l].
+struct GQ4K {
+    static constexpr int BYTES = 144, CH = 9, RS = 144, LAST = 128;
+    static constexpr int SUMK = 32, SUMSH = 5;  // x sums over 32 (the mins' pieces)
+    static constexpr bool SUMS = true;
+    struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r) {
+        const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
+        H o;
+        o.sc0 = h.y & 0x3F3F3F3Fu;
+        o.mn0 = h.z & 0x3F3F3F3Fu;
+        o.sc1 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        o.mn1 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+        o.d = qh_f16_lo(h.x);
+        o.dm = qh_f16_hi(h.x);
+        return o;
+    }
+    // B operands of sub-blocks 2p, 2p+1 for lane half hh (k = 16 hh + e).
+    template <int P>
+    static QH_DEV void bpair(const unsigned char* r, int hh, qh_i32x4& b0, qh_i32x4& b1) {
+        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 16 + 32 * P + 16 * hh);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            b0[i] = (int)(q[i] & 0x0F0F0F0Fu);
+            b1[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+        }
+    }
+    template <int SB>
+    static QH_DEV int scl(const H& h) { return (int)(((SB < 4 ? h.sc0 : h.sc1) >> (8 * (SB & 3))) & 0xFFu); }
+    // B operand of the sums MFMA: the 8 mins in k = 0..7 (lanes of half 0).
+    static QH_DEV qh_i32x4 bmin(const unsigned char*, const H& h, int hh) {
+        return hh == 0 ? qh_i32x4{(int)h.mn0, (int)h.mn1, 0, 0} : qh_i32x4{0, 0, 0, 0};
+    }
+};
+
+// Q5_K (src/dequant.rs:1146-1182): as Q4_K plus bit sb of qh[l] as bit 4.
+struct GQ5K {
+    static constexpr int BYTES = 176, CH = 11, RS = 176, LAST = 160;
+    static constexpr int SUMK = 32, SUMSH = 5;
+    static constexpr bool SUMS = true;
+    using H = GQ4K::H;
+    static QH_DEV H hdr(const unsigned char* r) { return GQ4K::hdr(r); }
+    template <int P>
+    static QH_DEV void bpair(const unsigned char* r, int hh, qh_i32x4& b0, qh_i32x4& b1) {
+        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 48 + 32 * P + 16 * hh);
+        const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * hh);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = u[i] >> (2 * P);
+            b0[i] = (int)((q[i] & 0x0F0F0F0Fu) | ((v & 0x01010101u) << 4));
+            b1[i] = (int)(((q[i] >> 4) & 0x0F0F0F0Fu) | ((v & 0x02020202u) << 3));
+        }
+    }
+    template <int SB>
+    static QH_DEV int scl(const H& h) { return GQ4K::scl<SB>(h); }
+    static QH_DEV qh_i32x4 bmin(const unsigned char* r, const H& h, int hh) { return GQ4K::bmin(r, h, hh); }
+};
+
+// Q6_K (src/dequant.rs:1583-1631): chunk c = 4 half + quarter covers 32
+// consecutive weights: ql[64 half + 32 (quarter&1) + l] nibble quarter>>1, qh[32
+// half + l] bits 2 quarter..; scales 2c (l < 16) and 2c + 1 (l >= 16).
+struct GQ6K {
+    static constexpr int BYTES = 210, CH = 14, RS = 240, LAST = 194;  // d lands at 222
+    static constexpr int SUMK = 16, SUMSH = 4;
+    static constexpr bool SUMS = false;  // the -32 is in the B operand
+    struct H { qh_u32x4 s; float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r) {
+        H o;
+        o.s = *reinterpret_cast<const qh_u32x4*>(r + 192);
+        o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 222));
+        o.dm = 0.f;
+        return o;
+    }
+    template <int C>
+    static QH_DEV qh_i32x4 bop(const unsigned char* r, int hh) {
+        constexpr int half = C >> 2, qu = C & 3;
+        const qh_u32x4 l = *reinterpret_cast<const qh_u32x4*>(r + 64 * half + 32 * (qu & 1) + 16 * hh);
+        const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 128 + 32 * half + 16 * hh);
+        qh_i32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            // q in 0..63 per byte; (q + 0x60) ^ 0x80 is q - 32 as a signed byte (no carries)
+            b[i] = (int)(((((l[i] >> (4 * (qu >> 1))) & 0x0F0F0F0Fu) | (((u[i] >> (2 * qu)) & 0x03030303u) << 4)) +
+                          0x60606060u) ^ 0x80808080u);
+        return b;
+    }
+    template <int G>
+    static QH_DEV int scl(const H& h) { return ((int)(h.s[G >> 2] >> (8 * (G & 3))) << 24) >> 24; }
+};
+
+template <class F>
+struct IsQ6 { static constexpr bool value = false; };
+template <>
+struct IsQ6<GQ6K> { static constexpr bool value = true; };
+
+// ---------------------------------------------------------------- kernel
+
+// LDS per wavefront: x digits of one group for NT tokens -- plane 2t+m (digit m
+// of token t, 256 bytes) at 256 (2t+m), sum digits of plane 2t+m at
+// SUMS + 16 (2t+m) (8 or 16 bytes used, the rest stays zero), 256 zero bytes, and
+// 2^-s / 2^-(s - SUMSH) per token.
+template <int NT>
+struct XL {
+    static constexpr int SUMS = 512 * NT;
+    static constexpr int ZERO = SUMS + 32 * NT;
+    static constexpr int RS_ = ZERO + 256;
+    static constexpr int BYTES = RS_ + 8 * NT;
+};
+
+template <class F, int NT, int W>
+__global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt, uint32_t wbytes,
+                                                 const float* __restrict__ x, float* __restrict__ y, int out_dim,
+                                                 uint32_t row_bytes, int ngroups, int in_dim, int n, int ldy) {
+    constexpr int CH = F::CH, RS = F::RS;
+    constexpr int NH = (32 * CH + 63) / 64;  // 16-byte loads per lane per group
+    constexpr int TILE = 32 * RS + 16;
+    constexpr int LPT = 64 / NT, EPL = 4 * NT;  // lanes per token, x elements per lane
+    constexpr int NV = EPL / 4;                  // float4 per lane
+    static_assert(NT == 2 || NT == 4 || NT == 8 || NT == 16, "NT");
+    using X = XL<NT>;
+    __shared__ __align__(16) unsigned char lds[W * TILE + W * X::BYTES + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int R = lane & 31, hh = lane >> 5;
+    unsigned char* wl = lds + w * TILE;
+    unsigned char* xl = lds + W * TILE + w * X::BYTES;
+    float* red = reinterpret_cast<float*>(lds + W * TILE + W * X::BYTES);
+    float* res = red + W * NT * 32;
+    const QhBuf wb = qh_buf(Wt, wbytes);
+    const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
+    const int ntiles = (out_dim + 31) / 32;
+    const int nch = (ngroups + W - 1) / W;
+
+    // Zero this wavefront's x area once: sum-digit padding and the zero area are
+    // never written afterwards.
+    for (int i = lane * 16; i < X::BYTES; i += 64 * 16)
+        if (i + 16 <= X::BYTES) *reinterpret_cast<qh_u32x4*>(xl + i) = qh_u32x4{0, 0, 0, 0};
+
+    // Weight slices of this lane: row rr[h] of the tile, byte offset goff[h] from
+    // the tile's first row, LDS offset soff[h] (lanes past 32 * CH: spare bytes).
+    uint32_t goff[NH], soff[NH];
+    int rr[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+        const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
+        rr[h] = q < 32 * CH ? r : 1 << 30;
+        goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
+        soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
+    }
+    // x slice of this lane: token tx, elements EPL * part .. of the group.
+    const int tx = lane / LPT, part = lane % LPT;
+
+    auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
+        const int g = ch * W + w;
+        const uint32_t base = (uint32_t)(tile * 32) * row_bytes;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            const bool ok = tile * 32 + rr[h] < out_dim && g < ngroups;
+            wo[h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)g);
+        }
+    };
+    auto load_x = [&](int ch, float4* xo) {
+        const int g = ch * W + w;
+        const uint32_t off = (g < ngroups && tx < n)
+                                 ? 4u * ((uint32_t)tx * (uint32_t)in_dim + 256u * (uint32_t)g + (uint32_t)(EPL * part))
+                                 : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const qh_u32x4 v = qh_ld128(xb, off + 16u * i);
+            xo[i] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+        }
+    };
+    // x -> two digit planes per token + digitised sums over SUMK.  `bad` turns NaN
+    // when x is not finite.
+    float bad = 0.f;
+    auto prep_x = [&](const float4* xv) {
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w))));
+            bad += ((xv[i].x * 0.f + xv[i].y * 0.f) + (xv[i].z * 0.f + xv[i].w * 0.f));
+        }
+#pragma unroll
+        for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        int e = 0;
+        (void)frexpf(m, &e);
+        // |x| * 2^s < 2^14: even after rounding, n + 0x8080 stays below 2^16.
+        int s = m > 0.f ? 14 - e : 0;
+        s = s > 126 ? 126 : s;
+        const float scx = ldexpf(1.0f, s), scs = ldexpf(1.0f, s - F::SUMSH);
+        const uint32_t bias = 0x4B400000u - 0x8080u;
+        unsigned char* p0 = xl + 256 * (2 * tx) + EPL * part;
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const float4 v = xv[i];
+            const uint32_t a0 = (__float_as_uint(fmaf(v.x, scx, 12582912.0f)) - bias) ^ 0x8080u;
+            const uint32_t a1 = (__float_as_uint(fmaf(v.y, scx, 12582912.0f)) - bias) ^ 0x8080u;
+            const uint32_t a2 = (__float_as_uint(fmaf(v.z, scx, 12582912.0f)) - bias) ^ 0x8080u;
+            const uint32_t a3 = (__float_as_uint(fmaf(v.w, scx, 12582912.0f)) - bias) ^ 0x8080u;
+            const uint32_t t01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+            const uint32_t t23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+            *reinterpret_cast<uint32_t*>(p0 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+            *reinterpret_cast<uint32_t*>(p0 + 256 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
+            psum += (v.x + v.y) + (v.z + v.w);
+            // sum pieces of SUMK elements: finished every SUMK/4 float4 (or across lanes)
+            if constexpr (F::SUMS && EPL >= F::SUMK) {
+                if ((i + 1) % (F::SUMK / 4) == 0) {
+                    const int j = (EPL * part + 4 * i) / F::SUMK;
+                    const uint32_t a = (__float_as_uint(fmaf(psum, scs, 12582912.0f)) - bias) ^ 0x8080u;
+                    xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)(a & 0xFFu);
+                    xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(a >> 8);
+                    psum = 0.f;
+                }
+            }
+        }
+        if constexpr (F::SUMS && EPL < F::SUMK) {
+            // a piece spans SUMK / EPL lanes (consecutive parts of one token)
+#pragma unroll
+            for (int o = 1; o < F::SUMK / EPL; o <<= 1) psum += __shfl_xor(psum, o);
+            if ((part % (F::SUMK / EPL)) == 0) {
+                const int j = (EPL * part) / F::SUMK;
+                const uint32_t a = (__float_as_uint(fmaf(psum, scs, 12582912.0f)) - bias) ^ 0x8080u;
+                xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)(a & 0xFFu);
+                xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(a >> 8);
+            }
+        }
+        if (part == 0) {
+            reinterpret_cast<float*>(xl + X::RS_)[tx] = ldexpf(1.0f, -s);
+            reinterpret_cast<float*>(xl + X::RS_)[NT + tx] = ldexpf(1.0f, F::SUMSH - s);
+        }
+    };
+    auto stage = [&](const qh_u32x4* wr) {
+#pragma unroll
+        for (int h = 0; h < NH; h++) *reinterpret_cast<qh_u32x4*>(wl + soff[h]) = wr[h];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    // Token slots of this lane: t = 4q + 2hh + r (q < 4, r < 2); result register
+    // 4q + 2r + m of a 16-token MFMA holds digit m of slot (q, r).
+    float tot[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) tot[i] = 0.f;
+    const unsigned char* wrow = wl + R * RS;
+    // A operand offsets.  Main (Q4_K/Q5_K): plane R (token R/2, digit R%2).
+    const uint32_t aoffm = (R >> 1) < NT ? 256u * R + 16u * hh : (uint32_t)X::ZERO;
+    // Sums MFMA: plane R's sum digits in k = 0..15 (half 0 only).
+    const uint32_t aoffs = (hh == 0 && (R >> 1) < NT) ? (uint32_t)(X::SUMS + 16 * R) : (uint32_t)X::ZERO;
+    // Q6_K: MFMA u covers tokens 8u..8u+7; rows R < 16 take k < 16, rows >= 16 k >= 16.
+    uint32_t aoff6[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int t = 8 * u + ((R & 15) >> 1);
+        aoff6[u] = ((R >> 4) == hh && t < NT) ? 256u * (16 * u + (R & 15)) + 16u * hh : (uint32_t)X::ZERO;
+    }
+
+    auto compute = [&]() {
+        const typename F::H hd = F::hdr(wrow);
+        const float* rsv = reinterpret_cast<const float*>(xl + X::RS_);
+        int acc[16];
+        int acc2[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = acc2[j] = 0;
+        if constexpr (!IsQ6<F>::value) {
+            auto pair = [&](auto PC) {
+                constexpr int P = decltype(PC)::value;
+                qh_i32x4 b0, b1;
+                F::template bpair<P>(wrow, hh, b0, b1);
+                const qh_i32x4 a0 = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 64 * P);
+                const qh_i32x4 a1 = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 64 * P + 32);
+                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                const qh_i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
+                const int s0 = F::template scl<2 * P>(hd);
+#pragma unroll
+                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(s0, d0[j]);
+                const qh_i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
+                const int s1 = F::template scl<2 * P + 1>(hd);
+#pragma unroll
+                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(s1, d1[j]);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            pair(std::integral_constant<int, 0>{});
+            pair(std::integral_constant<int, 1>{});
+            pair(std::integral_constant<int, 2>{});
+            pair(std::integral_constant<int, 3>{});
+        } else {
+            auto chunk = [&](auto CC) {
+                constexpr int C = decltype(CC)::value;
+                const qh_i32x4 b = F::template bop<C>(wrow, hh);
+                const int slo = F::template scl<2 * C>(hd), shi = F::template scl<2 * C + 1>(hd);
+                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                {
+                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoff6[0] + 32 * C);
+                    const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) acc[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
+                }
+                if constexpr (NT > 8) {
+                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoff6[1] + 32 * C);
+                    const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) acc2[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            chunk(std::integral_constant<int, 0>{});
+            chunk(std::integral_constant<int, 1>{});
+            chunk(std::integral_constant<int, 2>{});
+            chunk(std::integral_constant<int, 3>{});
+            chunk(std::integral_constant<int, 4>{});
+            chunk(std::integral_constant<int, 5>{});
+            chunk(std::integral_constant<int, 6>{});
+            chunk(std::integral_constant<int, 7>{});
+        }
+        // sums MFMA: the mins (Q4_K/Q5_K)
+        qh_i32x16 dm = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        if constexpr (F::SUMS) {
+            const qh_i32x4 as = *reinterpret_cast<const qh_i32x4*>(xl + aoffs);
+            dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(as, F::bmin(wrow, hd, hh), dm, 0, 0, 0);
+        }
+        // finish: slot (q, r) = token 4q + 2hh + r
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int t = 4 * q + 2 * hh + r;
+                if (4 * q >= NT) continue;  // slot beyond the tokens for both lane halves
+                int i0, i1;
+                if constexpr (!IsQ6<F>::value) {
+                    i0 = acc[4 * q + 2 * r];
+                    i1 = acc[4 * q + 2 * r + 1];
+                } else {
+                    // Q6_K: MFMA u = q/2 holds slot q in register 4 (q%2) + 2r + m
+                    const int* a = (q < 2) ? acc : acc2;
+                    i0 = a[4 * (q & 1) + 2 * r];
+                    i1 = a[4 * (q & 1) + 2 * r + 1];
+                }
+                const float P = fmaf((float)i1, 256.0f, (float)i0);
+                const int tt = t < NT ? t : 0;
+                if constexpr (F::SUMS) {
+                    const float Pm = fmaf((float)dm[4 * q + 2 * r + 1], 256.0f, (float)dm[4 * q + 2 * r]);
+                    tot[2 * q + r] += fmaf(hd.d * P, rsv[tt], -hd.dm * Pm * rsv[NT + tt]);
+                } else {
+                    tot[2 * q + r] += hd.d * P * rsv[tt];
+                }
+            }
+    };
+
+    int tile = blockIdx.x, ch = 0, done = 0;
+    if (tile >= ntiles) return;  // uniform over the workgroup
+    qh_u32x4 wr[NH];
+    float4 xv[NV];
+    load_x(0, xv);
+    load_w(tile, 0, wr);
+    for (;;) {
+        prep_x(xv);
+        int ntile = tile, nc = ch + 1;
+        if (nc == nch) { nc = 0; ntile += gridDim.x; }
+        load_x(nc, xv);  // next item's x (L2-resident), in flight during the compute
+        stage(wr);
+        load_w(ntile, nc, wr);  // past the last tile: all offsets out of range, no traffic
+        compute();
+        if (nc == 0) {
+            // Tile finished: lanes hold (token slot, weight row R); sum the wavefronts.
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const int t = 4 * q + 2 * hh + r;
+                    if (t < NT) red[(w * NT + t) * 32 + R] = tot[2 * q + r] + bad;
+                    tot[2 * q + r] = 0.f;
+                }
+            __syncthreads();
+            // y is written after the loop: a store inside it would make the
+            // compiler drain all loads in flight (stores and loads share vmcnt).
+            for (int i = threadIdx.x; i < NT * 32; i += 64 * W) {
+                float v = 0.f;
+#pragma unroll
+                for (int k = 0; k < W; k++) v += red[k * NT * 32 + i];
+                res[done * NT * 32 + i] = v;
+            }
+            __syncthreads();
+            done++;
+        }
+        if (ntile >= ntiles) break;
+        tile = ntile;
+        ch = nc;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < done * NT * 32; i += 64 * W) {
+        const int k = i / (NT * 32), t = (i / 32) % NT, r = i & 31;
+        const int row = (blockIdx.x + k * gridDim.x) * 32 + r;
+        if (t < n && row < out_dim) y[(size_t)t * ldy + row] = res[i];
+    }
+}
+
+template <class F, int NT, int W>
+static hipError_t launch_mmq(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim, int n,
+                             uint32_t row_bytes, hipStream_t st) {
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmq<F, NT, W>, 64 * W, 0) != hipSuccess ||
+            per_cu < 1)
+            return hipErrorNotSupported;
+        resident = per_cu * prop.multiProcessorCount;
+    }
+    const int ngroups = in_dim / 256;
+    const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
+    if (max_rows < 32 || (int64_t)n * in_dim * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    for (int64_t r0 = 0; r0 < out_dim; r0 += max_rows) {
+        const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
+        const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
+        const int ntiles = (rows + 31) / 32;
+        int grid = ntiles < resident ? ntiles : resident;
+        if ((ntiles + grid - 1) / grid > QG_MAXT) grid = (ntiles + QG_MAXT - 1) / QG_MAXT;
+        // y rows r0.. of every token: y + r0 with the token stride out_dim.
+        hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)grid), dim3(64 * W), 0, st,
+                           Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups, in_dim, n,
+                           out_dim);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Batched tokens on the matrix cores; hipErrorNotSupported when the type/shape
+// has no kernel here.  Tokens go in chunks of up to 16 (one weight pass each).
+hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
+                         hipStream_t st) {
+    if (in_dim % 256 || ((uintptr_t)x & 15u) || n < 2) return hipErrorNotSupported;
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K) return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    for (int t0 = 0; t0 < n; t0 += 16) {
+        const int nt = n - t0 < 16 ? n - t0 : 16;
+        const float* xs = x + (size_t)t0 * in_dim;
+        float* ys = y + (size_t)t0 * out_dim;
+        hipError_t e;
+#define QG_CASE(F)                                                                                   \
+    if (nt <= 2) e = launch_mmq<F, 2, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);             \
+    else if (nt <= 4) e = launch_mmq<F, 4, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);        \
+    else if (nt <= 8) e = launch_mmq<F, 8, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);        \
+    else e = launch_mmq<F, 16, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);
+        if (type == QT_Q4_K) { QG_CASE(GQ4K) }
+        else if (type == QT_Q5_K) { QG_CASE(GQ5K) }
+        else { QG_CASE(GQ6K) }
+#undef QG_CASE
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}

@@ -165,10 +165,15 @@ hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float
     return hipGetLastError();
 }
 
-// Batched tokens, first version: one batch-1 pass per token (weights are
-// re-streamed n times).  Replaced by the MFMA path for the shapes it covers.
+// Batched tokens: the matrix-core kernel (one weight pass per 16 tokens) where
+// it covers the type and shape, else one batch-1 pass per token.
 hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                           int n, hipStream_t st) {
+    if (n == 1) return qh_launch_gemv(type, W, x, y, in_dim, out_dim, st);
+    if (!qh_force_valu()) {
+        hipError_t e = qh_launch_mmq(type, W, x, y, in_dim, out_dim, n, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     for (int t = 0; t < n; t++) {
         hipError_t e = qh_launch_gemv(type, W, x + (size_t)t * in_dim, y + (size_t)t * out_dim, in_dim, out_dim, st);
         if (e != hipSuccess) return e;

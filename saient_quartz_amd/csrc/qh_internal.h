@@ -44,6 +44,8 @@ __device__ void qh_decode_block(uint32_t type, const uint8_t* blk, float* out);
 
 hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                            hipStream_t st);
+hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                         int n, hipStream_t st);
 hipError_t qh_launch_mmv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                          hipStream_t st);
 // QUARTZ_HIP_KERNEL=valu selects the lane-per-unit VALU kernels instead of the

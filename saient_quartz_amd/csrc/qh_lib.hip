@@ -5,5 +5,6 @@
 #include "qh_dequant.hip"
 #include "qh_mmv.hip"
 #include "qh_mmv16.hip"
+#include "qh_gemm.hip"
 #include "qh_gemv.hip"
 #include "qh_api.hip"

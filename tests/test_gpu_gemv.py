@@ -149,6 +149,27 @@ def test_gemm_vs_oracle(qh, oracle, t, n):
     assert cf.rel_l2(got, ref) < TOL
 
 
+# The matrix-core batched path (Q4_K, Q5_K, Q6_K): token counts that use each
+# token-tile size (2, 4, 8, 16) and the chunking past 16; shapes with several K
+# chunks, a partial last row tile and more tiles than one workgroup keeps.
+MMQ_CASES = [(40, 4096, 2), (40, 4096, 3), (77, 4096, 5), (300, 14336, 8), (100, 4096, 11), (130, 2048, 16),
+             (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4)]
+
+
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("case", MMQ_CASES, ids=lambda c: f"{c[0]}x{c[1]}n{c[2]}")
+def test_gemm_matrix_core(qh, oracle, t, case):
+    out_dim, in_dim, n = case
+    data = synth.weights(t, out_dim, in_dim, seed=17 * t + out_dim + n)
+    x = synth.activations(n, in_dim, seed=3 + n + in_dim)
+    # tokens of very different magnitudes: each has its own digit exponent
+    x = x * (10.0 ** np.linspace(-3, 3, n, dtype=np.float32))[:, None].astype(np.float32)
+    got = gpu_gemm(qh, t, x, data, in_dim, out_dim, n)
+    ref = oracle.gemm(t, x, data, in_dim, out_dim, n)
+    for k in range(n):
+        assert cf.rel_l2(got[k], ref[k]) < TOL, (t, case, k, cf.rel_l2(got[k], ref[k]))
+
+
 def test_expert_slices_and_moe4(qh, oracle):
     """Stacked experts addressed as base + e * type_size (src/cuda.rs:250-258)."""
     t, in_dim, out_dim, n_exp = 21, 1024, 64, 4
