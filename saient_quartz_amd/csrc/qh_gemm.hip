@@ -135,12 +135,13 @@ struct IsQ6<GQ6K> { static constexpr bool value = true; };
 // ---------------------------------------------------------------- kernel
 
 // LDS per wavefront: x digits of one group for NT tokens -- plane 2t+m (digit m
-// of token t, 256 bytes) at 256 (2t+m), sum digits of plane 2t+m at
+// of token t, 256 bytes) at PS (2t+m), sum digits of plane 2t+m at
 // SUMS + 16 (2t+m) (8 or 16 bytes used, the rest stays zero), 256 zero bytes, and
 // 2^-s / 2^-(s - SUMSH) per token.
 template <int NT>
 struct XL {
-    static constexpr int SUMS = 512 * NT;
+    static constexpr int PS = 272;  // plane stride: 256 bytes + 16, conflict-free b128 reads over 16 rows
+    static constexpr int SUMS = 2 * PS * NT;
     static constexpr int ZERO = SUMS + 32 * NT;
     static constexpr int RS_ = ZERO + 256;
     static constexpr int BYTES = RS_ + 8 * NT;
@@ -208,63 +209,77 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             xo[i] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
         }
     };
-    // x -> two digit planes per token + digitised sums over SUMK.  `bad` turns NaN
-    // when x is not finite.
-    float bad = 0.f;
+    // x -> two digit planes per token + digitised sums over SUMK.
+    //   fmaf(x, 2^s, 12615808) = 1.5 * 2^23 + 0x8080 + n (n = round(x 2^s), |n| <=
+    //   2^14), so the float's low 16 bits are n + 0x8080 and its bytes XOR 0x80
+    //   are the balanced digits; the sums are exact integer sums of those n (sum
+    //   of the float bits minus k * 0x4B408080, mod 2^32).
+    //   A token whose chunk holds Inf or NaN (max|x| is Inf, or a bit sum falls
+    //   outside the range finite values allow) gets 2^-s = NaN, so exactly its
+    //   outputs are NaN, as in the reference's f32 dot.
     auto prep_x = [&](const float4* xv) {
         float m = 0.f;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w))));
-            bad += ((xv[i].x * 0.f + xv[i].y * 0.f) + (xv[i].z * 0.f + xv[i].w * 0.f));
+            // v_max3_f32 with |.| source modifiers: one instruction per two elements
+            // (NaN is caught by the bit-sum check below, not by the max).
+            __asm__("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(m) : "v"(xv[i].x), "v"(xv[i].y));
+            __asm__("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(m) : "v"(xv[i].z), "v"(xv[i].w));
         }
 #pragma unroll
         for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
         int e = 0;
         (void)frexpf(m, &e);
-        // |x| * 2^s < 2^14: even after rounding, n + 0x8080 stays below 2^16.
+        // |x| * 2^s <= 2^14: even after rounding, n + 0x8080 stays below 2^16.
         int s = m > 0.f ? 14 - e : 0;
-        s = s > 126 ? 126 : s;
-        const float scx = ldexpf(1.0f, s), scs = ldexpf(1.0f, s - F::SUMSH);
-        const uint32_t bias = 0x4B400000u - 0x8080u;
-        unsigned char* p0 = xl + 256 * (2 * tx) + EPL * part;
-        float psum = 0.f;
+        s = s > 126 ? 126 : (s < -126 ? -126 : s);
+        const float scx = ldexpf(1.0f, s);
+        const float magic = 12615808.0f;  // 0x4B408080
+        unsigned char* p0 = xl + X::PS * (2 * tx) + EPL * part;
+        constexpr int PIECE = F::SUMS ? F::SUMK : EPL;  // elements per checked bit sum
+        constexpr int PL = PIECE < EPL ? PIECE : EPL;    // of which in this lane
+        uint32_t psum = 0;
+        bool nonfinite = !(m <= 3.0e38f);
+        auto piece_done = [&](int j) {
+            uint32_t ps = psum;
+            if constexpr (PIECE > EPL) {
+#pragma unroll
+                for (int o = 1; o < PIECE / EPL; o <<= 1) ps += (uint32_t)__shfl_xor((int)ps, o);
+            }
+            const int sn = (int)(ps - (uint32_t)PIECE * 0x4B408080u);
+            nonfinite |= sn > PIECE * 16384 || sn < -PIECE * 16384;
+            if constexpr (F::SUMS) {
+                if (PIECE <= EPL || (part % (PIECE / EPL)) == 0) {
+                    // sum of n in units of 2^SUMSH (|result| <= 2^14)
+                    const int ns = (sn + (1 << (F::SUMSH - 1))) >> F::SUMSH;
+                    const uint32_t u = (uint32_t)(ns + 0x8080);
+                    xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)((u & 0xFFu) ^ 0x80u);
+                    xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(((u >> 8) & 0xFFu) ^ 0x80u);
+                }
+            }
+            psum = 0;
+        };
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const float4 v = xv[i];
-            const uint32_t a0 = (__float_as_uint(fmaf(v.x, scx, 12582912.0f)) - bias) ^ 0x8080u;
-            const uint32_t a1 = (__float_as_uint(fmaf(v.y, scx, 12582912.0f)) - bias) ^ 0x8080u;
-            const uint32_t a2 = (__float_as_uint(fmaf(v.z, scx, 12582912.0f)) - bias) ^ 0x8080u;
-            const uint32_t a3 = (__float_as_uint(fmaf(v.w, scx, 12582912.0f)) - bias) ^ 0x8080u;
+            const uint32_t a0 = __float_as_uint(fmaf(v.x, scx, magic));
+            const uint32_t a1 = __float_as_uint(fmaf(v.y, scx, magic));
+            const uint32_t a2 = __float_as_uint(fmaf(v.z, scx, magic));
+            const uint32_t a3 = __float_as_uint(fmaf(v.w, scx, magic));
             const uint32_t t01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
             const uint32_t t23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
-            *reinterpret_cast<uint32_t*>(p0 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
-            *reinterpret_cast<uint32_t*>(p0 + 256 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
-            psum += (v.x + v.y) + (v.z + v.w);
-            // sum pieces of SUMK elements: finished every SUMK/4 float4 (or across lanes)
-            if constexpr (F::SUMS && EPL >= F::SUMK) {
-                if ((i + 1) % (F::SUMK / 4) == 0) {
-                    const int j = (EPL * part + 4 * i) / F::SUMK;
-                    const uint32_t a = (__float_as_uint(fmaf(psum, scs, 12582912.0f)) - bias) ^ 0x8080u;
-                    xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)(a & 0xFFu);
-                    xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(a >> 8);
-                    psum = 0.f;
-                }
-            }
+            *reinterpret_cast<uint32_t*>(p0 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+            *reinterpret_cast<uint32_t*>(p0 + X::PS + 4 * i) =
+                __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+            psum += a0 + a1 + a2 + a3;
+            if ((4 * i + 4) % PL == 0) piece_done((EPL * part + 4 * i) / PIECE);
         }
-        if constexpr (F::SUMS && EPL < F::SUMK) {
-            // a piece spans SUMK / EPL lanes (consecutive parts of one token)
+        // every lane of the token agrees on the flag
+        int nf = nonfinite ? 1 : 0;
 #pragma unroll
-            for (int o = 1; o < F::SUMK / EPL; o <<= 1) psum += __shfl_xor(psum, o);
-            if ((part % (F::SUMK / EPL)) == 0) {
-                const int j = (EPL * part) / F::SUMK;
-                const uint32_t a = (__float_as_uint(fmaf(psum, scs, 12582912.0f)) - bias) ^ 0x8080u;
-                xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)(a & 0xFFu);
-                xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(a >> 8);
-            }
-        }
+        for (int o = 1; o < LPT; o <<= 1) nf |= __shfl_xor(nf, o);
         if (part == 0) {
-            reinterpret_cast<float*>(xl + X::RS_)[tx] = ldexpf(1.0f, -s);
+            reinterpret_cast<float*>(xl + X::RS_)[tx] = nf ? __builtin_nanf("") : ldexpf(1.0f, -s);
             reinterpret_cast<float*>(xl + X::RS_)[NT + tx] = ldexpf(1.0f, F::SUMSH - s);
         }
     };
@@ -283,7 +298,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
     for (int i = 0; i < 8; i++) tot[i] = 0.f;
     const unsigned char* wrow = wl + R * RS;
     // A operand offsets.  Main (Q4_K/Q5_K): plane R (token R/2, digit R%2).
-    const uint32_t aoffm = (R >> 1) < NT ? 256u * R + 16u * hh : (uint32_t)X::ZERO;
+    const uint32_t aoffm = (R >> 1) < NT ? (uint32_t)X::PS * R + 16u * hh : (uint32_t)X::ZERO;
     // Sums MFMA: plane R's sum digits in k = 0..15 (half 0 only).
     const uint32_t aoffs = (hh == 0 && (R >> 1) < NT) ? (uint32_t)(X::SUMS + 16 * R) : (uint32_t)X::ZERO;
     // Q6_K: MFMA u covers tokens 8u..8u+7; rows R < 16 take k < 16, rows >= 16 k >= 16.
@@ -291,7 +306,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int t = 8 * u + ((R & 15) >> 1);
-        aoff6[u] = ((R >> 4) == hh && t < NT) ? 256u * (16 * u + (R & 15)) + 16u * hh : (uint32_t)X::ZERO;
+        aoff6[u] = ((R >> 4) == hh && t < NT) ? (uint32_t)X::PS * (16 * u + (R & 15)) + 16u * hh : (uint32_t)X::ZERO;
     }
 
     auto compute = [&]() {
@@ -313,6 +328,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 const int s0 = F::template scl<2 * P>(hd);
 #pragma unroll
                 for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(s0, d0[j]);
+                __builtin_amdgcn_sched_barrier(0);
                 const qh_i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
                 const int s1 = F::template scl<2 * P + 1>(hd);
 #pragma unroll
@@ -407,7 +423,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     const int t = 4 * q + 2 * hh + r;
-                    if (t < NT) red[(w * NT + t) * 32 + R] = tot[2 * q + r] + bad;
+                    if (t < NT) red[(w * NT + t) * 32 + R] = tot[2 * q + r];
                     tot[2 * q + r] = 0.f;
                 }
             __syncthreads();
@@ -466,6 +482,15 @@ static hipError_t launch_mmq(const uint8_t* Wt, const float* x, float* y, int in
     return hipSuccess;
 }
 
+// QUARTZ_HIP_MMQ_WAVES=4|8 forces the workgroup size (tuning).
+static int qh_mmq_waves_env() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_MMQ_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 // Batched tokens on the matrix cores; hipErrorNotSupported when the type/shape
 // has no kernel here.  Tokens go in chunks of up to 16 (one weight pass each).
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
@@ -478,15 +503,22 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
         const float* xs = x + (size_t)t0 * in_dim;
         float* ys = y + (size_t)t0 * out_dim;
         hipError_t e;
+        // 8 wavefronts per workgroup when the row tiles alone give few workgroups
+        // (measured faster for Q4_K/Q5_K at 4096 rows); Q6_K's 16-token kernel
+        // does not fit 8 wavefronts' registers.
+        const bool w8 = qh_mmq_waves_env() == 8 ||
+                        (qh_mmq_waves_env() != 4 && type != QT_Q6_K && (out_dim + 31) / 32 < 256);
+#define QG_NT(F, NT_)                                                                                 \
+    e = w8 ? launch_mmq<F, NT_, 8>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st)                     \
+           : launch_mmq<F, NT_, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);
 #define QG_CASE(F)                                                                                   \
-    if (nt <= 2) e = launch_mmq<F, 2, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);             \
-    else if (nt <= 4) e = launch_mmq<F, 4, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);        \
-    else if (nt <= 8) e = launch_mmq<F, 8, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);        \
-    else e = launch_mmq<F, 16, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);
+    if (nt <= 2) { QG_NT(F, 2) } else if (nt <= 4) { QG_NT(F, 4) } else if (nt <= 8) { QG_NT(F, 8) } \
+    else { QG_NT(F, 16) }
         if (type == QT_Q4_K) { QG_CASE(GQ4K) }
         else if (type == QT_Q5_K) { QG_CASE(GQ5K) }
         else { QG_CASE(GQ6K) }
 #undef QG_CASE
+#undef QG_NT
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
