@@ -121,6 +121,7 @@ def main():
     traffic = measured_traffic(ROOT / "profiles" / "mmv16_q4k_14336x4096_traffic.md")
     del Ws
     decode = None if args.no_decode else decode_leg(torch, args.decode_reps)
+    moe = None if args.no_decode else moe_leg(torch, args.decode_reps)
 
     cpu = None
     if not args.no_cpu:
@@ -147,6 +148,7 @@ def main():
                      "kernel": "qh_mmv16<M16Q4K, 16, 1, true>", "kernel_us": round(kern_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "decode": decode,
+        "moe": moe,
     }
     print(json.dumps(rec), flush=True)
 
@@ -186,6 +188,41 @@ def decode_leg(torch, reps):
         del g
     del step
     torch.cuda.empty_cache()
+    return out
+
+
+def moe_leg(torch, reps):
+    """Mixtral-shaped MoE expert layer: 8 experts x
+    (gate, up, down) with 16 gathered tokens each, IQ3_S and IQ2_XXS, one HIP
+    graph per layer step, timed over `reps` replays."""
+    from saient_quartz_amd.decode import MoeLayer
+
+    out = {"workload": "Mixtral-8x7B-shaped MoE expert layer: 8 experts, gate/up 14336x4096 + down 4096x14336, "
+                       "16 tokens gathered per expert (top-2 of 64 tokens), random-init weights"}
+    for name, t in (("iq3_s", 21), ("iq2_xxs", 16)):
+        layer = MoeLayer(t)
+        wbytes = layer.weight_bytes()
+        layer.issue()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            layer.issue()
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / reps
+        out[name] = {"ms_per_layer": round(ms, 4), "weight_bytes": wbytes,
+                     "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+                     "tokens_per_s": round(64 / (ms * 1e-3), 1)}
+        del g, layer
+        torch.cuda.empty_cache()
     return out
 
 

@@ -1,5 +1,5 @@
 // qh_gemm.hip -- batched dequant-GEMM for n = 2..16 tokens on the int8 matrix
-// cores (v_mfma_i32_32x32x32_i8), Q4_K / Q5_K / Q6_K.
+// cores (v_mfma_i32_32x32x32_i8), Q4_K / Q5_K / Q6_K / IQ3_S / IQ2_XXS.
 //
 // Y[t][j] = sum_k W[j,k] X[t][k], X and Y token-major.  One pass over the weights
 // serves every token: the weights are the B operand (32 weight rows = the 32
@@ -42,6 +42,7 @@ struct GQ4K {
     static constexpr int BYTES = 144, CH = 9, RS = 144, LAST = 128;
     static constexpr int SUMK = 32, SUMSH = 5;  // x sums over 32 (the mins' pieces)
     static constexpr bool SUMS = true;
+    static constexpr int KIND = 0, GRID = 0;  // sub-block pairs from one qs load
     struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
@@ -77,6 +78,7 @@ struct GQ5K {
     static constexpr int BYTES = 176, CH = 11, RS = 176, LAST = 160;
     static constexpr int SUMK = 32, SUMSH = 5;
     static constexpr bool SUMS = true;
+    static constexpr int KIND = 0, GRID = 0;
     using H = GQ4K::H;
     static QH_DEV H hdr(const unsigned char* r) { return GQ4K::hdr(r); }
     template <int P>
@@ -102,6 +104,7 @@ struct GQ6K {
     static constexpr int BYTES = 210, CH = 14, RS = 240, LAST = 194;  // d lands at 222
     static constexpr int SUMK = 16, SUMSH = 4;
     static constexpr bool SUMS = false;  // the -32 is in the B operand
+    static constexpr int KIND = 2, GRID = 0;  // two scales per 32 weights
     struct H { qh_u32x4 s; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         H o;
@@ -125,6 +128,72 @@ struct GQ6K {
     }
     template <int G>
     static QH_DEV int scl(const H& h) { return ((int)(h.s[G >> 2] >> (8 * (G & 3))) << 24) >> 24; }
+};
+
+
+// IQ3_S (src/dequant.rs:1184-1237), 110-byte blocks: d, qs[64], qh[8],
+// signs[32], scales[4].  Sub-block k (32 weights, scale d (1 + 2 nibble)):
+// 8-weight group l has grid indices qs[8k + 2l], qs[8k + 2l + 1] with bits 2l,
+// 2l+1 of qh[k] as bit 8, and sign byte signs[4k + l].  Weights are signed grid
+// bytes, so the B operand holds the dequantized value / (d scale) exactly.
+// The 7th 16-byte slice is loaded from block bytes 94-109: block byte b >= 96
+// sits at LDS b + 2.
+extern __device__ uint32_t qh_g_iq3s[512];
+extern __device__ uint64_t qh_g_iq2xxs[256];
+
+QH_DEV uint32_t qh_rd16(const unsigned char* p, int o) { return *reinterpret_cast<const uint16_t*>(p + o); }
+
+struct GIQ3S {
+    static constexpr int BYTES = 110, CH = 7, RS = 112, LAST = 94;
+    static constexpr int SUMK = 32, SUMSH = 5;
+    static constexpr bool SUMS = false;
+    static constexpr int KIND = 1, GRID = 1;  // one scale per 32 weights; IQ3S codebook in LDS
+    struct H { float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r) { return H{qh_h2f(qh_rd16(r, 0)), 0.f}; }
+    static QH_DEV int at(int o) { return o >= 96 ? o + 2 : o; }
+    template <int K>
+    static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
+        const int oq = 2 + 8 * K + 4 * hh;  // 4 index bytes of groups 2hh, 2hh+1
+        const uint32_t q = qh_rd16(r, oq) | (qh_rd16(r, oq + 2) << 16);
+        const uint32_t qh = (uint32_t)r[66 + K] >> (4 * hh);
+        const uint32_t sg = qh_rd16(r, at(74 + 4 * K + 2 * hh));
+        const uint32_t* g32 = reinterpret_cast<const uint32_t*>(grid);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t idx = ((q >> (8 * m)) & 0xFFu) | (((qh >> m) & 1u) << 8);
+            b[m] = (int)qh_negbytes(g32[idx], qh_signmask4(sg >> (4 * m)));
+        }
+        sc = 1 + 2 * (int)((r[at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
+    }
+};
+
+// IQ2_XXS (src/dequant.rs:1011-1041), 66-byte blocks: d, then per sub-block k 4
+// grid indices (bytes 2+8k..) and a u32 (bytes 6+8k..) holding four 7-bit sign
+// fields and the scale in bits 28-31: weight = d/8 (2 scale + 1) grid * sign.
+// The 5th slice is loaded from block bytes 50-65: block byte b >= 64 sits at LDS
+// b + 14.
+struct GIQ2XXS {
+    static constexpr int BYTES = 66, CH = 5, RS = 80, LAST = 50;
+    static constexpr int SUMK = 32, SUMSH = 5;
+    static constexpr bool SUMS = false;
+    static constexpr int KIND = 1, GRID = 2;  // IQ2XXS codebook in LDS
+    struct H { float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r) { return H{0.125f * qh_h2f(qh_rd16(r, 0)), 0.f}; }
+    static QH_DEV int at(int o) { return o >= 64 ? o + 14 : o; }
+    template <int K>
+    static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
+        const uint32_t a0 = qh_rd16(r, 2 + 8 * K + 2 * hh);  // indices of groups 2hh, 2hh+1
+        const uint32_t a1 = qh_rd16(r, at(6 + 8 * K)) | (qh_rd16(r, at(8 + 8 * K)) << 16);
+        const uint64_t* g64 = reinterpret_cast<const uint64_t*>(grid);
+#pragma unroll
+        for (int l = 0; l < 2; l++) {
+            const uint64_t g = g64[(a0 >> (8 * l)) & 0xFFu];
+            const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * hh + l))) & 127u);
+            b[2 * l] = (int)qh_negbytes((uint32_t)g, qh_signmask4(s8));
+            b[2 * l + 1] = (int)qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
+        }
+        sc = 2 * (int)(a1 >> 28) + 1;
+    }
 };
 
 template <class F>
@@ -158,13 +227,21 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
     constexpr int NV = EPL / 4;                  // float4 per lane
     static_assert(NT == 2 || NT == 4 || NT == 8 || NT == 16, "NT");
     using X = XL<NT>;
-    __shared__ __align__(16) unsigned char lds[W * TILE + W * X::BYTES + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4];
+    constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
+    __shared__ __align__(16) unsigned char lds[W * TILE + W * X::BYTES + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4 +
+                                               GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
     unsigned char* wl = lds + w * TILE;
     unsigned char* xl = lds + W * TILE + w * X::BYTES;
     float* red = reinterpret_cast<float*>(lds + W * TILE + W * X::BYTES);
     float* res = red + W * NT * 32;
+    unsigned char* gridl = reinterpret_cast<unsigned char*>(res + QG_MAXT * NT * 32);
+    if constexpr (F::GRID != 0) {
+        const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
+        for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
+        __syncthreads();
+    }
     const QhBuf wb = qh_buf(Wt, wbytes);
     const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
     const int ntiles = (out_dim + 31) / 32;
@@ -316,7 +393,28 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         int acc2[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) acc[j] = acc2[j] = 0;
-        if constexpr (!IsQ6<F>::value) {
+        if constexpr (F::KIND == 1) {
+            auto sub = [&](auto KC) {
+                constexpr int K = decltype(KC)::value;
+                qh_i32x4 b;
+                int sc;
+                F::template bop<K>(wrow, hh, gridl, b, sc);
+                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 32 * K);
+                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(sc, d[j]);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            sub(std::integral_constant<int, 0>{});
+            sub(std::integral_constant<int, 1>{});
+            sub(std::integral_constant<int, 2>{});
+            sub(std::integral_constant<int, 3>{});
+            sub(std::integral_constant<int, 4>{});
+            sub(std::integral_constant<int, 5>{});
+            sub(std::integral_constant<int, 6>{});
+            sub(std::integral_constant<int, 7>{});
+        } else if constexpr (!IsQ6<F>::value) {
             auto pair = [&](auto PC) {
                 constexpr int P = decltype(PC)::value;
                 qh_i32x4 b0, b1;
@@ -496,7 +594,8 @@ static int qh_mmq_waves_env() {
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                          hipStream_t st) {
     if (in_dim % 256 || ((uintptr_t)x & 15u) || n < 2) return hipErrorNotSupported;
-    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K) return hipErrorNotSupported;
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
+        return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     for (int t0 = 0; t0 < n; t0 += 16) {
         const int nt = n - t0 < 16 ? n - t0 : 16;
@@ -516,6 +615,8 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
     else { QG_NT(F, 16) }
         if (type == QT_Q4_K) { QG_CASE(GQ4K) }
         else if (type == QT_Q5_K) { QG_CASE(GQ5K) }
+        else if (type == QT_IQ3_S) { QG_CASE(GIQ3S) }
+        else if (type == QT_IQ2_XXS) { QG_CASE(GIQ2XXS) }
         else { QG_CASE(GQ6K) }
 #undef QG_CASE
 #undef QG_NT

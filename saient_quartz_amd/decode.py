@@ -82,3 +82,45 @@ class DecodeStep:
                 self._mm(t, w, self.y[name], o, i, n, sp)
         t, w, o, i = self.head
         self._mm(t, w, self.logits, o, i, n, sp)
+
+
+class MoeLayer:
+    """Mixtral-8x7B-shaped MoE expert layer: 8 experts,
+    each gate/up 14336x4096 and down 4096x14336 in one IQ type, 16 tokens
+    gathered per expert (top-2 routing of 64 tokens).  A step runs every
+    expert's three GEMMs (n = 16 tokens) through hip_gemm_async, as the
+    reference's per-expert loop does (src/cuda.rs:667-798).  The router, the
+    gather/scatter and swiglu are glue outside this library: the gathered
+    activations are fixed buffers."""
+
+    def __init__(self, ggml_type: int, experts: int = 8, tokens: int = 16, hidden: int = 4096, ffn: int = 14336,
+                 seed: int = 20261205):
+        self.t, self.E, self.n, self.h, self.f = ggml_type, experts, tokens, hidden, ffn
+        self.L = lib()
+        self.w = []
+        for e in range(experts):
+            self.w.append([synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e),
+                           synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e + 1),
+                           synth_device.weights(ggml_type, hidden, ffn, seed + 3 * e + 2)])
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed - 1)
+        self.x = torch.randn(experts, tokens, hidden, device="cuda", generator=g)
+        self.hbuf = torch.randn(experts, tokens, ffn, device="cuda", generator=g)
+        self.gate = torch.empty(experts, tokens, ffn, device="cuda")
+        self.up = torch.empty(experts, tokens, ffn, device="cuda")
+        self.down = torch.empty(experts, tokens, hidden, device="cuda")
+
+    def weight_bytes(self) -> int:
+        from . import type_size
+        return self.E * (2 * type_size(self.t, self.f * self.h) + type_size(self.t, self.h * self.f))
+
+    def issue(self, stream=None):
+        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        t, n, h, f = self.t, self.n, self.h, self.f
+        for e, (wg, wu, wd) in enumerate(self.w):
+            check("hip_gemm_async", self.L.hip_gemm_async(t, wg.data_ptr(), self.x[e].data_ptr(),
+                                                          self.gate[e].data_ptr(), h, f, n, sp))
+            check("hip_gemm_async", self.L.hip_gemm_async(t, wu.data_ptr(), self.x[e].data_ptr(),
+                                                          self.up[e].data_ptr(), h, f, n, sp))
+            check("hip_gemm_async", self.L.hip_gemm_async(t, wd.data_ptr(), self.hbuf[e].data_ptr(),
+                                                          self.down[e].data_ptr(), f, h, n, sp))

@@ -41,9 +41,27 @@ def q6k(out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
     return blk.reshape(-1)
 
 
+IQ2_XXS, IQ3_S = 16, 21
+_IQ_BYTES = {IQ2_XXS: 66, IQ3_S: 110}
+
+
+def iq(ggml_type: int, out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
+    """IQ2_XXS / IQ3_S: random grid indices, sign bits and scale nibbles,
+    f16 d ~ |N(0,0.01)| in bytes 0-1 of each block."""
+    g = _gen(seed)
+    nb = out_dim * in_dim // 256
+    bs = _IQ_BYTES[ggml_type]
+    blk = torch.randint(0, 256, (nb, bs), dtype=torch.uint8, device="cuda", generator=g)
+    d = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.01).half()
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    return blk.reshape(-1)
+
+
 def weights(ggml_type: int, out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
     if ggml_type == Q4_K:
         return q4k(out_dim, in_dim, seed)
     if ggml_type == Q6_K:
         return q6k(out_dim, in_dim, seed)
+    if ggml_type in _IQ_BYTES:
+        return iq(ggml_type, out_dim, in_dim, seed)
     raise ValueError(f"no device generator for ggml type {ggml_type}")

@@ -149,14 +149,14 @@ def test_gemm_vs_oracle(qh, oracle, t, n):
     assert cf.rel_l2(got, ref) < TOL
 
 
-# The matrix-core batched path (Q4_K, Q5_K, Q6_K): token counts that use each
+# The matrix-core batched path (Q4_K, Q5_K, Q6_K, IQ3_S, IQ2_XXS): token counts that use each
 # token-tile size (2, 4, 8, 16) and the chunking past 16; shapes with several K
 # chunks, a partial last row tile and more tiles than one workgroup keeps.
 MMQ_CASES = [(40, 4096, 2), (40, 4096, 3), (77, 4096, 5), (300, 14336, 8), (100, 4096, 11), (130, 2048, 16),
              (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4)]
 
 
-@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("t", [12, 13, 14, 21, 16])
 @pytest.mark.parametrize("case", MMQ_CASES, ids=lambda c: f"{c[0]}x{c[1]}n{c[2]}")
 def test_gemm_matrix_core(qh, oracle, t, case):
     out_dim, in_dim, n = case
