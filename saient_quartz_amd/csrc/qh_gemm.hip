@@ -201,40 +201,142 @@ struct IsQ6 { static constexpr bool value = false; };
 template <>
 struct IsQ6<GQ6K> { static constexpr bool value = true; };
 
-// ---------------------------------------------------------------- kernel
+// ---------------------------------------------------------------- x image
 
-// LDS per wavefront: x digits of one group for NT tokens -- plane 2t+m (digit m
-// of token t, 256 bytes) at PS (2t+m), sum digits of plane 2t+m at
-// SUMS + 16 (2t+m) (8 or 16 bytes used, the rest stays zero), 256 zero bytes, and
-// 2^-s / 2^-(s - SUMSH) per token.
-template <int NT>
-struct XL {
-    static constexpr int PS = 272;  // plane stride: 256 bytes + 16, conflict-free b128 reads over 16 rows
-    static constexpr int SUMS = 2 * PS * NT;
-    static constexpr int ZERO = SUMS + 32 * NT;
-    static constexpr int RS_ = ZERO + 256;
-    static constexpr int BYTES = RS_ + 8 * NT;
+// The x operand of one 256-element group for 16 token slots ("image"), written
+// once per call by qh_mmq_ximg and read by every workgroup with coalesced loads:
+// chunk c is the A operand of one MFMA, lane L's 16 bytes at 1024 c + 16 L
+// (lane L = row L % 32, k half L / 32 of the 32x32x32 MFMA).
+//   KIND 0 / 1 (one scale per 32 weights): chunk k < 8 = sub-block k, row 2t+m =
+//     digit m of token t; KIND 0 adds chunk 8, the sum digits of the 8
+//     sub-blocks (row 2t+m, k half 0, bytes 0..7).
+//   KIND 2 (Q6_K, scales per 16): chunk 8u+c = 32-weight chunk c for tokens
+//     8u..8u+7 (so <= 8 tokens need only chunks 0..7): row 2(t%8)+m takes k < 16, row 16 + 2(t%8)+m takes k >= 16, the
+//     other k half of each row is zero.
+// Then 16 bytes: the digit exponent s of each token slot (127: Inf/NaN seen).
+template <int KIND, bool SUMS>
+struct XImg {
+    static constexpr int CHUNKS = KIND == 2 ? 16 : (SUMS ? 9 : 8);
+    static constexpr int EXP = 1024 * CHUNKS;
+    static constexpr int BYTES = EXP + 256;  // per group
 };
+#define QG_MAX_GROUPS 256                     // in_dim <= 65536 on the matrix-core path
+#define QG_SCRATCH (QG_MAX_GROUPS * (16 * 1024 + 256))
+static __device__ __align__(256) unsigned char qh_mmq_scratch[QG_SCRATCH];
+
+// One workgroup (256 threads) per group: thread T digitises elements 16 (T%16)
+// .. +15 of token T/16 (zeros past n), building the image in LDS, then copies it
+// out.  Digits: fmaf(x, 2^s, 12615808) = 1.5 * 2^23 + 0x8080 + n with n =
+// round(x 2^s), |n| <= 2^14 (s = 14 - exponent of the token's max |x| over the
+// group), so the float's low bytes XOR 0x80 are the balanced digits of n.
+// Sums: exact integer sums of n over each sub-block, in units of 2^SUMSH.
+template <int KIND, bool SUMS, int SUMSH>
+__global__ __launch_bounds__(256) void qh_mmq_ximg(const float* __restrict__ x, unsigned char* __restrict__ img,
+                                                   int in_dim, int n) {
+    using XI = XImg<KIND, SUMS>;
+    __shared__ __align__(16) unsigned char im[XI::BYTES];
+    const int T = threadIdx.x, g = blockIdx.x;
+    const int t = T >> 4, p = T & 15;
+    for (int i = 16 * T; i < XI::BYTES; i += 16 * 256) *reinterpret_cast<qh_u32x4*>(im + i) = qh_u32x4{0, 0, 0, 0};
+    float4 v[4];
+    const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
+    const uint32_t off = t < n ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)g + 16u * p) : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qh_u32x4 u = qh_ld128(xb, off + 16u * i);
+        v[i] = float4{__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    // max over the 16 threads (one DPP row) of the token
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
+    int e = 0;
+    (void)frexpf(m, &e);
+    int s = m > 0.f ? 14 - e : 0;
+    s = s > 126 ? 126 : (s < -126 ? -126 : s);
+    const float scx = ldexpf(1.0f, s);
+    uint32_t a[16];
+    uint32_t hi_or = 0, sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a[4 * i + 0] = __float_as_uint(fmaf(v[i].x, scx, 12615808.0f));
+        a[4 * i + 1] = __float_as_uint(fmaf(v[i].y, scx, 12615808.0f));
+        a[4 * i + 2] = __float_as_uint(fmaf(v[i].z, scx, 12615808.0f));
+        a[4 * i + 3] = __float_as_uint(fmaf(v[i].w, scx, 12615808.0f));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        hi_or |= (a[i] >> 16) ^ 0x4B40u;  // nonzero iff a value was not finite (or out of range)
+        sum += a[i];
+    }
+    // 16 bytes of digit m, in element order
+    qh_u32x4 d0, d1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t t01 = __builtin_amdgcn_perm(a[4 * i + 1], a[4 * i], 0x05010400u);
+        const uint32_t t23 = __builtin_amdgcn_perm(a[4 * i + 3], a[4 * i + 2], 0x05010400u);
+        d0[i] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+        d1[i] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+    }
+    const int c32 = p >> 1, kh = p & 1;  // 32-element piece of the group, k half
+    if constexpr (KIND == 2) {
+        const int u = t >> 3, r = 16 * kh + 2 * (t & 7);
+        *reinterpret_cast<qh_u32x4*>(im + 1024 * (8 * u + c32) + 16 * (32 * kh + r)) = d0;
+        *reinterpret_cast<qh_u32x4*>(im + 1024 * (8 * u + c32) + 16 * (32 * kh + r + 1)) = d1;
+    } else {
+        *reinterpret_cast<qh_u32x4*>(im + 1024 * c32 + 16 * (32 * kh + 2 * t)) = d0;
+        *reinterpret_cast<qh_u32x4*>(im + 1024 * c32 + 16 * (32 * kh + 2 * t + 1)) = d1;
+    }
+    if constexpr (SUMS) {
+        // integer sum of n over the sub-block (this thread and its neighbour)
+        sum += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
+        if (kh == 0) {
+            const int sn = (int)(sum - 32u * 0x4B408080u);
+            const int ns = (sn + (1 << (SUMSH - 1))) >> SUMSH;
+            const uint32_t uu = (uint32_t)(ns + 0x8080);
+            im[1024 * 8 + 16 * (2 * t) + c32] = (unsigned char)((uu & 0xFFu) ^ 0x80u);
+            im[1024 * 8 + 16 * (2 * t + 1) + c32] = (unsigned char)(((uu >> 8) & 0xFFu) ^ 0x80u);
+        }
+    }
+    // the token's non-finite flag, over its 16 threads
+    uint32_t f = hi_or;
+    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0xB1, 0xF, 0xF, false);
+    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x4E, 0xF, 0xF, false);
+    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x141, 0xF, 0xF, false);
+    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x140, 0xF, 0xF, false);
+    __syncthreads();
+    if (p == 0) im[XI::EXP + t] = (unsigned char)(signed char)(f ? 127 : s);
+    __syncthreads();
+    unsigned char* dst = img + (size_t)g * XI::BYTES;
+    for (int i = 16 * T; i < XI::BYTES; i += 16 * 256)
+        *reinterpret_cast<qh_u32x4*>(dst + i) = *reinterpret_cast<const qh_u32x4*>(im + i);
+}
+
+// ---------------------------------------------------------------- kernel
 
 template <class F, int NT, int W>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt, uint32_t wbytes,
-                                                 const float* __restrict__ x, float* __restrict__ y, int out_dim,
-                                                 uint32_t row_bytes, int ngroups, int in_dim, int n, int ldy) {
+                                                 const unsigned char* __restrict__ img, float* __restrict__ y,
+                                                 int out_dim, uint32_t row_bytes, int ngroups, int n, int ldy) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte loads per lane per group
     constexpr int TILE = 32 * RS + 16;
-    constexpr int LPT = 64 / NT, EPL = 4 * NT;  // lanes per token, x elements per lane
-    constexpr int NV = EPL / 4;                  // float4 per lane
     static_assert(NT == 2 || NT == 4 || NT == 8 || NT == 16, "NT");
-    using X = XL<NT>;
+    using XI = XImg<F::KIND, F::SUMS>;
+    // Image chunks this kernel reads: Q6_K with <= 8 tokens needs only u = 0.
+    constexpr int NC = (F::KIND == 2) ? (NT > 8 ? 16 : 8) : XI::CHUNKS;
+    constexpr int XB = 1024 * NC;  // per-wavefront LDS x area
     constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
-    __shared__ __align__(16) unsigned char lds[W * TILE + W * X::BYTES + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4 +
-                                               GRIDB];
+    __shared__ __align__(16) unsigned char lds[W * TILE + W * XB + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4 + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
     unsigned char* wl = lds + w * TILE;
-    unsigned char* xl = lds + W * TILE + w * X::BYTES;
-    float* red = reinterpret_cast<float*>(lds + W * TILE + W * X::BYTES);
+    unsigned char* xl = lds + W * TILE + w * XB;
+    float* red = reinterpret_cast<float*>(lds + W * TILE + W * XB);
     float* res = red + W * NT * 32;
     unsigned char* gridl = reinterpret_cast<unsigned char*>(res + QG_MAXT * NT * 32);
     if constexpr (F::GRID != 0) {
@@ -243,14 +345,9 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         __syncthreads();
     }
     const QhBuf wb = qh_buf(Wt, wbytes);
-    const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
+    const QhBuf ib = qh_buf(img, (uint32_t)ngroups * XI::BYTES);
     const int ntiles = (out_dim + 31) / 32;
     const int nch = (ngroups + W - 1) / W;
-
-    // Zero this wavefront's x area once: sum-digit padding and the zero area are
-    // never written afterwards.
-    for (int i = lane * 16; i < X::BYTES; i += 64 * 16)
-        if (i + 16 <= X::BYTES) *reinterpret_cast<qh_u32x4*>(xl + i) = qh_u32x4{0, 0, 0, 0};
 
     // Weight slices of this lane: row rr[h] of the tile, byte offset goff[h] from
     // the tile's first row, LDS offset soff[h] (lanes past 32 * CH: spare bytes).
@@ -263,8 +360,6 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
     }
-    // x slice of this lane: token tx, elements EPL * part .. of the group.
-    const int tx = lane / LPT, part = lane % LPT;
 
     auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
         const int g = ch * W + w;
@@ -275,90 +370,21 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             wo[h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)g);
         }
     };
-    auto load_x = [&](int ch, float4* xo) {
+    // The group's image chunks (1 KB each, coalesced) and its exponents.
+    // Lanes whose A row holds a token slot >= NT load nothing (out of range: zeros).
+    const bool xrow = F::KIND == 2 ? ((R & 15) >> 1) < NT : (R >> 1) < NT;
+    auto load_x = [&](int ch, qh_u32x4* xo, qh_u32x4& eo) {
         const int g = ch * W + w;
-        const uint32_t off = (g < ngroups && tx < n)
-                                 ? 4u * ((uint32_t)tx * (uint32_t)in_dim + 256u * (uint32_t)g + (uint32_t)(EPL * part))
-                                 : 0x80000000u;
+        const uint32_t base = g < ngroups ? (uint32_t)g * XI::BYTES : 0x80000000u;
+        const uint32_t lb = xrow ? base + 16u * lane : 0x80000000u;
 #pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const qh_u32x4 v = qh_ld128(xb, off + 16u * i);
-            xo[i] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        }
+        for (int c = 0; c < NC; c++) xo[c] = qh_ld128(ib, lb + 1024u * c);
+        eo = qh_ld128(ib, base + XI::EXP);
     };
-    // x -> two digit planes per token + digitised sums over SUMK.
-    //   fmaf(x, 2^s, 12615808) = 1.5 * 2^23 + 0x8080 + n (n = round(x 2^s), |n| <=
-    //   2^14), so the float's low 16 bits are n + 0x8080 and its bytes XOR 0x80
-    //   are the balanced digits; the sums are exact integer sums of those n (sum
-    //   of the float bits minus k * 0x4B408080, mod 2^32).
-    //   A token whose chunk holds Inf or NaN (max|x| is Inf, or a bit sum falls
-    //   outside the range finite values allow) gets 2^-s = NaN, so exactly its
-    //   outputs are NaN, as in the reference's f32 dot.
-    auto prep_x = [&](const float4* xv) {
-        float m = 0.f;
+    // Registers -> this wavefront's LDS x area (each lane its own 16 bytes).
+    auto stage_x = [&](const qh_u32x4* xi) {
 #pragma unroll
-        for (int i = 0; i < NV; i++) {
-            // v_max3_f32 with |.| source modifiers: one instruction per two elements
-            // (NaN is caught by the bit-sum check below, not by the max).
-            __asm__("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(m) : "v"(xv[i].x), "v"(xv[i].y));
-            __asm__("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(m) : "v"(xv[i].z), "v"(xv[i].w));
-        }
-#pragma unroll
-        for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        int e = 0;
-        (void)frexpf(m, &e);
-        // |x| * 2^s <= 2^14: even after rounding, n + 0x8080 stays below 2^16.
-        int s = m > 0.f ? 14 - e : 0;
-        s = s > 126 ? 126 : (s < -126 ? -126 : s);
-        const float scx = ldexpf(1.0f, s);
-        const float magic = 12615808.0f;  // 0x4B408080
-        unsigned char* p0 = xl + X::PS * (2 * tx) + EPL * part;
-        constexpr int PIECE = F::SUMS ? F::SUMK : EPL;  // elements per checked bit sum
-        constexpr int PL = PIECE < EPL ? PIECE : EPL;    // of which in this lane
-        uint32_t psum = 0;
-        bool nonfinite = !(m <= 3.0e38f);
-        auto piece_done = [&](int j) {
-            uint32_t ps = psum;
-            if constexpr (PIECE > EPL) {
-#pragma unroll
-                for (int o = 1; o < PIECE / EPL; o <<= 1) ps += (uint32_t)__shfl_xor((int)ps, o);
-            }
-            const int sn = (int)(ps - (uint32_t)PIECE * 0x4B408080u);
-            nonfinite |= sn > PIECE * 16384 || sn < -PIECE * 16384;
-            if constexpr (F::SUMS) {
-                if (PIECE <= EPL || (part % (PIECE / EPL)) == 0) {
-                    // sum of n in units of 2^SUMSH (|result| <= 2^14)
-                    const int ns = (sn + (1 << (F::SUMSH - 1))) >> F::SUMSH;
-                    const uint32_t u = (uint32_t)(ns + 0x8080);
-                    xl[X::SUMS + 16 * (2 * tx) + j] = (unsigned char)((u & 0xFFu) ^ 0x80u);
-                    xl[X::SUMS + 16 * (2 * tx + 1) + j] = (unsigned char)(((u >> 8) & 0xFFu) ^ 0x80u);
-                }
-            }
-            psum = 0;
-        };
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const float4 v = xv[i];
-            const uint32_t a0 = __float_as_uint(fmaf(v.x, scx, magic));
-            const uint32_t a1 = __float_as_uint(fmaf(v.y, scx, magic));
-            const uint32_t a2 = __float_as_uint(fmaf(v.z, scx, magic));
-            const uint32_t a3 = __float_as_uint(fmaf(v.w, scx, magic));
-            const uint32_t t01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
-            const uint32_t t23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
-            *reinterpret_cast<uint32_t*>(p0 + 4 * i) = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
-            *reinterpret_cast<uint32_t*>(p0 + X::PS + 4 * i) =
-                __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
-            psum += a0 + a1 + a2 + a3;
-            if ((4 * i + 4) % PL == 0) piece_done((EPL * part + 4 * i) / PIECE);
-        }
-        // every lane of the token agrees on the flag
-        int nf = nonfinite ? 1 : 0;
-#pragma unroll
-        for (int o = 1; o < LPT; o <<= 1) nf |= __shfl_xor(nf, o);
-        if (part == 0) {
-            reinterpret_cast<float*>(xl + X::RS_)[tx] = nf ? __builtin_nanf("") : ldexpf(1.0f, -s);
-            reinterpret_cast<float*>(xl + X::RS_)[NT + tx] = ldexpf(1.0f, F::SUMSH - s);
-        }
+        for (int c = 0; c < NC; c++) *reinterpret_cast<qh_u32x4*>(xl + 1024 * c + 16 * lane) = xi[c];
     };
     auto stage = [&](const qh_u32x4* wr) {
 #pragma unroll
@@ -374,21 +400,10 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
 #pragma unroll
     for (int i = 0; i < 8; i++) tot[i] = 0.f;
     const unsigned char* wrow = wl + R * RS;
-    // A operand offsets.  Main (Q4_K/Q5_K): plane R (token R/2, digit R%2).
-    const uint32_t aoffm = (R >> 1) < NT ? (uint32_t)X::PS * R + 16u * hh : (uint32_t)X::ZERO;
-    // Sums MFMA: plane R's sum digits in k = 0..15 (half 0 only).
-    const uint32_t aoffs = (hh == 0 && (R >> 1) < NT) ? (uint32_t)(X::SUMS + 16 * R) : (uint32_t)X::ZERO;
-    // Q6_K: MFMA u covers tokens 8u..8u+7; rows R < 16 take k < 16, rows >= 16 k >= 16.
-    uint32_t aoff6[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int t = 8 * u + ((R & 15) >> 1);
-        aoff6[u] = ((R >> 4) == hh && t < NT) ? (uint32_t)X::PS * (16 * u + (R & 15)) + 16u * hh : (uint32_t)X::ZERO;
-    }
+    const unsigned char* xa = xl + 16 * lane;  // this lane's A operands: chunk c at xa + 1024 c
 
-    auto compute = [&]() {
+    auto compute = [&](const qh_u32x4& ex) {
         const typename F::H hd = F::hdr(wrow);
-        const float* rsv = reinterpret_cast<const float*>(xl + X::RS_);
         int acc[16];
         int acc2[16];
 #pragma unroll
@@ -399,7 +414,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 qh_i32x4 b;
                 int sc;
                 F::template bop<K>(wrow, hh, gridl, b, sc);
-                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 32 * K);
+                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * K);
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
@@ -414,13 +429,13 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             sub(std::integral_constant<int, 5>{});
             sub(std::integral_constant<int, 6>{});
             sub(std::integral_constant<int, 7>{});
-        } else if constexpr (!IsQ6<F>::value) {
+        } else if constexpr (F::KIND == 0) {
             auto pair = [&](auto PC) {
                 constexpr int P = decltype(PC)::value;
                 qh_i32x4 b0, b1;
                 F::template bpair<P>(wrow, hh, b0, b1);
-                const qh_i32x4 a0 = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 64 * P);
-                const qh_i32x4 a1 = *reinterpret_cast<const qh_i32x4*>(xl + aoffm + 64 * P + 32);
+                const qh_i32x4 a0 = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (2 * P));
+                const qh_i32x4 a1 = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (2 * P + 1));
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 const qh_i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
                 const int s0 = F::template scl<2 * P>(hd);
@@ -444,13 +459,13 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 const int slo = F::template scl<2 * C>(hd), shi = F::template scl<2 * C + 1>(hd);
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 {
-                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoff6[0] + 32 * C);
+                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * C);
                     const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
                     for (int j = 0; j < 8; j++) acc[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
                 }
                 if constexpr (NT > 8) {
-                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xl + aoff6[1] + 32 * C);
+                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (8 + C));
                     const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
                     for (int j = 0; j < 8; j++) acc2[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
@@ -469,51 +484,52 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         // sums MFMA: the mins (Q4_K/Q5_K)
         qh_i32x16 dm = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
         if constexpr (F::SUMS) {
-            const qh_i32x4 as = *reinterpret_cast<const qh_i32x4*>(xl + aoffs);
+            const qh_i32x4 as = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * 8);
             dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(as, F::bmin(wrow, hd, hh), dm, 0, 0, 0);
         }
-        // finish: slot (q, r) = token 4q + 2hh + r
+        // finish: slot (q, r) = token 4q + 2hh + r, exponent byte t of the image
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                const int t = 4 * q + 2 * hh + r;
                 if (4 * q >= NT) continue;  // slot beyond the tokens for both lane halves
+                const int t = 4 * q + 2 * hh + r;
+                const int se = ((int)(ex[t >> 2] << (24 - 8 * (t & 3)))) >> 24;
+                const float rs = se == 127 ? __builtin_nanf("") : ldexpf(1.0f, -se);
                 int i0, i1;
-                if constexpr (!IsQ6<F>::value) {
+                if constexpr (F::KIND != 2) {
                     i0 = acc[4 * q + 2 * r];
                     i1 = acc[4 * q + 2 * r + 1];
                 } else {
                     // Q6_K: MFMA u = q/2 holds slot q in register 4 (q%2) + 2r + m
-                    const int* a = (q < 2) ? acc : acc2;
-                    i0 = a[4 * (q & 1) + 2 * r];
-                    i1 = a[4 * (q & 1) + 2 * r + 1];
+                    const int* ap = (q < 2) ? acc : acc2;
+                    i0 = ap[4 * (q & 1) + 2 * r];
+                    i1 = ap[4 * (q & 1) + 2 * r + 1];
                 }
                 const float P = fmaf((float)i1, 256.0f, (float)i0);
-                const int tt = t < NT ? t : 0;
                 if constexpr (F::SUMS) {
                     const float Pm = fmaf((float)dm[4 * q + 2 * r + 1], 256.0f, (float)dm[4 * q + 2 * r]);
-                    tot[2 * q + r] += fmaf(hd.d * P, rsv[tt], -hd.dm * Pm * rsv[NT + tt]);
+                    tot[2 * q + r] += (hd.d * P - hd.dm * Pm * (float)(1 << F::SUMSH)) * rs;
                 } else {
-                    tot[2 * q + r] += hd.d * P * rsv[tt];
+                    tot[2 * q + r] += hd.d * P * rs;
                 }
             }
     };
 
     int tile = blockIdx.x, ch = 0, done = 0;
     if (tile >= ntiles) return;  // uniform over the workgroup
-    qh_u32x4 wr[NH];
-    float4 xv[NV];
-    load_x(0, xv);
+    qh_u32x4 wr[NH], xr[NC], er;
+    load_x(0, xr, er);
     load_w(tile, 0, wr);
     for (;;) {
-        prep_x(xv);
+        const qh_u32x4 ex = er;
+        stage_x(xr);
         int ntile = tile, nc = ch + 1;
         if (nc == nch) { nc = 0; ntile += gridDim.x; }
-        load_x(nc, xv);  // next item's x (L2-resident), in flight during the compute
+        load_x(nc, xr, er);  // next item's x image (L2-resident), in flight during the compute
         stage(wr);
         load_w(ntile, nc, wr);  // past the last tile: all offsets out of range, no traffic
-        compute();
+        compute(ex);
         if (nc == 0) {
             // Tile finished: lanes hold (token slot, weight row R); sum the wavefronts.
 #pragma unroll
@@ -548,8 +564,21 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
     }
 }
 
+// Device address of the x-image scratch, per device (hipGetSymbolAddress once).
+static unsigned char* qh_mmq_scratch_ptr() {
+    static unsigned char* ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(qh_mmq_scratch)) != hipSuccess) return nullptr;
+        ptrs[dev] = static_cast<unsigned char*>(p);
+    }
+    return ptrs[dev];
+}
+
 template <class F, int NT, int W>
-static hipError_t launch_mmq(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim, int n,
+static hipError_t launch_mmq(const uint8_t* Wt, const unsigned char* img, float* y, int in_dim, int out_dim, int n,
                              uint32_t row_bytes, hipStream_t st) {
     static int resident = 0;
     if (!resident) {
@@ -563,7 +592,7 @@ static hipError_t launch_mmq(const uint8_t* Wt, const float* x, float* y, int in
     }
     const int ngroups = in_dim / 256;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
-    if (max_rows < 32 || (int64_t)n * in_dim * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    if (max_rows < 32) return hipErrorNotSupported;
     for (int64_t r0 = 0; r0 < out_dim; r0 += max_rows) {
         const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
         const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
@@ -572,12 +601,20 @@ static hipError_t launch_mmq(const uint8_t* Wt, const float* x, float* y, int in
         if ((ntiles + grid - 1) / grid > QG_MAXT) grid = (ntiles + QG_MAXT - 1) / QG_MAXT;
         // y rows r0.. of every token: y + r0 with the token stride out_dim.
         hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups, in_dim, n,
-                           out_dim);
+                           Wt + (size_t)r0 * row_bytes, wbytes, img, y + r0, rows, row_bytes, ngroups, n, out_dim);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+template <class F, int NT>
+static hipError_t launch_mmq_w(bool w8, const uint8_t* W, const unsigned char* img, float* y, int in_dim,
+                               int out_dim, int n, uint32_t row_bytes, hipStream_t st) {
+    if constexpr (F::KIND != 2) {
+        if (w8) return launch_mmq<F, NT, 8>(W, img, y, in_dim, out_dim, n, row_bytes, st);
+    }
+    return launch_mmq<F, NT, 4>(W, img, y, in_dim, out_dim, n, row_bytes, st);
 }
 
 // QUARTZ_HIP_MMQ_WAVES=4|8 forces the workgroup size (tuning).
@@ -590,26 +627,39 @@ static int qh_mmq_waves_env() {
 }
 
 // Batched tokens on the matrix cores; hipErrorNotSupported when the type/shape
-// has no kernel here.  Tokens go in chunks of up to 16 (one weight pass each).
+// has no kernel here.  Tokens go in chunks of up to 16 (one weight pass each);
+// per chunk, qh_mmq_ximg writes the x image to the library's device scratch and
+// qh_mmq reads it.  The scratch is one array per device: calls that overlap on
+// one device (different streams) must be serialised by the caller.
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                          hipStream_t st) {
-    if (in_dim % 256 || ((uintptr_t)x & 15u) || n < 2) return hipErrorNotSupported;
+    if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || n < 2) return hipErrorNotSupported;
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;
+    if ((int64_t)n * in_dim * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    unsigned char* img = qh_mmq_scratch_ptr();
+    if (!img) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    const int ngroups = in_dim / 256;
     for (int t0 = 0; t0 < n; t0 += 16) {
         const int nt = n - t0 < 16 ? n - t0 : 16;
         const float* xs = x + (size_t)t0 * in_dim;
         float* ys = y + (size_t)t0 * out_dim;
         hipError_t e;
+        if (type == QT_Q6_K)
+            hipLaunchKernelGGL((qh_mmq_ximg<2, false, 4>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
+        else if (type == QT_IQ3_S || type == QT_IQ2_XXS)
+            hipLaunchKernelGGL((qh_mmq_ximg<1, false, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
+        else
+            hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
         // 8 wavefronts per workgroup when the row tiles alone give few workgroups
         // (measured faster for Q4_K/Q5_K at 4096 rows); Q6_K's 16-token kernel
         // does not fit 8 wavefronts' registers.
         const bool w8 = qh_mmq_waves_env() == 8 ||
                         (qh_mmq_waves_env() != 4 && type != QT_Q6_K && (out_dim + 31) / 32 < 256);
-#define QG_NT(F, NT_)                                                                                 \
-    e = w8 ? launch_mmq<F, NT_, 8>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st)                     \
-           : launch_mmq<F, NT_, 4>(W, xs, ys, in_dim, out_dim, nt, row_bytes, st);
+#define QG_NT(F, NT_) e = launch_mmq_w<F, NT_>(w8, W, img, ys, in_dim, out_dim, nt, row_bytes, st);
 #define QG_CASE(F)                                                                                   \
     if (nt <= 2) { QG_NT(F, 2) } else if (nt <= 4) { QG_NT(F, 4) } else if (nt <= 8) { QG_NT(F, 8) } \
     else { QG_NT(F, 16) }
@@ -622,5 +672,6 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 #undef QG_NT
         if (e != hipSuccess) return e;
     }
+    (void)ngroups;
     return hipSuccess;
 }
