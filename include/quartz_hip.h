@@ -19,7 +19,10 @@
  * y is overwritten, never accumulated.  Buffers are caller-owned device memory;
  * no entry point allocates device memory.  Calls on one stream are ordered; the
  * library keeps no per-call host state and is safe to call from several host
- * threads on distinct streams.
+ * threads on distinct streams, with one exception: hip_gemm / hip_gemm_async with
+ * n >= 2 on Q4_K, Q5_K, Q6_K, IQ3_S or IQ2_XXS stage the digitised activations in
+ * a static device array (4.2 MB, one per device), so such calls that overlap on
+ * one device must be serialised by the caller (e.g. one stream per device).
  */
 #ifndef QUARTZ_HIP_H
 #define QUARTZ_HIP_H
@@ -51,7 +54,9 @@ int hip_gemv_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, 
                    int out_dim, void* stream);
 
 /* Y[t][j] = sum_k W[j,k] X[t][k] for t < n (token-major).  GPU counterpart of
- * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv. */
+ * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv.  For n >= 2 the
+ * matrix-core path reads the weights once per 16 tokens (see the note above on
+ * its device scratch); results are within 2e-4 relative L2 per token. */
 int hip_gemm(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim, int out_dim,
              int n);
 int hip_gemm_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
