@@ -160,6 +160,12 @@ struct M16Q6K {
     static QH_DEV int mn(const H& h, int kg) { return scl<S>(h, kg); }
 };
 
+// 16-row tiles of the same formats (3 loads per lane and group instead of 2):
+// chosen when they spread the tiles more evenly over the CUs (4096 rows = 256
+// tiles = one per CU).
+struct M16Q4K16 : M16Q4K { static constexpr int ROWS = 16; };
+struct M16Q5K16 : M16Q5K { static constexpr int ROWS = 16; };
+
 // ---------------------------------------------------------------- kernel
 
 QH_DEV float qh_dpp_max(float m) {
@@ -446,14 +452,40 @@ static hipError_t dispatch_mmv16(const uint8_t* W, const float* x, float* y, int
     }
 }
 
+// Tile height: the default ROWS or 16, whichever gives the smaller
+// rows-per-tile x tiles-per-CU (QUARTZ_HIP_MMV16_ROWS=16|0 forces it, tuning).
+static bool qh_rows16_better(int rows, int out_dim) {
+    static const int env = [] {
+        const char* e = getenv("QUARTZ_HIP_MMV16_ROWS");
+        return e ? atoi(e) : -1;
+    }();
+    if (env >= 0) return env == 16;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+                  ? prop.multiProcessorCount
+                  : 256;
+    }
+    const int64_t ra = ((int64_t)out_dim + rows - 1) / rows, rb = ((int64_t)out_dim + 15) / 16;
+    return ((rb + cus - 1) / cus) * 16 < ((ra + cus - 1) / cus) * rows;
+}
+
 // Returns hipErrorNotSupported when the type/shape has no kernel here.
 hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                            hipStream_t st) {
     if (in_dim % 256 || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     switch (type) {
-        case QT_Q4_K: return dispatch_mmv16<M16Q4K>(W, x, y, in_dim, out_dim, row_bytes, st);
-        case QT_Q5_K: return dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q4_K:
+            return qh_rows16_better(M16Q4K::ROWS, out_dim)
+                       ? dispatch_mmv16<M16Q4K16>(W, x, y, in_dim, out_dim, row_bytes, st)
+                       : dispatch_mmv16<M16Q4K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q5_K:
+            return qh_rows16_better(M16Q5K::ROWS, out_dim)
+                       ? dispatch_mmv16<M16Q5K16>(W, x, y, in_dim, out_dim, row_bytes, st)
+                       : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
         default: return hipErrorNotSupported;
     }
