@@ -80,8 +80,8 @@ def test_gemv_fallback_shapes(qh, oracle, t, in_dim):
 
 # Shapes that give the persistent matrix-core kernel several row tiles per
 # workgroup (14336 rows), the tiles-per-workgroup cap (200000 rows), a partial
-# last tile and multi-chunk K (14336).
-BIG_SHAPES = [(14336, 4096), (4101, 14336), (200003, 256)]
+# last tile, multi-chunk K (14336) and the 16-row tiles chosen for 4096 rows.
+BIG_SHAPES = [(14336, 4096), (4101, 14336), (200003, 256), (4096, 4096), (4096, 14336)]
 
 
 @pytest.mark.parametrize("t", [12, 13, 14])
