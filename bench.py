@@ -156,8 +156,10 @@ def main():
 def decode_leg(torch, reps):
     """Llama-3-8B-shaped Q4_K_M decode step: the 225
     weight GEMVs of one step (32 layers x 7 + head) captured in one HIP graph,
-    timed over `reps` replays, for N = 1, 4, 16 tokens.  Weight streaming only:
-    the glue kernels between GEMVs are not part of this library yet."""
+    timed over `reps` replays, for N = 1, 4, 16 tokens.  At N = 1 the q+k and
+    gate+up projections go out as one hip_gemv_multi launch each ("n1"; "n1_unfused"
+    is one launch per matrix).  Weight streaming only: the glue kernels between
+    GEMVs are not part of this library yet."""
     from saient_quartz_amd.decode import DecodeStep, Shape
 
     shape = Shape()
@@ -166,12 +168,12 @@ def decode_leg(torch, reps):
     out = {"workload": "Llama-3-8B-shaped Q4_K_M decode step, weight GEMVs only (32 layers x q,k,v,o,gate,up,down "
                        "+ Q6_K head), random-init weights, synthetic activations",
            "weight_bytes": wbytes, "roofline_tok_s_n1": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)}
-    for n in (1, 4, 16):
+    for n, fuse in ((1, False), (1, True), (4, True), (16, True)):
         g = torch.cuda.CUDAGraph()
-        step.issue(n)  # eager warm-up (first-call device queries happen outside capture)
+        step.issue(n, fuse=fuse)  # eager warm-up (first-call device queries happen outside capture)
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
-            step.issue(n)
+            step.issue(n, fuse=fuse)
         g.replay()
         torch.cuda.synchronize()
         t0 = torch.cuda.Event(enable_timing=True)
@@ -182,7 +184,7 @@ def decode_leg(torch, reps):
         t1.record()
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / reps
-        out[f"n{n}"] = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
+        out[f"n{n}" + ("" if fuse or n > 1 else "_unfused")] = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
                         "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
                         "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
         del g

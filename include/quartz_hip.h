@@ -53,6 +53,17 @@ int hip_gemv(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float*
 int hip_gemv_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
                    int out_dim, void* stream);
 
+/* y[k] = W[k] x for k < count (1..4): several GEMVs that share x, the type and
+ * in_dim (a layer's q and k projections, or gate and up) in one launch.  W, y and
+ * out_dims are host arrays of count device pointers / row counts.  Each y[k] is
+ * bit-identical to hip_gemv(type, W[k], x, y[k], in_dim, out_dims[k]).  No
+ * counterpart in the reference, which calls cuda_gemv once per matrix
+ * (src/cuda.rs:556-562, :773-788); this is the decode-step launch fusion. */
+int hip_gemv_multi(uint32_t ggml_type, int count, const uint8_t* const* W, float* const* y, const int* out_dims,
+                   const float* d_x, int in_dim);
+int hip_gemv_multi_async(uint32_t ggml_type, int count, const uint8_t* const* W, float* const* y,
+                         const int* out_dims, const float* d_x, int in_dim, void* stream);
+
 /* Y[t][j] = sum_k W[j,k] X[t][k] for t < n (token-major).  GPU counterpart of
  * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv.  For n >= 2 the
  * matrix-core path reads the weights once per 16 tokens (see the note above on

@@ -86,6 +86,42 @@ int hip_gemv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_d
     return hip_gemv_async(type, W, x, y, in_dim, out_dim, nullptr);
 }
 
+int hip_gemv_multi_async(uint32_t type, int count, const uint8_t* const* W, float* const* y, const int* out_dims,
+                         const float* x, int in_dim, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 1 || count > 4 || !W || !y || !out_dims) return QH_ERR_RANGE;
+    const int qk = qh_block_elems(type);
+    if (qk == 0) {
+        int rc = QH_ERR_TYPE;
+        for (int k = 0; k < count; k++)
+            rc = qh_unknown_type("hip_gemv_multi", type, out_dims[k] > 0 ? y[k] : nullptr,
+                                 (size_t)(out_dims[k] > 0 ? out_dims[k] : 0), st);
+        return rc;
+    }
+    for (int k = 0; k < count; k++) {
+        int rc = qh_check_dims(type, in_dim, out_dims[k]);
+        if (rc) return rc;
+        if (out_dims[k] > 0 && (!W[k] || !y[k])) return QH_ERR_NULL;
+    }
+    if (!x) return QH_ERR_NULL;
+    if (!qh_force_valu()) {
+        hipError_t e = qh_launch_mmv16_multi(type, W, y, out_dims, count, x, in_dim, st);
+        if (e == hipSuccess) return QH_OK;
+        if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemv_multi");
+    }
+    // no fused kernel for this type/shape: one launch per matrix
+    for (int k = 0; k < count; k++) {
+        int rc = hip_gemv_async(type, W[k], x, y[k], in_dim, out_dims[k], stream);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
+int hip_gemv_multi(uint32_t type, int count, const uint8_t* const* W, float* const* y, const int* out_dims,
+                   const float* x, int in_dim) {
+    return hip_gemv_multi_async(type, count, W, y, out_dims, x, in_dim, nullptr);
+}
+
 int hip_gemm_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                    void* stream) {
     hipStream_t st = (hipStream_t)stream;

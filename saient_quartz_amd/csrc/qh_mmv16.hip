@@ -22,6 +22,8 @@
 //
 // Reference counterpart: the warp-per-row cuda_gemv kernels of
 // src/cuda_kernels.cu:1046-1077 (one f32 FMA per weight).
+#include <climits>
+
 #include "qh_formats.h"
 #include "qh_internal.h"
 
@@ -183,23 +185,43 @@ QH_DEV float qh_dpp_max(float m) {
 // loads of the next item are issued before the current one is computed, so every
 // wavefront keeps one item of loads in flight for the whole kernel.  When K fits
 // one chunk (X1: W * GPW >= in_dim / 256), x is digitised once per workgroup.
-template <class F, int W, int GPW, bool X1>
-__global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ Wt, uint32_t wbytes,
-                                                   const float* __restrict__ x, float* __restrict__ y, int out_dim,
-                                                   uint32_t row_bytes, int ngroups) {
+// Up to QH_MULTI weight matrices sharing x, type and in_dim, computed in one
+// launch: their row tiles form one index space (matrix m owns tiles tstart[m] ..
+// tstart[m+1]-1); a single GEMV is the one-matrix case.
+#define QH_MULTI 4
+struct QhMats {
+    const uint8_t* w[QH_MULTI];
+    float* y[QH_MULTI];
+    uint32_t wbytes[QH_MULTI];  // record count of each matrix's buffer range
+    int rows[QH_MULTI];
+    int tstart[QH_MULTI + 1];   // tstart[nm] = total tiles; entries past nm are INT_MAX
+};
+
+template <class F, int W, int GPW, bool X1, bool MULTI>
+__global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float* __restrict__ x, uint32_t row_bytes,
+                                                   int ngroups) {
     constexpr int ROWS = F::ROWS, CH = F::CH;
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
     static_assert(ROWS <= 16 && 16 * CH < QH_RS, "tile shape");
     constexpr int TILE = ROWS * QH_RS + 16;  // staging tile of one group + 16 spare bytes
     __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * W * 16 * 4 + QH_MAXT * 16 * 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const QhBuf wb = qh_buf(Wt, wbytes);
     const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
     unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
     unsigned char* xl = lds + W * GPW * TILE + w * (GPW * QH_XG);
     float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
     float* res = red + 2 * W * 16;  // finished rows of this workgroup's tiles
-    const int ntiles = (out_dim + ROWS - 1) / ROWS;
+    const int ntiles = mm.tstart[QH_MULTI];
+    // matrix of a (workgroup-uniform) tile index
+    auto mat_of = [&](int tile) {
+        int m = 0;
+        if constexpr (MULTI) {
+#pragma unroll
+            for (int k = 1; k < QH_MULTI; k++) m += tile >= mm.tstart[k];
+        }
+        return m;
+    };
+    const QhBuf wb0 = qh_buf(mm.w[0], mm.wbytes[0]);  // the one-matrix case, hoisted
     const int nch = (ngroups + W * GPW - 1) / (W * GPW);
 
     // Slices of this lane in a tile: row rr[h], byte offset goff[h] from the
@@ -233,6 +255,10 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ W
     // has no branches.
     auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
         const int g0 = ch * (W * GPW) + w * GPW;
+        const int m = mat_of(tile);
+        const QhBuf wb = MULTI ? qh_buf(mm.w[m], mm.wbytes[m]) : wb0;
+        const int out_dim = mm.rows[m];
+        if (MULTI) tile -= mm.tstart[m];
         const uint32_t base = (uint32_t)(tile * ROWS) * row_bytes;
 #pragma unroll
         for (int t = 0; t < GPW; t++)
@@ -382,40 +408,65 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const uint8_t* __restrict__ W
     }
     __syncthreads();
     for (int i = threadIdx.x; i < done * 16; i += 64 * W) {
-        const int row = (blockIdx.x + (i >> 4) * gridDim.x) * ROWS + (i & 15);
-        if ((i & 15) < ROWS && row < out_dim) y[row] = res[i];
+        const int tile = blockIdx.x + (i >> 4) * gridDim.x, m = mat_of(tile);
+        const int row = (tile - mm.tstart[m]) * ROWS + (i & 15);
+        if ((i & 15) < ROWS && row < mm.rows[m]) mm.y[m][row] = res[i];
     }
 }
 
+// nm matrices (each's weights < 2^31 bytes) in one launch.
 template <class F, int W, int GPW, bool X1>
-static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim,
-                               uint32_t row_bytes, hipStream_t st) {
+static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
+                                    const float* x, int in_dim, uint32_t row_bytes, hipStream_t st) {
     static int resident = 0;  // workgroups the device holds at once (per instantiation)
     if (!resident) {
         int dev = 0, per_cu = 0;
         hipDeviceProp_t prop;
         if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, GPW, X1>, 64 * W, 0) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, GPW, X1, false>, 64 * W, 0) !=
+                hipSuccess ||
             per_cu < 1)
             return hipErrorNotSupported;
         resident = per_cu * prop.multiProcessorCount;
     }
-    const int ngroups = in_dim / 256;
+    QhMats mm;
+    int tiles = 0;
+    for (int k = 0; k < QH_MULTI; k++) {
+        const bool on = k < nm;
+        mm.w[k] = on ? Ws[k] : nullptr;
+        mm.y[k] = on ? ys[k] : nullptr;
+        mm.rows[k] = on ? outs[k] : 0;
+        mm.wbytes[k] = on ? (uint32_t)(((uint64_t)outs[k] * row_bytes + 3) & ~(uint64_t)3) : 0;
+        mm.tstart[k] = on ? tiles : INT_MAX;
+        if (on) tiles += (outs[k] + F::ROWS - 1) / F::ROWS;
+    }
+    mm.tstart[QH_MULTI] = tiles;
+    if (tiles == 0) return hipSuccess;
+    // One workgroup per tile up to what the device holds at once (tiles go
+    // round-robin, so some workgroups take one more tile than others); more
+    // only when a workgroup would exceed QH_MAXT tiles.
+    int grid = tiles < resident ? tiles : resident;
+    if ((tiles + grid - 1) / grid > QH_MAXT) grid = (tiles + QH_MAXT - 1) / QH_MAXT;
+    if (nm > 1)
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
+                           row_bytes, in_dim / 256);
+    else
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, false>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
+                           row_bytes, in_dim / 256);
+    return hipGetLastError();
+}
+
+template <class F, int W, int GPW, bool X1>
+static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int in_dim, int out_dim,
+                               uint32_t row_bytes, hipStream_t st) {
     // Rows are processed in chunks whose weight bytes fit a 31-bit buffer range.
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / F::ROWS * F::ROWS;
     if (max_rows < F::ROWS) return hipErrorNotSupported;
     for (int64_t r0 = 0; r0 < out_dim; r0 += max_rows) {
         const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
-        const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
-        const int ntiles = (rows + F::ROWS - 1) / F::ROWS;
-        // One workgroup per tile up to what the device holds at once (tiles go
-        // round-robin, so some workgroups take one more tile than others); more
-        // only when a workgroup would exceed QH_MAXT tiles.
-        int grid = ntiles < resident ? ntiles : resident;
-        if ((ntiles + grid - 1) / grid > QH_MAXT) grid = (ntiles + QH_MAXT - 1) / QH_MAXT;
-        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           Wt + (size_t)r0 * row_bytes, wbytes, x, y + r0, rows, row_bytes, ngroups);
-        hipError_t e = hipGetLastError();
+        const uint8_t* w = Wt + (size_t)r0 * row_bytes;
+        float* yy = y + r0;
+        hipError_t e = launch_mmv16_mats<F, W, GPW, X1>(&w, &yy, &rows, 1, x, in_dim, row_bytes, st);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -487,6 +538,54 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
                        ? dispatch_mmv16<M16Q5K16>(W, x, y, in_dim, out_dim, row_bytes, st)
                        : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        default: return hipErrorNotSupported;
+    }
+}
+
+// Several GEMVs sharing x (same type and in_dim) in one launch; each matrix's
+// weights must fit a 31-bit buffer range.  hipErrorNotSupported otherwise.
+template <class F>
+static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm, const float* x,
+                              int in_dim, uint32_t row_bytes, hipStream_t st) {
+    int total = 0;
+    for (int k = 0; k < nm; k++) {
+        if ((int64_t)outs[k] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+        total += outs[k];
+    }
+    int v = qh_mmv16_variant_env();
+    if (v < 0) v = in_dim <= 4096 ? 4 : 10;
+    const bool x1w16 = in_dim <= 256 * 16, x1w8 = in_dim <= 256 * 8;
+    (void)total;
+    switch (v) {
+        case 4:
+            return x1w16 ? launch_mmv16_mats<F, 16, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
+                         : launch_mmv16_mats<F, 16, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+        case 10:
+            return x1w8 ? launch_mmv16_mats<F, 8, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
+                        : launch_mmv16_mats<F, 8, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+        case 2:
+            return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
+                                      : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
+                                 const float* x, int in_dim, hipStream_t st) {
+    if (nm < 1 || nm > QH_MULTI || in_dim % 256 || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    int total = 0;
+    for (int k = 0; k < nm; k++) total += outs[k];
+    switch (type) {
+        case QT_Q4_K:
+            return qh_rows16_better(M16Q4K::ROWS, total)
+                       ? multi_mmv16<M16Q4K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
+                       : multi_mmv16<M16Q4K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+        case QT_Q5_K:
+            return qh_rows16_better(M16Q5K::ROWS, total)
+                       ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
+                       : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
         default: return hipErrorNotSupported;
     }
 }

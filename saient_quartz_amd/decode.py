@@ -18,6 +18,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
+from .host import gemv_multi_async
 
 Q4_K, Q6_K = 12, 14
 
@@ -72,12 +73,27 @@ class DecodeStep:
             check("hip_gemm_async", self.L.hip_gemm_async(t, w.data_ptr(), x.data_ptr(), out.data_ptr(),
                                                           i, o, n, sp))
 
-    def issue(self, n: int = 1, stream=None):
-        """Enqueue one decode step's GEMVs for n tokens on `stream` (torch stream)."""
+    def issue(self, n: int = 1, stream=None, fuse: bool = True):
+        """Enqueue one decode step's GEMVs for n tokens on `stream` (torch stream).
+        With n = 1 and `fuse`, the projections that share x and type go out as one
+        hip_gemv_multi launch each: q+k (Q4_K) and gate+up (Q4_K)."""
         assert 1 <= n <= self.n_max
         sp = (stream or torch.cuda.current_stream()).cuda_stream
         names = [m[0] for m in self.shape.layer_mats()]
         for mats in self.layers:
+            by = dict(zip(names, mats))
+            if n == 1 and fuse:
+                for group in (("q", "k"), ("v",), ("o",), ("gate", "up"), ("down",)):
+                    if len(group) == 1:
+                        t, w, o, i = by[group[0]]
+                        self._mm(t, w, self.y[group[0]], o, i, n, sp)
+                        continue
+                    t, _, _, i = by[group[0]]
+                    x = self.x if i == self.shape.hidden else self.xf
+                    gemv_multi_async(self.L, t, [by[g][1].data_ptr() for g in group],
+                                     [self.y[g].data_ptr() for g in group], [by[g][2] for g in group],
+                                     x.data_ptr(), i, sp)
+                continue
             for name, (t, w, o, i) in zip(names, mats):
                 self._mm(t, w, self.y[name], o, i, n, sp)
         t, w, o, i = self.head

@@ -105,3 +105,13 @@ def verify_gemv_hip(x, data: np.ndarray, ggml_type: int, in_dim: int, out_dim: i
     buf = GpuBuf.upload(data)
     sc = GpuScratch(in_dim, out_dim)
     return sc.gemv(x, buf, ggml_type, in_dim, out_dim)
+
+
+def gemv_multi_async(L, ggml_type, w_ptrs, y_ptrs, out_dims, x_ptr, in_dim, stream_ptr):
+    """hip_gemv_multi_async with host arrays built from Python ints (device pointers)."""
+    import ctypes as C
+    k = len(w_ptrs)
+    wa = (C.c_void_p * k)(*w_ptrs)
+    ya = (C.c_void_p * k)(*y_ptrs)
+    oa = (C.c_int * k)(*out_dims)
+    check("hip_gemv_multi_async", L.hip_gemv_multi_async(ggml_type, k, wa, ya, oa, x_ptr, in_dim, stream_ptr))

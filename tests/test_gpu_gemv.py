@@ -98,6 +98,27 @@ def test_gemv_many_tiles(qh, oracle, t, shape):
     assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref)) + 1e-6
 
 
+@pytest.mark.parametrize("t", [12, 13, 14, 8, 21])
+@pytest.mark.parametrize("dims", [(4096, 1024), (14336, 14336), (37, 300, 5, 1000)], ids=str)
+def test_gemv_multi_matches_single(qh, t, dims):
+    """hip_gemv_multi (one launch for up to 4 matrices sharing x) gives each
+    matrix exactly the hip_gemv result (same kernel arithmetic; types without a
+    fused kernel fall back to one launch per matrix)."""
+    from saient_quartz_amd.host import gemv_multi_async
+    in_dim = 4096
+    datas = [synth.weights(t, o, in_dim, seed=50 + k) for k, o in enumerate(dims)]
+    x = synth.activations(1, in_dim, seed=9)[0]
+    ws = [GpuBuf.upload(d) for d in datas]
+    dx = GpuBuf.upload_f32(x)
+    ys = [GpuBuf.alloc_f32(o) for o in dims]
+    gemv_multi_async(qh, t, [w.ptr for w in ws], [y.ptr for y in ys], list(dims), dx.ptr, in_dim, None)
+    check("hip_sync", qh.hip_sync())
+    for k, o in enumerate(dims):
+        single = GpuBuf.alloc_f32(o)
+        check("hip_gemv", qh.hip_gemv(t, ws[k].ptr, dx.ptr, single.ptr, in_dim, o))
+        assert np.array_equal(ys[k].download(np.float32).view(np.uint32), single.download(np.float32).view(np.uint32))
+
+
 def test_gemv_launch_variant_8x2(qh):
     """The tuning override QUARTZ_HIP_MMV16=2 (8 waves x 2 groups) selects a
     launch shape the defaults do not use; it must give the same results.  Runs in
