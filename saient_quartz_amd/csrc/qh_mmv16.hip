@@ -37,6 +37,7 @@ typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
 #define QH_XG_ZERO 832
 #define QH_RS 240   // LDS line per row: 15 x 16 bytes, conflict-free b128 reads over 16 rows
 #define QH_MAXT 32  // row tiles per workgroup (their results wait in LDS until the end)
+#define QH_RING 4   // finished tiles per workgroup barrier (launches with few tiles)
 
 QH_DEV uint32_t qh_lo4(uint32_t q) { return q & 0x0F0F0F0Fu; }
 QH_DEV uint32_t qh_hi4(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
@@ -204,13 +205,16 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
     static_assert(ROWS <= 16 && 16 * CH < QH_RS, "tile shape");
     constexpr int TILE = ROWS * QH_RS + 16;  // staging tile of one group + 16 spare bytes
-    __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * W * 16 * 4 + QH_MAXT * 16 * 4];
+    // Wavefront partials of finished tiles wait in a ring of two sets of QH_RING
+    // tiles; the workgroup meets at a barrier only when a set is full.
+    __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 +
+                                               QH_MAXT * 16 * 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
     unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
     unsigned char* xl = lds + W * GPW * TILE + w * (GPW * QH_XG);
     float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
-    float* res = red + 2 * W * 16;  // finished rows of this workgroup's tiles
+    float* res = red + 2 * QH_RING * W * 16;  // finished rows of this workgroup's tiles
     const int ntiles = mm.tstart[QH_MULTI];
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
@@ -363,8 +367,31 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
         return fmaf(acc, rs, -accm);
     };
 
+    auto put = [&](int d, int c, float r) {  // y of row c of this workgroup's tile d
+        const int tile = blockIdx.x + d * gridDim.x, m = mat_of(tile);
+        const int row = (tile - mm.tstart[m]) * ROWS + c;
+        if (c < ROWS && row < mm.rows[m]) mm.y[m][row] = r;
+    };
+    // Sum the wavefront partials of tiles d0 .. d0+cnt-1 (one set of the ring)
+    // into res, or into y once the loop is over: a store inside the loop would
+    // make the compiler drain all loads in flight (stores and loads share vmcnt).
+    auto flush = [&](int d0, int cnt, bool direct) {
+        if ((int)threadIdx.x < 16 * cnt) {
+            const int d = d0 + ((int)threadIdx.x >> 4), c = threadIdx.x & 15;
+            const float* rb = red + (d % (2 * QH_RING)) * (W * 16) + c;
+            float r = 0.f;
+#pragma unroll
+            for (int i = 0; i < W; i++) r += rb[i * 16];
+            if (direct) put(d, c, r);
+            else res[d * 16 + c] = r;
+        }
+    };
     int tile = blockIdx.x, ch = 0, done = 0;
     if (tile >= ntiles) return;  // uniform over the workgroup
+    // Few tiles per workgroup: meet every QH_RING tiles (the end-of-kernel wait
+    // for the slowest wavefront is what short launches pay).  Many tiles: meet
+    // at every tile, which keeps the wavefronts on one tile's rows at a time.
+    const int ring = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x <= 2 * QH_RING ? QH_RING : 1;
     // Pipeline: the registers of an item are staged into LDS as soon as they
     // arrive and then receive the next item's loads, which stay in flight while
     // the staged item is computed.  No loaded value is carried around the loop
@@ -384,34 +411,28 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
         load_w(ntile, nc, wr);
         tot += compute(rs);
         if (nc == 0) {
-            // Tile finished: sum the four lanes of each column, then the wavefronts.
+            // Tile finished: sum the four lanes of each column into this
+            // wavefront's slot; the sum over wavefronts waits for a full set.
             float v = tot + bad;
             v += __shfl_xor(v, 16);
             v += __shfl_xor(v, 32);
-            float* rb = red + (done & 1) * (W * 16);
-            if (lane < 16) rb[w * 16 + lane] = v;
-            __syncthreads();
-            // y is written after the loop: a store inside it would make the
-            // compiler drain all loads in flight (stores and loads share vmcnt).
-            if (w == 0 && lane < 16) {
-                float r = 0.f;
-#pragma unroll
-                for (int i = 0; i < W; i++) r += rb[i * 16 + lane];
-                res[done * 16 + lane] = r;
-            }
+            if (lane < 16) red[((done % (2 * QH_RING)) * W + w) * 16 + lane] = v;
             tot = 0.f;
             done++;
+            if (done % ring == 0 && ntile < ntiles) {
+                __syncthreads();
+                flush(done - ring, ring, false);
+            }
         }
         if (ntile >= ntiles) break;
         tile = ntile;
         ch = nc;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < done * 16; i += 64 * W) {
-        const int tile = blockIdx.x + (i >> 4) * gridDim.x, m = mat_of(tile);
-        const int row = (tile - mm.tstart[m]) * ROWS + (i & 15);
-        if ((i & 15) < ROWS && row < mm.rows[m]) mm.y[m][row] = res[i];
-    }
+    // The last set goes straight to y; earlier sets wait in res.
+    const int last = done % ring ? done % ring : ring;
+    flush(done - last, last, true);
+    for (int i = threadIdx.x; i < (done - last) * 16; i += 64 * W) put(i >> 4, i & 15, res[i]);
 }
 
 // nm matrices (each's weights < 2^31 bytes) in one launch.
