@@ -33,7 +33,9 @@
 typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t qh_i32x16 __attribute__((ext_vector_type(16)));
 
-#define QG_MAXT 4  // row tiles per workgroup (their results wait in LDS until the end)
+#define QG_WAVES 4          // wavefronts per workgroup
+#define QG_TARGET_WGS 256   // workgroups a launch aims for (measured best: one per CU; more split K further and lose)
+#define QG_PART_TILES 2048  // (row tile, K split) partials the scratch holds
 
 // ---------------------------------------------------------------- formats
 
@@ -223,6 +225,10 @@ struct XImg {
 #define QG_MAX_GROUPS 256                     // in_dim <= 65536 on the matrix-core path
 #define QG_SCRATCH (QG_MAX_GROUPS * (16 * 1024 + 256))
 static __device__ __align__(256) unsigned char qh_mmq_scratch[QG_SCRATCH];
+// Split-K partials (16 tokens x 32 rows per (tile, split)) and per-tile arrival
+// counters; every counter is back at zero when a launch ends.
+static __device__ __align__(256) float qh_mmq_part[QG_PART_TILES * 16 * 32];
+static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES];
 
 // One workgroup (256 threads) per group: thread T digitises elements 16 (T%16)
 // .. +15 of token T/16 (zeros past n), building the image in LDS, then copies it
@@ -318,27 +324,37 @@ __global__ __launch_bounds__(256) void qh_mmq_ximg(const float* __restrict__ x, 
 
 // ---------------------------------------------------------------- kernel
 
+QH_DEV qh_i32x4 qh_as_i32x4(const qh_u32x4& v) { return qh_i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w}; }
+
+// One workgroup of W wavefronts per (row tile of 32 rows, K split): wavefront w
+// takes the split's groups w, w + W, ...  Per group ("item") it stages the tile's
+// weight slices through its LDS tile (coalesced 16-byte loads, the next item's
+// in flight during the compute) and loads the group's x image straight into
+// the A-operand registers (L2-resident, issued before the weights are staged).
+// The wavefronts' partials meet in LDS at the end; with more than one split,
+// each split stores its partial tile to `part` and the last split to arrive
+// (per-tile counter in `cnt`) adds the splits in order 0, 1, ... and writes y,
+// so the result does not depend on which split finishes last.
 template <class F, int NT, int W>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt, uint32_t wbytes,
                                                  const unsigned char* __restrict__ img, float* __restrict__ y,
-                                                 int out_dim, uint32_t row_bytes, int ngroups, int n, int ldy) {
+                                                 int out_dim, uint32_t row_bytes, int ngroups, int n, int ldy,
+                                                 int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte loads per lane per group
     constexpr int TILE = 32 * RS + 16;
     static_assert(NT == 2 || NT == 4 || NT == 8 || NT == 16, "NT");
+    static_assert(TILE >= NT * 32 * 4, "the wavefront partials reuse the staging tile");
     using XI = XImg<F::KIND, F::SUMS>;
     // Image chunks this kernel reads: Q6_K with <= 8 tokens needs only u = 0.
     constexpr int NC = (F::KIND == 2) ? (NT > 8 ? 16 : 8) : XI::CHUNKS;
-    constexpr int XB = 1024 * NC;  // per-wavefront LDS x area
     constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
-    __shared__ __align__(16) unsigned char lds[W * TILE + W * XB + W * NT * 32 * 4 + QG_MAXT * NT * 32 * 4 + GRIDB];
+    __shared__ __align__(16) unsigned char lds[W * TILE + GRIDB];
+    __shared__ int last_split;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
     unsigned char* wl = lds + w * TILE;
-    unsigned char* xl = lds + W * TILE + w * XB;
-    float* red = reinterpret_cast<float*>(lds + W * TILE + W * XB);
-    float* res = red + W * NT * 32;
-    unsigned char* gridl = reinterpret_cast<unsigned char*>(res + QG_MAXT * NT * 32);
+    unsigned char* gridl = lds + W * TILE;
     if constexpr (F::GRID != 0) {
         const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
@@ -346,45 +362,33 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
     }
     const QhBuf wb = qh_buf(Wt, wbytes);
     const QhBuf ib = qh_buf(img, (uint32_t)ngroups * XI::BYTES);
-    const int ntiles = (out_dim + 31) / 32;
-    const int nch = (ngroups + W - 1) / W;
+    const int tile = blockIdx.x / splits, sp = blockIdx.x - tile * splits;
+    const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
 
     // Weight slices of this lane: row rr[h] of the tile, byte offset goff[h] from
     // the tile's first row, LDS offset soff[h] (lanes past 32 * CH: spare bytes).
     uint32_t goff[NH], soff[NH];
-    int rr[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) {
         const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
-        rr[h] = q < 32 * CH ? r : 1 << 30;
-        goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
+        const bool ok = q < 32 * CH && tile * 32 + r < out_dim;
+        goff[h] = ok ? (uint32_t)(tile * 32 + r) * row_bytes + (c == CH - 1 ? F::LAST : 16u * c) : 0x80000000u;
         soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
     }
-
-    auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
-        const int g = ch * W + w;
-        const uint32_t base = (uint32_t)(tile * 32) * row_bytes;
+    auto load_w = [&](int g, qh_u32x4* wo) {
+        const uint32_t go = g < g1 ? (uint32_t)F::BYTES * (uint32_t)g : 0x80000000u;
 #pragma unroll
-        for (int h = 0; h < NH; h++) {
-            const bool ok = tile * 32 + rr[h] < out_dim && g < ngroups;
-            wo[h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)g);
-        }
+        for (int h = 0; h < NH; h++) wo[h] = qh_ld128(wb, goff[h] + go);
     };
     // The group's image chunks (1 KB each, coalesced) and its exponents.
     // Lanes whose A row holds a token slot >= NT load nothing (out of range: zeros).
     const bool xrow = F::KIND == 2 ? ((R & 15) >> 1) < NT : (R >> 1) < NT;
-    auto load_x = [&](int ch, qh_u32x4* xo, qh_u32x4& eo) {
-        const int g = ch * W + w;
-        const uint32_t base = g < ngroups ? (uint32_t)g * XI::BYTES : 0x80000000u;
+    auto load_x = [&](int g, qh_u32x4* xo, qh_u32x4& eo) {
+        const uint32_t base = (uint32_t)g * XI::BYTES;
         const uint32_t lb = xrow ? base + 16u * lane : 0x80000000u;
 #pragma unroll
         for (int c = 0; c < NC; c++) xo[c] = qh_ld128(ib, lb + 1024u * c);
         eo = qh_ld128(ib, base + XI::EXP);
-    };
-    // Registers -> this wavefront's LDS x area (each lane its own 16 bytes).
-    auto stage_x = [&](const qh_u32x4* xi) {
-#pragma unroll
-        for (int c = 0; c < NC; c++) *reinterpret_cast<qh_u32x4*>(xl + 1024 * c + 16 * lane) = xi[c];
     };
     auto stage = [&](const qh_u32x4* wr) {
 #pragma unroll
@@ -400,9 +404,8 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
 #pragma unroll
     for (int i = 0; i < 8; i++) tot[i] = 0.f;
     const unsigned char* wrow = wl + R * RS;
-    const unsigned char* xa = xl + 16 * lane;  // this lane's A operands: chunk c at xa + 1024 c
 
-    auto compute = [&](const qh_u32x4& ex) {
+    auto compute = [&](const qh_u32x4& ex, const qh_u32x4* xa) {
         const typename F::H hd = F::hdr(wrow);
         int acc[16];
         int acc2[16];
@@ -414,7 +417,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 qh_i32x4 b;
                 int sc;
                 F::template bop<K>(wrow, hh, gridl, b, sc);
-                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * K);
+                const qh_i32x4 a = qh_as_i32x4(xa[K]);
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
@@ -434,8 +437,8 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 constexpr int P = decltype(PC)::value;
                 qh_i32x4 b0, b1;
                 F::template bpair<P>(wrow, hh, b0, b1);
-                const qh_i32x4 a0 = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (2 * P));
-                const qh_i32x4 a1 = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (2 * P + 1));
+                const qh_i32x4 a0 = qh_as_i32x4(xa[2 * P]);
+                const qh_i32x4 a1 = qh_as_i32x4(xa[2 * P + 1]);
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 const qh_i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
                 const int s0 = F::template scl<2 * P>(hd);
@@ -459,13 +462,13 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
                 const int slo = F::template scl<2 * C>(hd), shi = F::template scl<2 * C + 1>(hd);
                 const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
                 {
-                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * C);
+                    const qh_i32x4 a = qh_as_i32x4(xa[C]);
                     const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
                     for (int j = 0; j < 8; j++) acc[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
                 }
                 if constexpr (NT > 8) {
-                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * (8 + C));
+                    const qh_i32x4 a = qh_as_i32x4(xa[8 + C]);
                     const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 #pragma unroll
                     for (int j = 0; j < 8; j++) acc2[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         // sums MFMA: the mins (Q4_K/Q5_K)
         qh_i32x16 dm = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
         if constexpr (F::SUMS) {
-            const qh_i32x4 as = *reinterpret_cast<const qh_i32x4*>(xa + 1024 * 8);
+            const qh_i32x4 as = qh_as_i32x4(xa[8]);
             dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(as, F::bmin(wrow, hd, hh), dm, 0, 0, 0);
         }
         // finish: slot (q, r) = token 4q + 2hh + r, exponent byte t of the image
@@ -516,80 +519,115 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             }
     };
 
-    int tile = blockIdx.x, ch = 0, done = 0;
-    if (tile >= ntiles) return;  // uniform over the workgroup
     qh_u32x4 wr[NH], xr[NC], er;
-    load_x(0, xr, er);
-    load_w(tile, 0, wr);
-    for (;;) {
-        const qh_u32x4 ex = er;
-        stage_x(xr);
-        int ntile = tile, nc = ch + 1;
-        if (nc == nch) { nc = 0; ntile += gridDim.x; }
-        load_x(nc, xr, er);  // next item's x image (L2-resident), in flight during the compute
+    int g = g0 + w;
+    load_w(g, wr);
+    while (g < g1) {
+        load_x(g, xr, er);
         stage(wr);
-        load_w(ntile, nc, wr);  // past the last tile: all offsets out of range, no traffic
-        compute(ex);
-        if (nc == 0) {
-            // Tile finished: lanes hold (token slot, weight row R); sum the wavefronts.
+        load_w(g + W, wr);  // past the split: all offsets out of range, no traffic
+        compute(er, xr);
+        g += W;
+    }
+    // Wavefront partials -> this wavefront's staging tile (its own LDS), then
+    // the sum over wavefronts in order 0..W-1.
+    float* red = reinterpret_cast<float*>(wl);
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
-                for (int r = 0; r < 2; r++) {
-                    const int t = 4 * q + 2 * hh + r;
-                    if (t < NT) red[(w * NT + t) * 32 + R] = tot[2 * q + r];
-                    tot[2 * q + r] = 0.f;
-                }
-            __syncthreads();
-            // y is written after the loop: a store inside it would make the
-            // compiler drain all loads in flight (stores and loads share vmcnt).
-            for (int i = threadIdx.x; i < NT * 32; i += 64 * W) {
-                float v = 0.f;
-#pragma unroll
-                for (int k = 0; k < W; k++) v += red[k * NT * 32 + i];
-                res[done * NT * 32 + i] = v;
-            }
-            __syncthreads();
-            done++;
+        for (int r = 0; r < 2; r++) {
+            const int t = 4 * q + 2 * hh + r;
+            if (t < NT) red[t * 32 + R] = tot[2 * q + r];
         }
-        if (ntile >= ntiles) break;
-        tile = ntile;
-        ch = nc;
-    }
     __syncthreads();
-    for (int i = threadIdx.x; i < done * NT * 32; i += 64 * W) {
-        const int k = i / (NT * 32), t = (i / 32) % NT, r = i & 31;
-        const int row = (blockIdx.x + k * gridDim.x) * 32 + r;
-        if (t < n && row < out_dim) y[(size_t)t * ldy + row] = res[i];
+    float v[(NT * 32 + 64 * W - 1) / (64 * W)];
+#pragma unroll
+    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
+        const int i = threadIdx.x + 64 * W * j;
+        float a = 0.f;
+        if (i < NT * 32) {
+#pragma unroll
+            for (int k = 0; k < W; k++) a += reinterpret_cast<const float*>(lds + k * TILE)[i];
+        }
+        v[j] = a;
     }
+    auto put = [&](int i, float a) {
+        const int t = i >> 5, row = tile * 32 + (i & 31);
+        if (t < n && row < out_dim) y[(size_t)t * ldy + row] = a;
+    };
+    if (splits == 1) {
+#pragma unroll
+        for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
+            const int i = threadIdx.x + 64 * W * j;
+            if (i < NT * 32) put(i, v[j]);
+        }
+        return;
+    }
+    float* mine = part + (size_t)blockIdx.x * (NT * 32);
+#pragma unroll
+    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
+        const int i = threadIdx.x + 64 * W * j;
+        if (i < NT * 32) __hip_atomic_store(mine + i, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Agent-scope stores and loads of the partials reach the device's point of
+    // coherence without writing back or invalidating whole L2s (which a
+    // release/acquire fence per workgroup would, at a cost measured in tens of
+    // microseconds per launch).  Every thread's stores have completed (vmcnt 0)
+    // before the barrier, and the counter is bumped only after it.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_split = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(splits - 1);
+    __syncthreads();
+    if (!last_split) return;
+    const float* tp = part + (size_t)tile * splits * (NT * 32);
+#pragma unroll
+    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
+        const int i = threadIdx.x + 64 * W * j;
+        if (i < NT * 32) {
+            float a = 0.f;
+            for (int k = 0; k < splits; k++)
+                a += __hip_atomic_load(tp + k * (NT * 32) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            put(i, a);
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
-// Device address of the x-image scratch, per device (hipGetSymbolAddress once).
-static unsigned char* qh_mmq_scratch_ptr() {
-    static unsigned char* ptrs[64] = {};
+// Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
+struct QgScratch { unsigned char* img; float* part; unsigned int* cnt; };
+static const QgScratch* qh_mmq_scratch_ptrs() {
+    static QgScratch ptrs[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    if (!ptrs[dev]) {
-        void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(qh_mmq_scratch)) != hipSuccess) return nullptr;
-        ptrs[dev] = static_cast<unsigned char*>(p);
+    QgScratch& p = ptrs[dev];
+    if (!p.img) {
+        void *a = nullptr, *b = nullptr, *c = nullptr;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qh_mmq_scratch)) != hipSuccess ||
+            hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) != hipSuccess ||
+            hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) != hipSuccess)
+            return nullptr;
+        p.part = static_cast<float*>(b);
+        p.cnt = static_cast<unsigned int*>(c);
+        p.img = static_cast<unsigned char*>(a);
     }
-    return ptrs[dev];
+    return &p;
 }
 
-template <class F, int NT, int W>
-static hipError_t launch_mmq(const uint8_t* Wt, const unsigned char* img, float* y, int in_dim, int out_dim, int n,
+// QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row tile (tuning).
+static int qh_mmq_splits_env() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_MMQ_SPLITS");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <class F, int NT>
+static hipError_t launch_mmq(const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim, int n,
                              uint32_t row_bytes, hipStream_t st) {
-    static int resident = 0;
-    if (!resident) {
-        int dev = 0, per_cu = 0;
-        hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmq<F, NT, W>, 64 * W, 0) != hipSuccess ||
-            per_cu < 1)
-            return hipErrorNotSupported;
-        resident = per_cu * prop.multiProcessorCount;
-    }
+    constexpr int W = QG_WAVES;
     const int ngroups = in_dim / 256;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
     if (max_rows < 32) return hipErrorNotSupported;
@@ -597,33 +635,25 @@ static hipError_t launch_mmq(const uint8_t* Wt, const unsigned char* img, float*
         const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
         const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
         const int ntiles = (rows + 31) / 32;
-        int grid = ntiles < resident ? ntiles : resident;
-        if ((ntiles + grid - 1) / grid > QG_MAXT) grid = (ntiles + QG_MAXT - 1) / QG_MAXT;
+        // K splits: enough workgroups to fill the chip (about QG_TARGET_WGS), at
+        // least one group per wavefront, and partials within the scratch.
+        int splits = qh_mmq_splits_env();
+        if (splits <= 0) {
+            splits = (QG_TARGET_WGS + ntiles - 1) / ntiles;
+            const int cap = ngroups / W > 1 ? ngroups / W : 1;
+            splits = splits < cap ? splits : cap;
+        }
+        splits = splits < ngroups ? splits : ngroups;
+        if ((int64_t)ntiles * splits > QG_PART_TILES) splits = QG_PART_TILES / ntiles;
+        if (splits < 1) splits = 1;
         // y rows r0.. of every token: y + r0 with the token stride out_dim.
-        hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           Wt + (size_t)r0 * row_bytes, wbytes, img, y + r0, rows, row_bytes, ngroups, n, out_dim);
+        hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)(ntiles * splits)), dim3(64 * W), 0, st,
+                           Wt + (size_t)r0 * row_bytes, wbytes, sc.img, y + r0, rows, row_bytes, ngroups, n, out_dim,
+                           splits, sc.part, sc.cnt);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
-}
-
-template <class F, int NT>
-static hipError_t launch_mmq_w(bool w8, const uint8_t* W, const unsigned char* img, float* y, int in_dim,
-                               int out_dim, int n, uint32_t row_bytes, hipStream_t st) {
-    if constexpr (F::KIND != 2) {
-        if (w8) return launch_mmq<F, NT, 8>(W, img, y, in_dim, out_dim, n, row_bytes, st);
-    }
-    return launch_mmq<F, NT, 4>(W, img, y, in_dim, out_dim, n, row_bytes, st);
-}
-
-// QUARTZ_HIP_MMQ_WAVES=4|8 forces the workgroup size (tuning).
-static int qh_mmq_waves_env() {
-    static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMQ_WAVES");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
 }
 
 // Batched tokens on the matrix cores; hipErrorNotSupported when the type/shape
@@ -637,8 +667,9 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;
     if ((int64_t)n * in_dim * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    unsigned char* img = qh_mmq_scratch_ptr();
-    if (!img) return hipErrorNotSupported;
+    const QgScratch* sc = qh_mmq_scratch_ptrs();
+    if (!sc) return hipErrorNotSupported;
+    unsigned char* img = sc->img;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     const int ngroups = in_dim / 256;
     for (int t0 = 0; t0 < n; t0 += 16) {
@@ -654,12 +685,7 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
             hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        // 8 wavefronts per workgroup when the row tiles alone give few workgroups
-        // (measured faster for Q4_K/Q5_K at 4096 rows); Q6_K's 16-token kernel
-        // does not fit 8 wavefronts' registers.
-        const bool w8 = qh_mmq_waves_env() == 8 ||
-                        (qh_mmq_waves_env() != 4 && type != QT_Q6_K && (out_dim + 31) / 32 < 256);
-#define QG_NT(F, NT_) e = launch_mmq_w<F, NT_>(w8, W, img, ys, in_dim, out_dim, nt, row_bytes, st);
+#define QG_NT(F, NT_) e = launch_mmq<F, NT_>(W, *sc, ys, in_dim, out_dim, nt, row_bytes, st);
 #define QG_CASE(F)                                                                                   \
     if (nt <= 2) { QG_NT(F, 2) } else if (nt <= 4) { QG_NT(F, 4) } else if (nt <= 8) { QG_NT(F, 8) } \
     else { QG_NT(F, 16) }
