@@ -519,15 +519,23 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             }
     };
 
+    // This wavefront's groups g0 + w + W j, j < nw, taken from j = rot on
+    // (rotating with the workgroup): workgroups that run together then read
+    // different groups' x images instead of all hitting the same L2 lines.
+    const int nw = g1 - g0 > w ? (g1 - g0 - w + W - 1) / W : 0;
+    const int rot = nw ? (int)(blockIdx.x % (unsigned)nw) : 0;
+    auto grp = [&](int k) { return k < nw ? g0 + w + W * (k + rot < nw ? k + rot : k + rot - nw) : g1; };
     qh_u32x4 wr[NH], xr[NC], er;
-    int g = g0 + w;
-    load_w(g, wr);
-    while (g < g1) {
+    load_w(grp(0), wr);
+    for (int k = 0; k < nw; k++) {
+        const int g = grp(k);
         load_x(g, xr, er);
+        // Keep the x loads ahead of the stage's wait for the weights (left to
+        // itself the compiler issues them after it, exposing their latency).
+        __builtin_amdgcn_sched_barrier(0);
         stage(wr);
-        load_w(g + W, wr);  // past the split: all offsets out of range, no traffic
+        load_w(grp(k + 1), wr);  // past the last group: all offsets out of range, no traffic
         compute(er, xr);
-        g += W;
     }
     // Wavefront partials -> this wavefront's staging tile (its own LDS), then
     // the sum over wavefronts in order 0..W-1.
@@ -615,6 +623,27 @@ static const QgScratch* qh_mmq_scratch_ptrs() {
     return &p;
 }
 
+template <class F, int NT, int W>
+static hipError_t launch_mmq(const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim, int n,
+                             uint32_t row_bytes, hipStream_t st);
+
+// QUARTZ_HIP_MMQ_WAVES=4|8|16 forces the wavefronts per workgroup (tuning).
+static int qh_mmq_waves_env() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_MMQ_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <class F, int NT>
+static hipError_t launch_mmq_w(int waves, const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim,
+                               int n, uint32_t row_bytes, hipStream_t st) {
+    if (waves == 16) return launch_mmq<F, NT, 16>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
+    if (waves == 8) return launch_mmq<F, NT, 8>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
+    return launch_mmq<F, NT, 4>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
+}
+
 // QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row tile (tuning).
 static int qh_mmq_splits_env() {
     static const int v = [] {
@@ -624,10 +653,9 @@ static int qh_mmq_splits_env() {
     return v;
 }
 
-template <class F, int NT>
+template <class F, int NT, int W>
 static hipError_t launch_mmq(const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim, int n,
                              uint32_t row_bytes, hipStream_t st) {
-    constexpr int W = QG_WAVES;
     const int ngroups = in_dim / 256;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
     if (max_rows < 32) return hipErrorNotSupported;
@@ -685,7 +713,8 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
             hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-#define QG_NT(F, NT_) e = launch_mmq<F, NT_>(W, *sc, ys, in_dim, out_dim, nt, row_bytes, st);
+        const int waves = qh_mmq_waves_env() ? qh_mmq_waves_env() : QG_WAVES;
+#define QG_NT(F, NT_) e = launch_mmq_w<F, NT_>(waves, W, *sc, ys, in_dim, out_dim, nt, row_bytes, st);
 #define QG_CASE(F)                                                                                   \
     if (nt <= 2) { QG_NT(F, 2) } else if (nt <= 4) { QG_NT(F, 4) } else if (nt <= 8) { QG_NT(F, 8) } \
     else { QG_NT(F, 16) }

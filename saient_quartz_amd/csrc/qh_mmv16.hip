@@ -241,7 +241,6 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
         soff[h] = q < ROWS * CH ? (uint32_t)(r * QH_RS + 16 * c) : (uint32_t)(ROWS * QH_RS);
     }
     const int n = lane & 15, kg = lane >> 4;
-    const unsigned char* wrow = wl + (n < ROWS ? n : 0) * QH_RS;
     // A operand of MFMA s: digit plane n%4 of lane kg's piece in rows 4kg..4kg+2.
     const bool arow = (n >> 2) == kg && (n & 3) < 3;
     uint32_t aoff[4], xsoff[4];
