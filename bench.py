@@ -196,19 +196,22 @@ def decode_leg(torch, reps):
 def moe_leg(torch, reps):
     """Mixtral-shaped MoE expert layer: 8 experts x
     (gate, up, down) with 16 gathered tokens each, IQ3_S and IQ2_XXS, one HIP
-    graph per layer step, timed over `reps` replays."""
+    graph per layer step, timed over `reps` replays: grouped (gate+up of all
+    experts in one hip_gemm_grouped call, down in one hip_gemm_moe call) and
+    per expert (24 hip_gemm calls, "<type>_per_expert")."""
     from saient_quartz_amd.decode import MoeLayer
 
     out = {"workload": "Mixtral-8x7B-shaped MoE expert layer: 8 experts, gate/up 14336x4096 + down 4096x14336, "
                        "16 tokens gathered per expert (top-2 of 64 tokens), random-init weights"}
-    for name, t in (("iq3_s", 21), ("iq2_xxs", 16)):
+    for name, t, grouped in (("iq3_s", 21, True), ("iq3_s_per_expert", 21, False), ("iq2_xxs", 16, True),
+                             ("iq2_xxs_per_expert", 16, False)):
         layer = MoeLayer(t)
         wbytes = layer.weight_bytes()
-        layer.issue()
+        layer.issue(grouped=grouped)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            layer.issue()
+            layer.issue(grouped=grouped)
         g.replay()
         torch.cuda.synchronize()
         t0 = torch.cuda.Event(enable_timing=True)

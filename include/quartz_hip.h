@@ -19,9 +19,10 @@
  * y is overwritten, never accumulated.  Buffers are caller-owned device memory;
  * no entry point allocates device memory.  Calls on one stream are ordered; the
  * library keeps no per-call host state and is safe to call from several host
- * threads on distinct streams, with one exception: hip_gemm / hip_gemm_async with
- * n >= 2 on Q4_K, Q5_K, Q6_K, IQ3_S or IQ2_XXS stage the digitised activations in
- * a static device array (4.2 MB, one per device), so such calls that overlap on
+ * threads on distinct streams, with one exception: hip_gemm / hip_gemm_grouped /
+ * hip_gemm_moe (and their _async forms) with n >= 2 on Q4_K, Q5_K, Q6_K, IQ3_S
+ * or IQ2_XXS stage the digitised activations and split-K partials in static
+ * device arrays (about 21 MB, one set per device), so such calls that overlap on
  * one device must be serialised by the caller (e.g. one stream per device).
  */
 #ifndef QUARTZ_HIP_H
@@ -72,6 +73,31 @@ int hip_gemm(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float*
              int n);
 int hip_gemm_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
                    int out_dim, int n, void* stream);
+
+/* Y[k] = X[k] W[k]^T for k < count: several batched GEMMs of one type and
+ * in_dim in as few launches as the device scratch allows (one weight pass per 16
+ * tokens of each matrix).  W, x, y, n and out_dims are host arrays of count
+ * entries: device pointers, tokens n[k] >= 0 (x[k] is [n[k]][in_dim], y[k] is
+ * [n[k]][out_dims[k]], token-major) and row counts.  Matrices that share an x
+ * pointer (a layer's q/k/v, gate/up) share its digitisation.  No counterpart in
+ * the reference, whose CPU gemm (src/dequant.rs:143-200) takes one matrix. */
+int hip_gemm_grouped(uint32_t ggml_type, int count, const uint8_t* const* W, const float* const* x,
+                     float* const* y, const int* n, const int* out_dims, int in_dim);
+int hip_gemm_grouped_async(uint32_t ggml_type, int count, const uint8_t* const* W, const float* const* x,
+                           float* const* y, const int* n, const int* out_dims, int in_dim, void* stream);
+
+/* Mixture-of-experts layer GEMMs over gathered tokens: for i < n_sel, expert
+ * e = expert_ids[i] (its weights at d_experts + e * hip_type_size(type,
+ * in_dim*out_dim), the expert slicing of src/cuda.rs:250-258 / :723-725)
+ * multiplies tokens tok_off[i] .. tok_off[i+1]-1 of d_x[.][in_dim] into the same
+ * rows of d_y[.][out_dim].  expert_ids and tok_off (n_sel + 1 entries, non-
+ * decreasing) are host arrays.  Generalises cuda_gemv_moe4
+ * (src/cuda_kernels.cu:1085-1106: <= 4 experts, one token each) to any number
+ * of experts and tokens, as the per-expert loop of src/cuda.rs:667-798 needs. */
+int hip_gemm_moe(uint32_t ggml_type, const uint8_t* d_experts, int n_sel, const int* expert_ids, const int* tok_off,
+                 const float* d_x, float* d_y, int in_dim, int out_dim);
+int hip_gemm_moe_async(uint32_t ggml_type, const uint8_t* d_experts, int n_sel, const int* expert_ids,
+                       const int* tok_off, const float* d_x, float* d_y, int in_dim, int out_dim, void* stream);
 
 /* Up to 4 expert GEMVs in one call.  Replaces cuda_gemv_moe4
  * (src/cuda_kernels.cu:1085-1106, Rust decl src/cuda.rs:39-45); any type. */

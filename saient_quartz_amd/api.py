@@ -51,6 +51,11 @@ _SIGS = {
     "hip_gemm": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "hip_gemm_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                  C.c_void_p]),
+    "hip_gemm_grouped": (C.c_int, [C.c_uint32, C.c_int] + [C.c_void_p] * 5 + [C.c_int]),
+    "hip_gemm_grouped_async": (C.c_int, [C.c_uint32, C.c_int] + [C.c_void_p] * 5 + [C.c_int, C.c_void_p]),
+    "hip_gemm_moe": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int]),
+    "hip_gemm_moe_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int,
+                                                                                          C.c_void_p]),
     "hip_gemv_moe4": (C.c_int, [C.c_uint32] + [C.c_void_p] * 12 + [C.c_int, C.c_int, C.c_int]),
     "hip_dequant": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t]),
     "hip_dequant_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),

@@ -142,6 +142,81 @@ int hip_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_d
     return hip_gemm_async(type, W, x, y, in_dim, out_dim, n, nullptr);
 }
 
+int hip_gemm_grouped_async(uint32_t type, int count, const uint8_t* const* W, const float* const* x, float* const* y,
+                           const int* n, const int* out_dims, int in_dim, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 0) return QH_ERR_RANGE;
+    if (count == 0) return QH_OK;
+    if (!W || !x || !y || !n || !out_dims) return QH_ERR_NULL;
+    if (qh_block_elems(type) == 0) {
+        int rc = QH_ERR_TYPE;
+        for (int k = 0; k < count; k++) {
+            const size_t cnt = (out_dims[k] > 0 && n[k] > 0) ? (size_t)out_dims[k] * (size_t)n[k] : 0;
+            rc = qh_unknown_type("hip_gemm_grouped", type, cnt ? y[k] : nullptr, cnt, st);
+        }
+        return rc;
+    }
+    bool batched = false;
+    for (int k = 0; k < count; k++) {
+        int rc = qh_check_dims(type, in_dim, out_dims[k]);
+        if (rc) return rc;
+        if (n[k] < 0) return QH_ERR_DIMS;
+        if (n[k] > 0 && out_dims[k] > 0 && (!W[k] || !x[k] || !y[k])) return QH_ERR_NULL;
+        batched = batched || (n[k] > 1 && out_dims[k] > 0);
+    }
+    if (batched && !qh_force_valu()) {
+        hipError_t e = qh_launch_mmq_grouped(type, count, W, x, y, n, out_dims, in_dim, st);
+        if (e == hipSuccess) return QH_OK;
+        if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_grouped");
+    }
+    // single tokens only, or no grouped kernel for this type/shape: one call per matrix
+    for (int k = 0; k < count; k++) {
+        int rc = hip_gemm_async(type, W[k], x[k], y[k], in_dim, out_dims[k], n[k], stream);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
+int hip_gemm_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* x, float* const* y,
+                     const int* n, const int* out_dims, int in_dim) {
+    return hip_gemm_grouped_async(type, count, W, x, y, n, out_dims, in_dim, nullptr);
+}
+
+int hip_gemm_moe_async(uint32_t type, const uint8_t* experts, int n_sel, const int* expert_ids, const int* tok_off,
+                       const float* x, float* y, int in_dim, int out_dim, void* stream) {
+    if (n_sel < 0) return QH_ERR_RANGE;
+    if (n_sel == 0) return QH_OK;
+    if (!expert_ids || !tok_off) return QH_ERR_NULL;
+    const int qk = qh_block_elems(type);
+    const size_t slice = (qk && in_dim > 0 && out_dim >= 0 && in_dim % qk == 0)
+                             ? qh_type_size(type, (size_t)in_dim * (size_t)out_dim)
+                             : 0;
+    const uint8_t* Ws[16];
+    const float* Xs[16];
+    float* Ys[16];
+    int ns[16], outs[16];
+    for (int k0 = 0; k0 < n_sel; k0 += 16) {
+        const int cnt = n_sel - k0 < 16 ? n_sel - k0 : 16;
+        for (int k = 0; k < cnt; k++) {
+            const int e = expert_ids[k0 + k], a = tok_off[k0 + k], b = tok_off[k0 + k + 1];
+            if (e < 0 || a < 0 || b < a) return QH_ERR_RANGE;
+            Ws[k] = experts ? experts + (size_t)e * slice : nullptr;
+            Xs[k] = x ? x + (size_t)a * (size_t)(in_dim > 0 ? in_dim : 0) : nullptr;
+            Ys[k] = y ? y + (size_t)a * (size_t)(out_dim > 0 ? out_dim : 0) : nullptr;
+            ns[k] = b - a;
+            outs[k] = out_dim;
+        }
+        int rc = hip_gemm_grouped_async(type, cnt, Ws, Xs, Ys, ns, outs, in_dim, stream);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
+int hip_gemm_moe(uint32_t type, const uint8_t* experts, int n_sel, const int* expert_ids, const int* tok_off,
+                 const float* x, float* y, int in_dim, int out_dim) {
+    return hip_gemm_moe_async(type, experts, n_sel, expert_ids, tok_off, x, y, in_dim, out_dim, nullptr);
+}
+
 int hip_gemv_moe4(uint32_t type, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2, const uint8_t* w3,
                   const float* xi0, const float* xi1, const float* xi2, const float* xi3, float* o0, float* o1,
                   float* o2, float* o3, int n_act, int in_dim, int out_dim) {

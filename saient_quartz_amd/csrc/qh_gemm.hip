@@ -27,6 +27,8 @@
 // Reference counterpart: dequant::gemm (src/dequant.rs:143-200) with
 // q4k_row_batched / q6k_row_batched (:38-122); the reference has no GPU
 // batched path.
+#include <climits>
+
 #include "qh_formats.h"
 #include "qh_internal.h"
 
@@ -223,12 +225,28 @@ struct XImg {
     static constexpr int BYTES = EXP + 256;  // per group
 };
 #define QG_MAX_GROUPS 256                     // in_dim <= 65536 on the matrix-core path
-#define QG_SCRATCH (QG_MAX_GROUPS * (16 * 1024 + 256))
+#define QG_SCRATCH (4 * QG_MAX_GROUPS * (16 * 1024 + 256))  // 16.6 MB: 4 slots at the largest in_dim
 static __device__ __align__(256) unsigned char qh_mmq_scratch[QG_SCRATCH];
 // Split-K partials (16 tokens x 32 rows per (tile, split)) and per-tile arrival
 // counters; every counter is back at zero when a launch ends.
 static __device__ __align__(256) float qh_mmq_part[QG_PART_TILES * 16 * 32];
 static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES];
+
+#define QG_MAXG 16  // matrices (or row chunks) per grouped launch
+struct QgXs {        // the distinct token blocks of one grouped launch
+    const float* x[QG_MAXG];
+    int n[QG_MAXG];  // tokens (<= 16)
+};
+struct QgGroups {    // the matrices of one grouped launch
+    const uint8_t* w[QG_MAXG];
+    float* y[QG_MAXG];
+    uint32_t wbytes[QG_MAXG];  // buffer range of each matrix's weights
+    int rows[QG_MAXG];
+    int n[QG_MAXG];            // tokens of the matrix's x block
+    int ldy[QG_MAXG];          // y token stride
+    int slot[QG_MAXG];         // x image slot
+    int bstart[QG_MAXG + 1];   // first workgroup of each matrix; entries past the count are INT_MAX
+};
 
 // One workgroup (256 threads) per group: thread T digitises elements 16 (T%16)
 // .. +15 of token T/16 (zeros past n), building the image in LDS, then copies it
@@ -236,12 +254,16 @@ static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES];
 // round(x 2^s), |n| <= 2^14 (s = 14 - exponent of the token's max |x| over the
 // group), so the float's low bytes XOR 0x80 are the balanced digits of n.
 // Sums: exact integer sums of n over each sub-block, in units of 2^SUMSH.
+// Grid (groups, slots): slot s digitises the n[s] tokens at x[s] into image
+// slot s (img + s * ngroups * XI::BYTES).
 template <int KIND, bool SUMS, int SUMSH>
-__global__ __launch_bounds__(256) void qh_mmq_ximg(const float* __restrict__ x, unsigned char* __restrict__ img,
-                                                   int in_dim, int n) {
+__global__ __launch_bounds__(256) void qh_mmq_ximg(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
     using XI = XImg<KIND, SUMS>;
     __shared__ __align__(16) unsigned char im[XI::BYTES];
     const int T = threadIdx.x, g = blockIdx.x;
+    const float* __restrict__ x = xs.x[blockIdx.y];
+    const int n = xs.n[blockIdx.y];
+    img += (size_t)blockIdx.y * gridDim.x * XI::BYTES;
     const int t = T >> 4, p = T & 15;
     for (int i = 16 * T; i < XI::BYTES; i += 16 * 256) *reinterpret_cast<qh_u32x4*>(im + i) = qh_u32x4{0, 0, 0, 0};
     float4 v[4];
@@ -336,10 +358,9 @@ QH_DEV qh_i32x4 qh_as_i32x4(const qh_u32x4& v) { return qh_i32x4{(int)v.x, (int)
 // (per-tile counter in `cnt`) adds the splits in order 0, 1, ... and writes y,
 // so the result does not depend on which split finishes last.
 template <class F, int NT, int W>
-__global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt, uint32_t wbytes,
-                                                 const unsigned char* __restrict__ img, float* __restrict__ y,
-                                                 int out_dim, uint32_t row_bytes, int ngroups, int n, int ldy,
-                                                 int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
+__global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const unsigned char* __restrict__ img,
+                                                 uint32_t row_bytes, int ngroups, int splits,
+                                                 float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte loads per lane per group
     constexpr int TILE = 32 * RS + 16;
@@ -360,9 +381,18 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
         __syncthreads();
     }
-    const QhBuf wb = qh_buf(Wt, wbytes);
-    const QhBuf ib = qh_buf(img, (uint32_t)ngroups * XI::BYTES);
-    const int tile = blockIdx.x / splits, sp = blockIdx.x - tile * splits;
+    // This workgroup's matrix (uniform), row tile and K split.  Every matrix's
+    // workgroups start at a multiple of `splits`, so blockIdx / splits is a
+    // launch-wide tile index (for the split counters and partials).
+    int gi = 0;
+#pragma unroll
+    for (int k = 1; k < QG_MAXG; k++) gi += (int)blockIdx.x >= gs.bstart[k];
+    const int out_dim = gs.rows[gi], n = gs.n[gi], ldy = gs.ldy[gi];
+    float* __restrict__ y = gs.y[gi];
+    const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
+    const QhBuf ib = qh_buf(img + (size_t)gs.slot[gi] * ngroups * XI::BYTES, (uint32_t)ngroups * XI::BYTES);
+    const int lb = blockIdx.x - gs.bstart[gi];
+    const int tile = lb / splits, sp = lb - tile * splits, gt = blockIdx.x / splits;
     const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
 
     // Weight slices of this lane: row rr[h] of the tile, byte offset goff[h] from
@@ -585,11 +615,11 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0)
-        last_split = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last_split = __hip_atomic_fetch_add(&cnt[gt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      (unsigned)(splits - 1);
     __syncthreads();
     if (!last_split) return;
-    const float* tp = part + (size_t)tile * splits * (NT * 32);
+    const float* tp = part + (size_t)gt * splits * (NT * 32);
 #pragma unroll
     for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
         const int i = threadIdx.x + 64 * W * j;
@@ -600,7 +630,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const uint8_t* __restrict__ Wt,
             put(i, a);
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    if (threadIdx.x == 0) __hip_atomic_store(&cnt[gt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
@@ -623,10 +653,6 @@ static const QgScratch* qh_mmq_scratch_ptrs() {
     return &p;
 }
 
-template <class F, int NT, int W>
-static hipError_t launch_mmq(const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim, int n,
-                             uint32_t row_bytes, hipStream_t st);
-
 // QUARTZ_HIP_MMQ_WAVES=4|8|16 forces the wavefronts per workgroup (tuning).
 static int qh_mmq_waves_env() {
     static const int v = [] {
@@ -634,14 +660,6 @@ static int qh_mmq_waves_env() {
         return e ? atoi(e) : 0;
     }();
     return v;
-}
-
-template <class F, int NT>
-static hipError_t launch_mmq_w(int waves, const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim,
-                               int n, uint32_t row_bytes, hipStream_t st) {
-    if (waves == 16) return launch_mmq<F, NT, 16>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
-    if (waves == 8) return launch_mmq<F, NT, 8>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
-    return launch_mmq<F, NT, 4>(Wt, sc, y, in_dim, out_dim, n, row_bytes, st);
 }
 
 // QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row tile (tuning).
@@ -654,79 +672,166 @@ static int qh_mmq_splits_env() {
 }
 
 template <class F, int NT, int W>
-static hipError_t launch_mmq(const uint8_t* Wt, const QgScratch& sc, float* y, int in_dim, int out_dim, int n,
-                             uint32_t row_bytes, hipStream_t st) {
+static void launch_mmq(const QgGroups& gs, int wgs, int splits, const QgScratch& sc, uint32_t row_bytes, int ngroups,
+                       hipStream_t st) {
+    hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)wgs), dim3(64 * W), 0, st, gs, sc.img, row_bytes, ngroups,
+                       splits, sc.part, sc.cnt);
+}
+
+template <class F, int NT>
+static void launch_mmq_w(int waves, const QgGroups& gs, int wgs, int splits, const QgScratch& sc, uint32_t row_bytes,
+                         int ngroups, hipStream_t st) {
+    if (waves == 16) launch_mmq<F, NT, 16>(gs, wgs, splits, sc, row_bytes, ngroups, st);
+    else if (waves == 8) launch_mmq<F, NT, 8>(gs, wgs, splits, sc, row_bytes, ngroups, st);
+    else launch_mmq<F, NT, 4>(gs, wgs, splits, sc, row_bytes, ngroups, st);
+}
+
+template <class F>
+static void launch_mmq_nt(int nt, int waves, const QgGroups& gs, int wgs, int splits, const QgScratch& sc,
+                          uint32_t row_bytes, int ngroups, hipStream_t st) {
+    if (nt <= 2) launch_mmq_w<F, 2>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
+    else if (nt <= 4) launch_mmq_w<F, 4>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
+    else if (nt <= 8) launch_mmq_w<F, 8>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
+    else launch_mmq_w<F, 16>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
+}
+
+// Bytes of one x image slot (all groups of in_dim) for a type's kernel.
+static size_t qg_slot_bytes(uint32_t type, int ngroups) {
+    const size_t per = type == QT_Q6_K ? XImg<2, false>::BYTES
+                       : (type == QT_IQ3_S || type == QT_IQ2_XXS) ? XImg<1, false>::BYTES
+                                                                  : XImg<0, true>::BYTES;
+    return per * (size_t)ngroups;
+}
+
+struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
+    const uint8_t* w;
+    const float* x;
+    float* y;
+    int n, rows, ldy;
+};
+
+// One grouped launch pair: the prologue digitises every distinct token block
+// into its image slot, then the main kernel covers every entry's row tiles.
+static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, uint32_t row_bytes,
+                         const QgScratch& sc, hipStream_t st) {
     const int ngroups = in_dim / 256;
+    const int waves = qh_mmq_waves_env() ? qh_mmq_waves_env() : QG_WAVES;
+    QgXs xs = {};
+    QgGroups gs = {};
+    int nslots = 0, ntmax = 0, tiles = 0;
+    for (int i = 0; i < cnt; i++) {
+        int j = 0;
+        while (j < nslots && !(xs.x[j] == en[i].x && xs.n[j] == en[i].n)) j++;
+        if (j == nslots) {
+            xs.x[j] = en[i].x;
+            xs.n[j] = en[i].n;
+            nslots++;
+        }
+        gs.w[i] = en[i].w;
+        gs.y[i] = en[i].y;
+        gs.wbytes[i] = (uint32_t)(((uint64_t)en[i].rows * row_bytes + 3) & ~(uint64_t)3);
+        gs.rows[i] = en[i].rows;
+        gs.n[i] = en[i].n;
+        gs.ldy[i] = en[i].ldy;
+        gs.slot[i] = j;
+        ntmax = en[i].n > ntmax ? en[i].n : ntmax;
+        tiles += (en[i].rows + 31) / 32;
+    }
+    // K splits: enough workgroups to fill the chip (about QG_TARGET_WGS), at
+    // least one group per wavefront, and partials within the scratch.
+    int splits = qh_mmq_splits_env();
+    if (splits <= 0) {
+        splits = (QG_TARGET_WGS + tiles - 1) / tiles;
+        const int cap = ngroups / waves > 1 ? ngroups / waves : 1;
+        splits = splits < cap ? splits : cap;
+    }
+    splits = splits < ngroups ? splits : ngroups;
+    if ((int64_t)tiles * splits > QG_PART_TILES) splits = QG_PART_TILES / tiles;
+    if (splits < 1) splits = 1;
+    int wgs = 0;
+    for (int i = 0; i < QG_MAXG; i++) {
+        gs.bstart[i] = i < cnt ? wgs : INT_MAX;
+        if (i < cnt) wgs += (en[i].rows + 31) / 32 * splits;
+    }
+    gs.bstart[QG_MAXG] = INT_MAX;
+
+    const dim3 pg((unsigned)ngroups, (unsigned)nslots);
+    if (type == QT_Q6_K)
+        hipLaunchKernelGGL((qh_mmq_ximg<2, false, 4>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
+    else if (type == QT_IQ3_S || type == QT_IQ2_XXS)
+        hipLaunchKernelGGL((qh_mmq_ximg<1, false, 5>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
+    else
+        hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (type) {
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+    }
+    return hipGetLastError();
+}
+
+// Batched tokens on the matrix cores for `count` matrices of one type and
+// in_dim: Y[i][t][:] = W[i] X[i][t][:] for t < n[i] (token-major, y token stride
+// out_dims[i]); hipErrorNotSupported when the type/shape has no kernel here.
+// Tokens go in chunks of up to 16 (one weight pass each); matrices whose
+// weights pass 2 GB go in row chunks.  Per launch, qh_mmq_ximg writes the x
+// images to the library's device scratch and qh_mmq reads them; the scratch is
+// one array per device, so calls that overlap on one device (different
+// streams) must be serialised by the caller.
+hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
+                                 float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st) {
+    if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || count < 1) return hipErrorNotSupported;
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
+        return hipErrorNotSupported;
+    const QgScratch* sc = qh_mmq_scratch_ptrs();
+    if (!sc) return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    const int ngroups = in_dim / 256;
+    int max_slots = (int)(QG_SCRATCH / qg_slot_bytes(type, ngroups));
+    max_slots = max_slots < QG_MAXG ? max_slots : QG_MAXG;
+    if (max_slots < 1) return hipErrorNotSupported;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
     if (max_rows < 32) return hipErrorNotSupported;
-    for (int64_t r0 = 0; r0 < out_dim; r0 += max_rows) {
-        const int rows = (int)((out_dim - r0) < max_rows ? (out_dim - r0) : max_rows);
-        const uint32_t wbytes = (uint32_t)(((uint64_t)rows * row_bytes + 3) & ~(uint64_t)3);
-        const int ntiles = (rows + 31) / 32;
-        // K splits: enough workgroups to fill the chip (about QG_TARGET_WGS), at
-        // least one group per wavefront, and partials within the scratch.
-        int splits = qh_mmq_splits_env();
-        if (splits <= 0) {
-            splits = (QG_TARGET_WGS + ntiles - 1) / ntiles;
-            const int cap = ngroups / W > 1 ? ngroups / W : 1;
-            splits = splits < cap ? splits : cap;
+    int nmax = 0;
+    for (int i = 0; i < count; i++) nmax = n[i] > nmax ? n[i] : nmax;
+    QgEntry batch[QG_MAXG];
+    for (int t0 = 0; t0 < nmax; t0 += 16) {
+        int cnt = 0, slots = 0;
+        const float* last_x = nullptr;
+        for (int i = 0; i < count; i++) {
+            if (n[i] <= t0 || out_dims[i] <= 0) continue;
+            const int nt = n[i] - t0 < 16 ? n[i] - t0 : 16;
+            const float* xs = X[i] + (size_t)t0 * in_dim;
+            for (int64_t r0 = 0; r0 < out_dims[i]; r0 += max_rows) {
+                // a new slot unless the previous entry's x is the same
+                const bool new_slot = !(cnt > 0 && xs == last_x && batch[cnt - 1].n == nt);
+                if (cnt == QG_MAXG || (new_slot && slots == max_slots)) {
+                    hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st);
+                    if (e != hipSuccess) return e;
+                    cnt = 0;
+                    slots = 0;
+                }
+                if (!(cnt > 0 && xs == last_x && batch[cnt - 1].n == nt)) slots++;
+                const int rows = (int)(out_dims[i] - r0 < max_rows ? out_dims[i] - r0 : max_rows);
+                batch[cnt++] = QgEntry{W[i] + (size_t)r0 * row_bytes, xs, Y[i] + (size_t)t0 * out_dims[i] + r0, nt,
+                                       rows, out_dims[i]};
+                last_x = xs;
+            }
         }
-        splits = splits < ngroups ? splits : ngroups;
-        if ((int64_t)ntiles * splits > QG_PART_TILES) splits = QG_PART_TILES / ntiles;
-        if (splits < 1) splits = 1;
-        // y rows r0.. of every token: y + r0 with the token stride out_dim.
-        hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)(ntiles * splits)), dim3(64 * W), 0, st,
-                           Wt + (size_t)r0 * row_bytes, wbytes, sc.img, y + r0, rows, row_bytes, ngroups, n, out_dim,
-                           splits, sc.part, sc.cnt);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (cnt) {
+            hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st);
+            if (e != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }
 
-// Batched tokens on the matrix cores; hipErrorNotSupported when the type/shape
-// has no kernel here.  Tokens go in chunks of up to 16 (one weight pass each);
-// per chunk, qh_mmq_ximg writes the x image to the library's device scratch and
-// qh_mmq reads it.  The scratch is one array per device: calls that overlap on
-// one device (different streams) must be serialised by the caller.
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                          hipStream_t st) {
-    if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || n < 2) return hipErrorNotSupported;
-    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
-        return hipErrorNotSupported;
-    if ((int64_t)n * in_dim * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    const QgScratch* sc = qh_mmq_scratch_ptrs();
-    if (!sc) return hipErrorNotSupported;
-    unsigned char* img = sc->img;
-    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
-    const int ngroups = in_dim / 256;
-    for (int t0 = 0; t0 < n; t0 += 16) {
-        const int nt = n - t0 < 16 ? n - t0 : 16;
-        const float* xs = x + (size_t)t0 * in_dim;
-        float* ys = y + (size_t)t0 * out_dim;
-        hipError_t e;
-        if (type == QT_Q6_K)
-            hipLaunchKernelGGL((qh_mmq_ximg<2, false, 4>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
-        else if (type == QT_IQ3_S || type == QT_IQ2_XXS)
-            hipLaunchKernelGGL((qh_mmq_ximg<1, false, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
-        else
-            hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), dim3(ngroups), dim3(256), 0, st, xs, img, in_dim, nt);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        const int waves = qh_mmq_waves_env() ? qh_mmq_waves_env() : QG_WAVES;
-#define QG_NT(F, NT_) e = launch_mmq_w<F, NT_>(waves, W, *sc, ys, in_dim, out_dim, nt, row_bytes, st);
-#define QG_CASE(F)                                                                                   \
-    if (nt <= 2) { QG_NT(F, 2) } else if (nt <= 4) { QG_NT(F, 4) } else if (nt <= 8) { QG_NT(F, 8) } \
-    else { QG_NT(F, 16) }
-        if (type == QT_Q4_K) { QG_CASE(GQ4K) }
-        else if (type == QT_Q5_K) { QG_CASE(GQ5K) }
-        else if (type == QT_IQ3_S) { QG_CASE(GIQ3S) }
-        else if (type == QT_IQ2_XXS) { QG_CASE(GIQ2XXS) }
-        else { QG_CASE(GQ6K) }
-#undef QG_CASE
-#undef QG_NT
-        if (e != hipSuccess) return e;
-    }
-    (void)ngroups;
-    return hipSuccess;
+    if (n < 2) return hipErrorNotSupported;
+    return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st);
 }

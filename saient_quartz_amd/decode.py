@@ -18,7 +18,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import gemv_multi_async
+from .host import gemm_grouped_async, gemm_moe_async, gemv_multi_async
 
 Q4_K, Q6_K = 12, 14
 
@@ -75,14 +75,15 @@ class DecodeStep:
 
     def issue(self, n: int = 1, stream=None, fuse: bool = True):
         """Enqueue one decode step's GEMVs for n tokens on `stream` (torch stream).
-        With n = 1 and `fuse`, the projections that share x and type go out as one
-        hip_gemv_multi launch each: q+k (Q4_K) and gate+up (Q4_K)."""
+        With `fuse`, the projections that share x and type go out as one call
+        each: q+k (Q4_K) and gate+up (Q4_K), through hip_gemv_multi at n = 1 and
+        hip_gemm_grouped (one x digitisation, one weight launch) at n > 1."""
         assert 1 <= n <= self.n_max
         sp = (stream or torch.cuda.current_stream()).cuda_stream
         names = [m[0] for m in self.shape.layer_mats()]
         for mats in self.layers:
             by = dict(zip(names, mats))
-            if n == 1 and fuse:
+            if fuse:
                 for group in (("q", "k"), ("v",), ("o",), ("gate", "up"), ("down",)):
                     if len(group) == 1:
                         t, w, o, i = by[group[0]]
@@ -90,9 +91,14 @@ class DecodeStep:
                         continue
                     t, _, _, i = by[group[0]]
                     x = self.x if i == self.shape.hidden else self.xf
-                    gemv_multi_async(self.L, t, [by[g][1].data_ptr() for g in group],
-                                     [self.y[g].data_ptr() for g in group], [by[g][2] for g in group],
-                                     x.data_ptr(), i, sp)
+                    if n == 1:
+                        gemv_multi_async(self.L, t, [by[g][1].data_ptr() for g in group],
+                                         [self.y[g].data_ptr() for g in group], [by[g][2] for g in group],
+                                         x.data_ptr(), i, sp)
+                    else:
+                        gemm_grouped_async(self.L, t, [by[g][1].data_ptr() for g in group],
+                                           [x.data_ptr()] * len(group), [self.y[g].data_ptr() for g in group],
+                                           [n] * len(group), [by[g][2] for g in group], i, sp)
                 continue
             for name, (t, w, o, i) in zip(names, mats):
                 self._mm(t, w, self.y[name], o, i, n, sp)
@@ -103,21 +109,24 @@ class DecodeStep:
 class MoeLayer:
     """Mixtral-8x7B-shaped MoE expert layer: 8 experts,
     each gate/up 14336x4096 and down 4096x14336 in one IQ type, 16 tokens
-    gathered per expert (top-2 routing of 64 tokens).  A step runs every
-    expert's three GEMMs (n = 16 tokens) through hip_gemm_async, as the
-    reference's per-expert loop does (src/cuda.rs:667-798).  The router, the
-    gather/scatter and swiglu are glue outside this library: the gathered
-    activations are fixed buffers."""
+    gathered per expert (top-2 routing of 64 tokens).  Each projection's experts
+    are stacked in one buffer (expert e at base + e * slice bytes, as
+    src/cuda.rs:250-258 addresses them).  A step runs every expert's three GEMMs:
+    grouped (default), gate and up of all experts in one hip_gemm_grouped call
+    (each expert's x digitised once for both) and down in one hip_gemm_moe call;
+    or per expert, three hip_gemm calls each, as the reference's loop does
+    (src/cuda.rs:667-798).  The router, the gather/scatter and swiglu are glue
+    outside this library: the gathered activations are fixed buffers."""
 
     def __init__(self, ggml_type: int, experts: int = 8, tokens: int = 16, hidden: int = 4096, ffn: int = 14336,
                  seed: int = 20261205):
+        from . import type_size
         self.t, self.E, self.n, self.h, self.f = ggml_type, experts, tokens, hidden, ffn
         self.L = lib()
-        self.w = []
-        for e in range(experts):
-            self.w.append([synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e),
-                           synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e + 1),
-                           synth_device.weights(ggml_type, hidden, ffn, seed + 3 * e + 2)])
+        self.slice = type_size(ggml_type, ffn * hidden)
+        self.wg = torch.cat([synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e) for e in range(experts)])
+        self.wu = torch.cat([synth_device.weights(ggml_type, ffn, hidden, seed + 3 * e + 1) for e in range(experts)])
+        self.wd = torch.cat([synth_device.weights(ggml_type, hidden, ffn, seed + 3 * e + 2) for e in range(experts)])
         g = torch.Generator(device="cuda")
         g.manual_seed(seed - 1)
         self.x = torch.randn(experts, tokens, hidden, device="cuda", generator=g)
@@ -127,16 +136,27 @@ class MoeLayer:
         self.down = torch.empty(experts, tokens, hidden, device="cuda")
 
     def weight_bytes(self) -> int:
-        from . import type_size
-        return self.E * (2 * type_size(self.t, self.f * self.h) + type_size(self.t, self.h * self.f))
+        return 3 * self.E * self.slice
 
-    def issue(self, stream=None):
+    def expert(self, w, e):
+        return w.data_ptr() + e * self.slice
+
+    def issue(self, stream=None, grouped: bool = True):
         sp = (stream or torch.cuda.current_stream()).cuda_stream
-        t, n, h, f = self.t, self.n, self.h, self.f
-        for e, (wg, wu, wd) in enumerate(self.w):
-            check("hip_gemm_async", self.L.hip_gemm_async(t, wg.data_ptr(), self.x[e].data_ptr(),
+        t, n, h, f, E = self.t, self.n, self.h, self.f, self.E
+        if grouped:
+            xs = [self.x[e].data_ptr() for e in range(E)]
+            gemm_grouped_async(self.L, t, [self.expert(self.wg, e) for e in range(E)] +
+                               [self.expert(self.wu, e) for e in range(E)], xs + xs,
+                               [self.gate[e].data_ptr() for e in range(E)] + [self.up[e].data_ptr() for e in range(E)],
+                               [n] * (2 * E), [f] * (2 * E), h, sp)
+            gemm_moe_async(self.L, t, self.wd.data_ptr(), list(range(E)), [n * e for e in range(E + 1)],
+                           self.hbuf.data_ptr(), self.down.data_ptr(), f, h, sp)
+            return
+        for e in range(E):
+            check("hip_gemm_async", self.L.hip_gemm_async(t, self.expert(self.wg, e), self.x[e].data_ptr(),
                                                           self.gate[e].data_ptr(), h, f, n, sp))
-            check("hip_gemm_async", self.L.hip_gemm_async(t, wu.data_ptr(), self.x[e].data_ptr(),
+            check("hip_gemm_async", self.L.hip_gemm_async(t, self.expert(self.wu, e), self.x[e].data_ptr(),
                                                           self.up[e].data_ptr(), h, f, n, sp))
-            check("hip_gemm_async", self.L.hip_gemm_async(t, wd.data_ptr(), self.hbuf[e].data_ptr(),
+            check("hip_gemm_async", self.L.hip_gemm_async(t, self.expert(self.wd, e), self.hbuf[e].data_ptr(),
                                                           self.down[e].data_ptr(), f, h, n, sp))

@@ -115,3 +115,23 @@ def gemv_multi_async(L, ggml_type, w_ptrs, y_ptrs, out_dims, x_ptr, in_dim, stre
     ya = (C.c_void_p * k)(*y_ptrs)
     oa = (C.c_int * k)(*out_dims)
     check("hip_gemv_multi_async", L.hip_gemv_multi_async(ggml_type, k, wa, ya, oa, x_ptr, in_dim, stream_ptr))
+
+
+def gemm_grouped_async(L, ggml_type, w_ptrs, x_ptrs, y_ptrs, ns, out_dims, in_dim, stream_ptr):
+    """hip_gemm_grouped_async with host arrays built from Python ints (device pointers)."""
+    import ctypes as C
+    k = len(w_ptrs)
+    check("hip_gemm_grouped_async",
+          L.hip_gemm_grouped_async(ggml_type, k, (C.c_void_p * k)(*w_ptrs), (C.c_void_p * k)(*x_ptrs),
+                                   (C.c_void_p * k)(*y_ptrs), (C.c_int * k)(*ns), (C.c_int * k)(*out_dims),
+                                   in_dim, stream_ptr))
+
+
+def gemm_moe_async(L, ggml_type, experts_ptr, expert_ids, tok_off, x_ptr, y_ptr, in_dim, out_dim, stream_ptr):
+    """hip_gemm_moe_async: expert_ids[i] takes gathered tokens tok_off[i] .. tok_off[i+1]-1."""
+    import ctypes as C
+    k = len(expert_ids)
+    assert len(tok_off) == k + 1
+    check("hip_gemm_moe_async",
+          L.hip_gemm_moe_async(ggml_type, experts_ptr, k, (C.c_int * k)(*expert_ids), (C.c_int * (k + 1))(*tok_off),
+                               x_ptr, y_ptr, in_dim, out_dim, stream_ptr))

@@ -58,6 +58,13 @@ def test_argument_errors_before_any_gpu_call():
     assert L.hip_dequant(12, nul, nul, 256) == -3
     assert L.hip_dequant(12, nul, nul, 0) == 0
     assert L.hip_dequant(5, nul, nul, 32) == -1
+    assert L.hip_gemm_grouped(12, -1, nul, nul, nul, nul, nul, 256) == -5
+    assert L.hip_gemm_grouped(12, 0, nul, nul, nul, nul, nul, 256) == 0
+    assert L.hip_gemm_grouped(12, 1, nul, nul, nul, nul, nul, 256) == -3
+    assert L.hip_gemm_moe(12, nul, -1, nul, nul, nul, nul, 256, 8) == -5
+    assert L.hip_gemm_moe(12, nul, 0, nul, nul, nul, nul, 256, 8) == 0
+    assert L.hip_gemm_moe(12, nul, 2, nul, nul, nul, nul, 256, 8) == -3
+    assert L.hip_gemm_moe(12, nul, 1, (C.c_int * 1)(-1), (C.c_int * 2)(0, 1), nul, nul, 256, 8) == -5
     assert L.hip_status_string(-2).decode().startswith("bad dimensions")
 
 
