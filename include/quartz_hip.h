@@ -42,6 +42,8 @@ extern "C" {
 #define QH_ERR_NULL (-3)  /* null device pointer with non-empty dims */
 #define QH_ERR_HIP (-4)   /* HIP runtime error; hip_last_error() has the message */
 #define QH_ERR_RANGE (-5) /* argument outside a documented limit */
+#define QH_ERR_FORMAT (-6) /* malformed or unsupported GGUF file (message in hip_last_error) */
+#define QH_ERR_IO (-7)     /* file cannot be opened, mapped or written */
 
 /* GGML type ids handled: 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0,
  * 10 Q2_K, 12 Q4_K, 13 Q5_K, 14 Q6_K, 16 IQ2_XXS, 17 IQ2_XS, 20 IQ4_NL,
@@ -140,6 +142,60 @@ int hip_set_ksigns(const uint8_t* host);
 /* Diagnostics. */
 const char* hip_status_string(int status);
 const char* hip_last_error(void); /* last HIP error seen on this host thread ("" if none) */
+
+/* ---------------------------------------------------------------- GGUF
+ * Reader for the weight container either side of the GEMV path: GgufFile
+ * (src/gguf.rs:61-191).  hip_gguf_open memory-maps the file and parses the
+ * header (magic 0x46554747, versions 1..3; v1 has u32 counts and dims), the
+ * typed metadata and the tensor infos; the data section starts at the next
+ * multiple of general.alignment (default 32).  Errors the reference reports with
+ * bail! come back as QH_ERR_FORMAT / QH_ERR_IO with its message in
+ * hip_last_error().  Metadata getters follow GgufValue::as_u32 / as_u64 / as_str
+ * (src/gguf.rs:18-35).  hip_gguf_tensor_data is GgufFile::tensor_data
+ * (src/gguf.rs:116-121), a view into the map; hip_gguf_upload copies a tensor to
+ * a new device buffer (free with hip_drop), as GpuWeights::from_weights does per
+ * tensor (src/cuda.rs:170-172).  Value types: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32,
+ * 5 i32, 6 f32, 7 bool, 8 string, 9 array, 10 u64, 11 i64, 12 f64. */
+typedef struct qh_gguf qh_gguf;
+typedef struct qh_gguf_writer qh_gguf_writer;
+
+int hip_gguf_open(const char* path, qh_gguf** out);
+void hip_gguf_close(qh_gguf* f);
+uint32_t hip_gguf_version(const qh_gguf* f);
+uint64_t hip_gguf_data_offset(const qh_gguf* f);
+uint64_t hip_gguf_alignment(const qh_gguf* f);
+int64_t hip_gguf_kv_count(const qh_gguf* f);
+const char* hip_gguf_kv_key(const qh_gguf* f, int64_t i);  /* file order */
+int hip_gguf_kv_type(const qh_gguf* f, const char* key, uint32_t* elem_type, uint64_t* count); /* -1: absent */
+int hip_gguf_get_u32(const qh_gguf* f, const char* key, uint32_t* v);  /* Uint32 or Int32 */
+int hip_gguf_get_u64(const qh_gguf* f, const char* key, uint64_t* v);  /* Uint64 or Uint32 */
+int hip_gguf_get_i64(const qh_gguf* f, const char* key, int64_t* v);   /* any integer or bool */
+int hip_gguf_get_f32(const qh_gguf* f, const char* key, float* v);
+int hip_gguf_get_f64(const qh_gguf* f, const char* key, double* v);    /* Float64 or Float32 */
+const char* hip_gguf_get_str(const qh_gguf* f, const char* key, uint64_t* len);
+const void* hip_gguf_get_array(const qh_gguf* f, const char* key, uint32_t* elem_type, uint64_t* count);
+const char* hip_gguf_get_array_str(const qh_gguf* f, const char* key, uint64_t i, uint64_t* len);
+int64_t hip_gguf_tensor_count(const qh_gguf* f);
+int64_t hip_gguf_find_tensor(const qh_gguf* f, const char* name);  /* -1: absent */
+int hip_gguf_tensor_info(const qh_gguf* f, int64_t i, const char** name, uint32_t* n_dims, uint64_t* dims8,
+                         uint32_t* ggml_type, uint64_t* offset);
+const void* hip_gguf_tensor_data(const qh_gguf* f, int64_t i, size_t* bytes);
+int hip_gguf_upload(const qh_gguf* f, int64_t i, void** d_ptr, size_t* bytes);
+
+/* Writer: the container make_test_model.py produces (version 3, tensors in
+ * order, each padded to general.alignment, default 32), for any ggml type and
+ * metadata type.  Tensor data pointers must stay valid until _write. */
+qh_gguf_writer* hip_gguf_writer_new(void);
+void hip_gguf_writer_free(qh_gguf_writer* w);
+int hip_gguf_writer_kv_scalar(qh_gguf_writer* w, const char* key, uint32_t type, const void* le8);
+int hip_gguf_writer_kv_str(qh_gguf_writer* w, const char* key, const char* s, uint64_t len);
+int hip_gguf_writer_kv_array(qh_gguf_writer* w, const char* key, uint32_t elem_type, const void* data,
+                             uint64_t count);
+int hip_gguf_writer_kv_array_str(qh_gguf_writer* w, const char* key, const char* const* strs, const uint64_t* lens,
+                                 uint64_t count);
+int hip_gguf_writer_tensor(qh_gguf_writer* w, const char* name, uint32_t n_dims, const uint64_t* dims,
+                           uint32_t ggml_type, const void* data);
+int hip_gguf_writer_write(const qh_gguf_writer* w, const char* path);
 
 #ifdef __cplusplus
 }

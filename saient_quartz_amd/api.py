@@ -7,7 +7,7 @@ _LIB = None
 
 QH_OK = 0
 STATUS = {0: "ok", -1: "unsupported ggml_type", -2: "bad dimensions", -3: "null pointer",
-          -4: "HIP runtime error", -5: "argument out of range"}
+          -4: "HIP runtime error", -5: "argument out of range", -6: "malformed GGUF file", -7: "file I/O error"}
 
 # ggml type id -> (name, elements per block, bytes per block); src/gguf.rs:172-191
 GGML_TYPES = {
@@ -23,7 +23,7 @@ TYPE_IDS = {v[0]: k for k, v in GGML_TYPES.items()}
 class QuartzHipError(RuntimeError):
     def __init__(self, fn, status):
         msg = f"{fn} -> {status} ({STATUS.get(status, '?')})"
-        if status == -4 and _LIB is not None:
+        if status in (-4, -6, -7) and _LIB is not None:
             msg += ": " + _LIB.hip_last_error().decode()
         super().__init__(msg)
         self.status = status
@@ -56,6 +56,35 @@ _SIGS = {
     "hip_gemm_moe": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int]),
     "hip_gemm_moe_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int,
                                                                                           C.c_void_p]),
+    "hip_gguf_open": (C.c_int, [C.c_char_p, C.c_void_p]),
+    "hip_gguf_close": (None, [C.c_void_p]),
+    "hip_gguf_version": (C.c_uint32, [C.c_void_p]),
+    "hip_gguf_data_offset": (C.c_uint64, [C.c_void_p]),
+    "hip_gguf_alignment": (C.c_uint64, [C.c_void_p]),
+    "hip_gguf_kv_count": (C.c_int64, [C.c_void_p]),
+    "hip_gguf_kv_key": (C.c_char_p, [C.c_void_p, C.c_int64]),
+    "hip_gguf_kv_type": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p]),
+    "hip_gguf_get_u32": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_u64": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_i64": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_f32": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_f64": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_str": (C.c_void_p, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "hip_gguf_get_array": (C.c_void_p, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p]),
+    "hip_gguf_get_array_str": (C.c_void_p, [C.c_void_p, C.c_char_p, C.c_uint64, C.c_void_p]),
+    "hip_gguf_tensor_count": (C.c_int64, [C.c_void_p]),
+    "hip_gguf_find_tensor": (C.c_int64, [C.c_void_p, C.c_char_p]),
+    "hip_gguf_tensor_info": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "hip_gguf_tensor_data": (C.c_void_p, [C.c_void_p, C.c_int64, C.c_void_p]),
+    "hip_gguf_upload": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "hip_gguf_writer_new": (C.c_void_p, []),
+    "hip_gguf_writer_free": (None, [C.c_void_p]),
+    "hip_gguf_writer_kv_scalar": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.c_void_p]),
+    "hip_gguf_writer_kv_str": (C.c_int, [C.c_void_p, C.c_char_p, C.c_char_p, C.c_uint64]),
+    "hip_gguf_writer_kv_array": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.c_void_p, C.c_uint64]),
+    "hip_gguf_writer_kv_array_str": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_uint64]),
+    "hip_gguf_writer_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p]),
+    "hip_gguf_writer_write": (C.c_int, [C.c_void_p, C.c_char_p]),
     "hip_gemv_moe4": (C.c_int, [C.c_uint32] + [C.c_void_p] * 12 + [C.c_int, C.c_int, C.c_int]),
     "hip_dequant": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t]),
     "hip_dequant_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),

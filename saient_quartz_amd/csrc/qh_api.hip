@@ -17,6 +17,9 @@ extern __device__ uint32_t qh_g_iq3s[512];
 
 static thread_local char qh_errbuf[256];
 
+// Message for hip_last_error() from host-side code (the GGUF reader/writer).
+void qh_set_error(const char* msg) { snprintf(qh_errbuf, sizeof qh_errbuf, "%s", msg); }
+
 bool qh_force_valu() {
     static const bool v = [] {
         const char* e = getenv("QUARTZ_HIP_KERNEL");
@@ -62,6 +65,8 @@ const char* hip_status_string(int s) {
         case QH_ERR_NULL: return "null device pointer";
         case QH_ERR_HIP: return "HIP runtime error";
         case QH_ERR_RANGE: return "argument out of range";
+        case QH_ERR_FORMAT: return "malformed or unsupported GGUF file";
+        case QH_ERR_IO: return "file I/O error";
         default: return "unknown status";
     }
 }

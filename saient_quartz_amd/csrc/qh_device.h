@@ -118,7 +118,8 @@ QH_DEV float qh_dot4u(const float* xv, uint32_t w, float s) {
 }
 
 // Spread the low 4 bits of t (t < 16) to bit 0 of each byte.
-QH_DEV uint32_t qh_spread4(uint32_t t) { return (t * 0x00204081u) & 0x01010101u; }
+// (t < 16 and 0x204081 < 2^24: the full-rate 24-bit multiply is exact here.)
+QH_DEV uint32_t qh_spread4(uint32_t t) { return __umul24(t, 0x00204081u) & 0x01010101u; }
 
 // Byte-wise conditional negation: bytes whose mask byte is 0xFF are negated
 // (g must have no zero bytes where negated, true for every IQ codebook entry).
@@ -128,7 +129,10 @@ QH_DEV uint32_t qh_negbytes(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01
 QH_DEV uint32_t qh_ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
 
 // 0xFF in byte j of the result for every set bit j (j < 4) of s.
-QH_DEV uint32_t qh_signmask4(uint32_t s4) { return qh_spread4(s4 & 0xFu) * 0xFFu; }
+QH_DEV uint32_t qh_signmask4(uint32_t s4) {
+    const uint32_t s = qh_spread4(s4 & 0xFu);
+    return (s << 8) - s;  // s * 0xFF, bytes 0 or 0xFF
+}
 
 // ---------------------------------------------------------------- reductions
 

@@ -59,4 +59,5 @@ hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float
                           hipStream_t st);
 hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                           int n, hipStream_t st);
+void qh_set_error(const char* msg);  // hip_last_error() text
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

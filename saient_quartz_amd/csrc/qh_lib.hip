@@ -8,3 +8,4 @@
 #include "qh_gemm.hip"
 #include "qh_gemv.hip"
 #include "qh_api.hip"
+#include "qh_gguf.hip"
