@@ -143,6 +143,59 @@ int hip_set_ksigns(const uint8_t* host);
 const char* hip_status_string(int status);
 const char* hip_last_error(void); /* last HIP error seen on this host thread ("" if none) */
 
+/* ---------------------------------------------------------------- decode-step glue
+ * The kernels between the GEMVs of a decode step, twins of the reference's
+ * forward-pass helpers (src/cuda_kernels.cu:1129-1290, Rust decls
+ * src/cuda.rs:20-55), same arguments and formulas; f32 results differ only by
+ * summation order (wave64 reductions).  Plain forms run on the default stream,
+ * _async forms on the given one.  hip_attention_decode is new: the three
+ * attention kernels fused into one launch (seq_len <= 16384; QH_ERR_RANGE past
+ * it), sinks may be NULL (no sink).  hip_embed_lookup decodes any supported type
+ * bit-exactly (the reference handles Q5_1, IQ4_NL and BF16). */
+int hip_vec_add(float* dst, const float* src, int n);                                  /* dst += src */
+int hip_vec_add_async(float* dst, const float* src, int n, void* stream);
+int hip_vec_scale_add(float* dst, const float* src, float scale, int n);                /* dst += scale*src */
+int hip_vec_scale_add_async(float* dst, const float* src, float scale, int n, void* stream);
+int hip_vec_zero(float* dst, int n);
+int hip_vec_zero_async(float* dst, int n, void* stream);
+int hip_rms_norm(float* out, const float* x, const float* w, int n);                    /* eps 1e-5; out may be x */
+int hip_rms_norm_async(float* out, const float* x, const float* w, int n, void* stream);
+int hip_rope_yarn(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx,
+                  int neox);
+int hip_rope_yarn_async(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale,
+                        int yarn_orig_ctx, int neox, void* stream);
+int hip_kv_append(float* k_cache, float* v_cache, const float* k, const float* v, int pos, int kv_dim);
+int hip_kv_append_async(float* k_cache, float* v_cache, const float* k, const float* v, int pos, int kv_dim,
+                        void* stream);
+int hip_attn_score(float* scores, const float* q, const float* k_cache, int seq_len, int head_dim, int kv_dim,
+                   int kv_head_off, float scale);
+int hip_softmax_sink(float* x, int n, float sink);                                     /* sink <= -1e29: none */
+int hip_attn_values(float* out, const float* scores, const float* v_cache, int seq_len, int head_dim, int kv_dim,
+                    int kv_head_off);
+int hip_attn_score_all(float* scores, const float* q, const float* k_cache, int n_heads, int n_kv_heads, int seq_len,
+                       int head_dim, int kv_dim, int max_seq, float scale);
+int hip_attn_score_all_async(float* scores, const float* q, const float* k_cache, int n_heads, int n_kv_heads,
+                             int seq_len, int head_dim, int kv_dim, int max_seq, float scale, void* stream);
+int hip_softmax_sink_all(float* scores, int n_heads, int seq_len, int max_seq, const float* sinks);
+int hip_softmax_sink_all_async(float* scores, int n_heads, int seq_len, int max_seq, const float* sinks,
+                               void* stream);
+int hip_attn_values_all(float* out, const float* scores, const float* v_cache, int n_heads, int n_kv_heads,
+                        int seq_len, int head_dim, int kv_dim, int max_seq);
+int hip_attn_values_all_async(float* out, const float* scores, const float* v_cache, int n_heads, int n_kv_heads,
+                              int seq_len, int head_dim, int kv_dim, int max_seq, void* stream);
+int hip_attention_decode(float* out, const float* q, const float* k_cache, const float* v_cache, const float* sinks,
+                         int n_heads, int n_kv_heads, int seq_len, int head_dim, int kv_dim, float scale);
+int hip_attention_decode_async(float* out, const float* q, const float* k_cache, const float* v_cache,
+                               const float* sinks, int n_heads, int n_kv_heads, int seq_len, int head_dim, int kv_dim,
+                               float scale, void* stream);
+int hip_swiglu(float* out, const float* gate, const float* up, int n);
+int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* stream);
+int hip_swiglu_oai(float* out, const float* gate, const float* up, int n);
+int hip_swiglu_oai_async(float* out, const float* gate, const float* up, int n, void* stream);
+int hip_embed_lookup(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim);
+int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim,
+                           void* stream);
+
 /* ---------------------------------------------------------------- GGUF
  * Reader for the weight container either side of the GEMV path: GgufFile
  * (src/gguf.rs:61-191).  hip_gguf_open memory-maps the file and parses the

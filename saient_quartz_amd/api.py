@@ -85,6 +85,35 @@ _SIGS = {
     "hip_gguf_writer_kv_array_str": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_uint64]),
     "hip_gguf_writer_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p]),
     "hip_gguf_writer_write": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "hip_vec_add": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int]),
+    "hip_vec_add_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "hip_vec_scale_add": (C.c_int, [C.c_void_p, C.c_void_p, C.c_float, C.c_int]),
+    "hip_vec_scale_add_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p]),
+    "hip_vec_zero": (C.c_int, [C.c_void_p, C.c_int]),
+    "hip_vec_zero_async": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
+    "hip_rms_norm": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]),
+    "hip_rms_norm_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "hip_rope_yarn": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int]),
+    "hip_rope_yarn_async": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int, C.c_void_p]),
+    "hip_kv_append": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+    "hip_kv_append_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "hip_attn_score_all": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    "hip_attn_score_all_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_void_p]),
+    "hip_softmax_sink_all": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "hip_softmax_sink_all_async": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "hip_attn_values_all": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "hip_attn_values_all_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "hip_attention_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    "hip_attention_decode_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_void_p]),
+    "hip_swiglu": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]),
+    "hip_swiglu_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "hip_swiglu_oai": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]),
+    "hip_swiglu_oai_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "hip_embed_lookup": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int]),
+    "hip_embed_lookup_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_void_p]),
+    "hip_attn_score": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    "hip_softmax_sink": (C.c_int, [C.c_void_p, C.c_int, C.c_float]),
+    "hip_attn_values": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int]),
     "hip_gemv_moe4": (C.c_int, [C.c_uint32] + [C.c_void_p] * 12 + [C.c_int, C.c_int, C.c_int]),
     "hip_dequant": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t]),
     "hip_dequant_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),

@@ -236,6 +236,168 @@ int hip_gemv_moe4(uint32_t type, const uint8_t* w0, const uint8_t* w1, const uin
     return QH_OK;
 }
 
+// ---------------------------------------------------------------- decode-step glue
+// Twins of the reference's forward-pass helpers (src/cuda_kernels.cu:1129-1290,
+// Rust decls src/cuda.rs:20-55); the plain forms run on the default stream.
+#define QH_GLUE(call, what)                                  \
+    do {                                                     \
+        hipError_t qh_e_ = (call);                           \
+        if (qh_e_ != hipSuccess) return qh_fail(qh_e_, what); \
+        return QH_OK;                                        \
+    } while (0)
+
+int hip_vec_add_async(float* dst, const float* src, int n, void* s) {
+    if (n > 0 && (!dst || !src)) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_vec(0, dst, src, 0.f, n, (hipStream_t)s), "hip_vec_add");
+}
+int hip_vec_add(float* dst, const float* src, int n) { return hip_vec_add_async(dst, src, n, nullptr); }
+int hip_vec_scale_add_async(float* dst, const float* src, float scale, int n, void* s) {
+    if (n > 0 && (!dst || !src)) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_vec(1, dst, src, scale, n, (hipStream_t)s), "hip_vec_scale_add");
+}
+int hip_vec_scale_add(float* dst, const float* src, float scale, int n) {
+    return hip_vec_scale_add_async(dst, src, scale, n, nullptr);
+}
+int hip_vec_zero_async(float* dst, int n, void* s) {
+    if (n > 0 && !dst) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_vec(2, dst, nullptr, 0.f, n, (hipStream_t)s), "hip_vec_zero");
+}
+int hip_vec_zero(float* dst, int n) { return hip_vec_zero_async(dst, n, nullptr); }
+
+int hip_rms_norm_async(float* out, const float* x, const float* w, int n, void* s) {
+    if (n <= 0) return n == 0 ? QH_OK : QH_ERR_DIMS;
+    if (!out || !x || !w) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_rms_norm(out, x, w, n, (hipStream_t)s), "hip_rms_norm");
+}
+int hip_rms_norm(float* out, const float* x, const float* w, int n) { return hip_rms_norm_async(out, x, w, n, nullptr); }
+
+int hip_rope_yarn_async(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale,
+                        int yarn_orig_ctx, int neox, void* s) {
+    if (n_heads < 0 || head_dim < 0 || head_dim % 2) return QH_ERR_DIMS;
+    if (n_heads * head_dim > 0 && !x) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_rope(x, n_heads, head_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, (hipStream_t)s),
+            "hip_rope_yarn");
+}
+int hip_rope_yarn(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx,
+                  int neox) {
+    return hip_rope_yarn_async(x, n_heads, head_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, nullptr);
+}
+
+int hip_kv_append_async(float* k_cache, float* v_cache, const float* k, const float* v, int pos, int kv_dim, void* s) {
+    if (pos < 0 || kv_dim < 0) return QH_ERR_DIMS;
+    if (kv_dim == 0) return QH_OK;
+    if (!k_cache || !v_cache || !k || !v) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_kv_append(k_cache, v_cache, k, v, pos, kv_dim, (hipStream_t)s), "hip_kv_append");
+}
+int hip_kv_append(float* k_cache, float* v_cache, const float* k, const float* v, int pos, int kv_dim) {
+    return hip_kv_append_async(k_cache, v_cache, k, v, pos, kv_dim, nullptr);
+}
+
+static int qh_attn_dims(int n_heads, int n_kv, int seq, int hd, int kv_dim, int max_seq) {
+    if (n_heads < 0 || n_kv <= 0 || seq < 0 || hd <= 0 || seq > max_seq) return QH_ERR_DIMS;
+    if ((int64_t)n_kv * hd > kv_dim) return QH_ERR_DIMS;
+    return QH_OK;
+}
+
+int hip_attn_score_all_async(float* scores, const float* q, const float* k_cache, int n_heads, int n_kv_heads,
+                             int seq_len, int head_dim, int kv_dim, int max_seq, float scale, void* s) {
+    int rc = qh_attn_dims(n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq);
+    if (rc) return rc;
+    if (n_heads && seq_len && (!scores || !q || !k_cache)) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_attn(0, scores, q, k_cache, nullptr, n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq,
+                         scale, (hipStream_t)s), "hip_attn_score_all");
+}
+int hip_attn_score_all(float* scores, const float* q, const float* k_cache, int n_heads, int n_kv_heads, int seq_len,
+                       int head_dim, int kv_dim, int max_seq, float scale) {
+    return hip_attn_score_all_async(scores, q, k_cache, n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq,
+                                    scale, nullptr);
+}
+int hip_softmax_sink_all_async(float* scores, int n_heads, int seq_len, int max_seq, const float* sinks, void* s) {
+    if (n_heads < 0 || seq_len < 0 || seq_len > max_seq) return QH_ERR_DIMS;
+    if (n_heads && seq_len && !scores) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_attn(1, scores, nullptr, nullptr, sinks, n_heads, 1, seq_len, 1, 1, max_seq, -1e30f,
+                         (hipStream_t)s), "hip_softmax_sink_all");
+}
+int hip_softmax_sink_all(float* scores, int n_heads, int seq_len, int max_seq, const float* sinks) {
+    return hip_softmax_sink_all_async(scores, n_heads, seq_len, max_seq, sinks, nullptr);
+}
+int hip_attn_values_all_async(float* out, const float* scores, const float* v_cache, int n_heads, int n_kv_heads,
+                              int seq_len, int head_dim, int kv_dim, int max_seq, void* s) {
+    int rc = qh_attn_dims(n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq);
+    if (rc) return rc;
+    if (n_heads && (!out || !scores || !v_cache)) return QH_ERR_NULL;
+    if (seq_len == 0) return hip_vec_zero_async(out, n_heads * head_dim, s);
+    QH_GLUE(qh_glue_attn(2, out, scores, v_cache, nullptr, n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq,
+                         0.f, (hipStream_t)s), "hip_attn_values_all");
+}
+int hip_attn_values_all(float* out, const float* scores, const float* v_cache, int n_heads, int n_kv_heads,
+                        int seq_len, int head_dim, int kv_dim, int max_seq) {
+    return hip_attn_values_all_async(out, scores, v_cache, n_heads, n_kv_heads, seq_len, head_dim, kv_dim, max_seq,
+                                     nullptr);
+}
+
+// Single-head forms (cuda_attn_score / cuda_softmax_sink / cuda_attn_values).
+int hip_attn_score(float* scores, const float* q, const float* k_cache, int seq_len, int head_dim, int kv_dim,
+                   int kv_head_off, float scale) {
+    if (kv_head_off < 0 || kv_head_off + head_dim > kv_dim) return QH_ERR_DIMS;
+    return hip_attn_score_all_async(scores, q, k_cache ? k_cache + kv_head_off : nullptr, 1, 1, seq_len, head_dim,
+                                    kv_dim, seq_len, scale, nullptr);
+}
+int hip_softmax_sink(float* x, int n, float sink) {
+    if (n < 0) return QH_ERR_DIMS;
+    if (n && !x) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_attn(1, x, nullptr, nullptr, nullptr, 1, 1, n, 1, 1, n, sink, nullptr), "hip_softmax_sink");
+}
+int hip_attn_values(float* out, const float* scores, const float* v_cache, int seq_len, int head_dim, int kv_dim,
+                    int kv_head_off) {
+    if (kv_head_off < 0 || kv_head_off + head_dim > kv_dim) return QH_ERR_DIMS;
+    return hip_attn_values_all_async(out, scores, v_cache ? v_cache + kv_head_off : nullptr, 1, 1, seq_len, head_dim,
+                                     kv_dim, seq_len, nullptr);
+}
+
+int hip_attention_decode_async(float* out, const float* q, const float* k_cache, const float* v_cache,
+                               const float* sinks, int n_heads, int n_kv_heads, int seq_len, int head_dim, int kv_dim,
+                               float scale, void* s) {
+    int rc = qh_attn_dims(n_heads, n_kv_heads, seq_len, head_dim, kv_dim, seq_len);
+    if (rc) return rc;
+    if (n_heads && (!out || !q || !k_cache || !v_cache)) return QH_ERR_NULL;
+    if (seq_len == 0) return hip_vec_zero_async(out, n_heads * head_dim, s);
+    hipError_t e = qh_glue_attention_decode(out, q, k_cache, v_cache, sinks, n_heads, n_kv_heads, seq_len, head_dim,
+                                            kv_dim, scale, (hipStream_t)s);
+    if (e == hipErrorNotSupported) return QH_ERR_RANGE;  // seq_len beyond the kernel's LDS score buffer
+    if (e != hipSuccess) return qh_fail(e, "hip_attention_decode");
+    return QH_OK;
+}
+int hip_attention_decode(float* out, const float* q, const float* k_cache, const float* v_cache, const float* sinks,
+                         int n_heads, int n_kv_heads, int seq_len, int head_dim, int kv_dim, float scale) {
+    return hip_attention_decode_async(out, q, k_cache, v_cache, sinks, n_heads, n_kv_heads, seq_len, head_dim, kv_dim,
+                                      scale, nullptr);
+}
+
+int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* s) {
+    if (n > 0 && (!out || !gate || !up)) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_swiglu(0, out, gate, up, n, (hipStream_t)s), "hip_swiglu");
+}
+int hip_swiglu(float* out, const float* gate, const float* up, int n) { return hip_swiglu_async(out, gate, up, n, nullptr); }
+int hip_swiglu_oai_async(float* out, const float* gate, const float* up, int n, void* s) {
+    if (n > 0 && (!out || !gate || !up)) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_swiglu(1, out, gate, up, n, (hipStream_t)s), "hip_swiglu_oai");
+}
+int hip_swiglu_oai(float* out, const float* gate, const float* up, int n) {
+    return hip_swiglu_oai_async(out, gate, up, n, nullptr);
+}
+
+int hip_embed_lookup_async(float* out, const uint8_t* data, uint32_t ggml_type, int token, int embed_dim, void* s) {
+    const int qk = qh_block_elems(ggml_type);
+    if (qk == 0) return QH_ERR_TYPE;
+    if (token < 0 || embed_dim <= 0 || embed_dim % qk) return QH_ERR_DIMS;
+    if (!out || !data) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_embed(out, data, ggml_type, token, embed_dim, (hipStream_t)s), "hip_embed_lookup");
+}
+int hip_embed_lookup(float* out, const uint8_t* data, uint32_t ggml_type, int token, int embed_dim) {
+    return hip_embed_lookup_async(out, data, ggml_type, token, embed_dim, nullptr);
+}
+
 int hip_dequant_async(uint32_t type, const uint8_t* W, float* out, size_t n, void* stream) {
     const int qk = qh_block_elems(type);
     if (qk == 0) return QH_ERR_TYPE;

@@ -7,5 +7,6 @@
 #include "qh_mmv16.hip"
 #include "qh_gemm.hip"
 #include "qh_gemv.hip"
+#include "qh_glue.hip"
 #include "qh_api.hip"
 #include "qh_gguf.hip"

@@ -1,0 +1,91 @@
+"""Closed-form pins of oracle/glue_ref.py (the checker of the glue kernels):
+properties the reference formulas fix, chosen so a dropped term, a swapped
+pair index or a wrong sign fails one of them.  CPU only."""
+import sys
+from pathlib import Path
+
+import numpy as np
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "oracle"))
+import glue_ref as g  # noqa: E402
+
+
+def test_rope_identity_at_pos0_and_norm_preserving():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(4 * 64)
+    for neox in (False, True):
+        assert np.allclose(g.rope_yarn(x, 4, 64, 0, 10000.0, neox=neox), x)
+        y = g.rope_yarn(x, 4, 64, 37, 10000.0, neox=neox).reshape(4, 64)
+        xr = x.reshape(4, 64)
+        if neox:
+            pn = lambda a: a[:, :32] ** 2 + a[:, 32:] ** 2
+        else:
+            pn = lambda a: a[:, 0::2] ** 2 + a[:, 1::2] ** 2
+        assert np.allclose(pn(y), pn(xr))
+
+
+def test_rope_pairing_and_angle():
+    # one head, head_dim 4: pair 0 has inv_freq 1, pair 1 has theta^-0.5
+    x = np.array([1.0, 0.0, 0.0, 0.0])
+    y = g.rope_yarn(x, 1, 4, 2, 100.0, neox=False)  # NORM: pair (0, 1), angle 2
+    assert np.allclose(y, [np.cos(2), np.sin(2), 0, 0])
+    y = g.rope_yarn(x, 1, 4, 2, 100.0, neox=True)  # NEOX: pair (0, 2)
+    assert np.allclose(y, [np.cos(2), 0, np.sin(2), 0])
+    x = np.array([0.0, 1.0, 0.0, 0.0])
+    y = g.rope_yarn(x, 1, 4, 3, 100.0, neox=True)  # pair 1: (1, 3), inv_freq 0.1
+    assert np.allclose(y, [0, np.cos(0.3), 0, np.sin(0.3)])
+
+
+def test_yarn_ramp_limits():
+    # wavelengths far below hfw keep inv_freq; far above lfw divide by the scale
+    x = np.zeros(2 * 64)
+    x[0] = 1.0
+    x[62] = 1.0  # the last (longest) pair of head 0 in NORM pairing
+    a = g.rope_yarn(x, 2, 64, 5, 1e6, yarn_scale=4.0, yarn_orig_ctx=4096)
+    b = g.rope_yarn(x, 2, 64, 5, 1e6)
+    assert np.allclose(a[:2], b[:2])  # pair 0: wavelen 2*pi < hfw = 128 -> unchanged
+    inv_last = 1e6 ** (-62 / 64)
+    assert np.allclose(a[62:64], [np.cos(5 * inv_last / 4), np.sin(5 * inv_last / 4)])
+
+
+def test_rms_norm_constant_and_scale():
+    w = np.linspace(0.5, 2.0, 16)
+    y = g.rms_norm(np.full(16, -3.0), w)
+    assert np.allclose(y, -w * 3.0 / np.sqrt(9.0 + 1e-5))
+    x = np.random.default_rng(2).standard_normal(16)
+    assert np.allclose(g.rms_norm(2 * x, w), g.rms_norm(x, w), rtol=1e-5)
+
+
+def test_softmax_sink():
+    x = np.array([1.0, 2.0, -1.0])
+    p = g.softmax_sink(x)
+    assert np.isclose(p.sum(), 1.0) and np.allclose(p, np.exp(x) / np.exp(x).sum())
+    q = g.softmax_sink(x, 0.5)
+    assert np.isclose(q.sum(), 1.0 - np.exp(0.5) / (np.exp(x).sum() + np.exp(0.5)))
+    assert np.allclose(g.softmax_sink(x, -1e30), p)
+
+
+def test_attention_one_token_and_gqa_mapping():
+    rng = np.random.default_rng(3)
+    hd, nh, nkv = 8, 4, 2
+    kc = rng.standard_normal((5, nkv * hd))
+    vc = rng.standard_normal((5, nkv * hd))
+    q = rng.standard_normal(nh * hd)
+    _, out = g.attention(q, kc, vc, nh, nkv, 1, hd, nkv * hd, 0.3)
+    for h in range(nh):
+        kvh = h * nkv // nh
+        assert np.allclose(out[h * hd:(h + 1) * hd], vc[0, kvh * hd:(kvh + 1) * hd])
+    probs, out = g.attention(q, kc, vc, nh, nkv, 5, hd, nkv * hd, 0.3)
+    h = 3  # kv head 1
+    s = kc[:, hd:] @ q[3 * hd:] * 0.3
+    p = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
+    assert np.allclose(probs[h], p) and np.allclose(out[3 * hd:], p @ vc[:, hd:])
+
+
+def test_swiglu_forms():
+    gg = np.array([-3.0, 0.0, 2.0, 9.0])
+    assert np.allclose(g.swiglu(gg, np.ones(4)), gg / (1 + np.exp(-gg)))
+    assert np.allclose(g.swiglu(np.zeros(4), gg), 0.0)
+    o = g.swiglu_oai(gg, np.array([0.0, 1.0, 8.0, -9.0]))
+    assert np.isclose(o[3], 7 / (1 + np.exp(-1.702 * 7)) * (-7 + 1))
+    assert np.isclose(o[2], 2 / (1 + np.exp(-3.404)) * 8.0)
