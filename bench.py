@@ -168,6 +168,8 @@ def decode_leg(torch, reps):
     out = {"workload": "Llama-3-8B-shaped Q4_K_M decode step, weight GEMVs only (32 layers x q,k,v,o,gate,up,down "
                        "+ Q6_K head), random-init weights, synthetic activations",
            "weight_bytes": wbytes, "roofline_tok_s_n1": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)}
+    full = forward_leg(torch, reps, wbytes)
+    out.update(full)
     for n, fuse in ((1, False), (1, True), (4, True), (16, True)):
         g = torch.cuda.CUDAGraph()
         step.issue(n, fuse=fuse)  # eager warm-up (first-call device queries happen outside capture)
@@ -187,6 +189,44 @@ def decode_leg(torch, reps):
         out[f"n{n}" + ("" if fuse or n > 1 else "_unfused")] = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
                         "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
                         "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+        del g
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
+def forward_leg(torch, reps, wbytes):
+    """End-to-end Llama-3-8B-shaped decode step (ForwardStep: embedding lookup,
+    32 x [fused norm + q/k/v, RoPE + KV append + attention, o + residual, fused
+    norm + gate/up, swiglu, down + residual], fused final norm + head), one HIP
+    graph per position, timed over `reps` replays at KV position 0 and 511."""
+    from saient_quartz_amd.decode import ForwardStep, ModelConfig
+
+    cfg = ModelConfig(max_seq=1024)
+    step = ForwardStep(cfg, ForwardStep.random_weights(cfg))
+    out = {}
+    for pos in (0, 511):
+        step.issue(1, pos)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step.issue(1, pos)
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.isfinite(step.logits).all():
+            raise SystemExit("decode step produced non-finite logits")
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / reps
+        out[f"n1_full_pos{pos}"] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+                                    "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                                    "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+                                    "launches": 1 + 7 * cfg.layers + 1}
         del g
     del step
     torch.cuda.empty_cache()

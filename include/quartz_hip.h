@@ -67,6 +67,23 @@ int hip_gemv_multi(uint32_t ggml_type, int count, const uint8_t* const* W, float
 int hip_gemv_multi_async(uint32_t ggml_type, int count, const uint8_t* const* W, float* const* y,
                          const int* out_dims, const float* d_x, int in_dim, void* stream);
 
+/* y[k] (op)= W[k] x' for k < count (1..4) matrices sharing x, type and in_dim,
+ * with the decode step's neighbours of a GEMV fused in:
+ *   norm_w != NULL: x' = rms_norm(x) * norm_w (eps 1e-5), the reference's
+ *     cuda_rms_norm before the q/k/v, gate/up and lm_head GEMVs
+ *     (src/cuda.rs:549-562, :729-733, :773-781, :824-833);
+ *   accumulate != 0: y[k] += W[k] x' instead of =, the residual cuda_vec_add
+ *     after the o and down GEMVs (src/cuda.rs:647-662, :782-799).
+ * One launch for Q4_K/Q5_K/Q6_K when the norm's x fits one workgroup
+ * (in_dim <= 4096) or without the norm; otherwise the separate kernels run on
+ * `scratch` (device, in_dim + max(out_dims) floats; may be NULL when the fused
+ * kernel applies, QH_ERR_NULL if it was needed).  x must not alias any y[k].
+ * Results are within the GEMV tolerance of the separate-kernel sequence (the
+ * row scale rsqrt(mean(x^2)+eps) is applied after the dot instead of before). */
+int hip_gemv_fused_async(uint32_t ggml_type, int count, const uint8_t* const* W, float* const* y,
+                         const int* out_dims, const float* d_x, const float* norm_w, int accumulate, int in_dim,
+                         float* scratch, void* stream);
+
 /* Y[t][j] = sum_k W[j,k] X[t][k] for t < n (token-major).  GPU counterpart of
  * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv.  For n >= 2 the
  * matrix-core path reads the weights once per 16 tokens (see the note above on
@@ -192,6 +209,23 @@ int hip_swiglu(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* stream);
 int hip_swiglu_oai(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_oai_async(float* out, const float* gate, const float* up, int n, void* stream);
+/* The attention block of one decode step in one launch: RoPE (as hip_rope_yarn)
+ * on q (n_heads heads) and k (n_kv_heads heads), the K/V-cache append of the
+ * rotated k and of v at row pos (as hip_kv_append), then attention over pos + 1
+ * cached positions (as hip_attention_decode; sinks may be NULL).  Replaces the
+ * reference's cuda_rope_yarn x2 + cuda_kv_append + cuda_attn_score_all +
+ * cuda_softmax_sink_all + cuda_attn_values_all (src/cuda.rs:614-645, no sliding
+ * window).  q and k are not modified; out gets n_heads * head_dim floats.
+ * The sequence is split into 32-row slices over up to 64 workgroups per kv
+ * head whose partial softmax states are merged through the library's static
+ * device scratch (4 MB, per device; calls that overlap on one device race).
+ * Limits (else QH_ERR_RANGE): head_dim and kv_dim multiples of 4, head_dim <=
+ * 256, <= 16 q heads per kv head, n_kv_heads <= 256, k_cache / v_cache 16-byte
+ * aligned. */
+int hip_attention_step_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                             float* v_cache, const float* sinks, int n_heads, int n_kv_heads, int head_dim,
+                             int kv_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox,
+                             float scale, void* stream);
 int hip_embed_lookup(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim);
 int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim,
                            void* stream);

@@ -110,7 +110,7 @@ int hip_gemv_multi_async(uint32_t type, int count, const uint8_t* const* W, floa
     }
     if (!x) return QH_ERR_NULL;
     if (!qh_force_valu()) {
-        hipError_t e = qh_launch_mmv16_multi(type, W, y, out_dims, count, x, in_dim, st);
+        hipError_t e = qh_launch_mmv16_multi(type, W, y, out_dims, count, x, in_dim, st, nullptr, 0);
         if (e == hipSuccess) return QH_OK;
         if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemv_multi");
     }
@@ -125,6 +125,52 @@ int hip_gemv_multi_async(uint32_t type, int count, const uint8_t* const* W, floa
 int hip_gemv_multi(uint32_t type, int count, const uint8_t* const* W, float* const* y, const int* out_dims,
                    const float* x, int in_dim) {
     return hip_gemv_multi_async(type, count, W, y, out_dims, x, in_dim, nullptr);
+}
+
+int hip_gemv_fused_async(uint32_t type, int count, const uint8_t* const* W, float* const* y, const int* out_dims,
+                         const float* x, const float* norm_w, int accumulate, int in_dim, float* scratch,
+                         void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 1 || count > 4 || !W || !y || !out_dims) return QH_ERR_RANGE;
+    if (!norm_w && !accumulate) return hip_gemv_multi_async(type, count, W, y, out_dims, x, in_dim, stream);
+    const int qk = qh_block_elems(type);
+    if (qk == 0) {
+        int rc = QH_ERR_TYPE;
+        for (int k = 0; k < count; k++)
+            rc = qh_unknown_type("hip_gemv_fused", type, out_dims[k] > 0 ? y[k] : nullptr,
+                                 (size_t)(out_dims[k] > 0 ? out_dims[k] : 0), st);
+        return rc;
+    }
+    int max_out = 0;
+    for (int k = 0; k < count; k++) {
+        int rc = qh_check_dims(type, in_dim, out_dims[k]);
+        if (rc) return rc;
+        if (out_dims[k] > 0 && (!W[k] || !y[k])) return QH_ERR_NULL;
+        if (out_dims[k] > max_out) max_out = out_dims[k];
+    }
+    if (!x) return QH_ERR_NULL;
+    if (!qh_force_valu()) {
+        hipError_t e = qh_launch_mmv16_multi(type, W, y, out_dims, count, x, in_dim, st, norm_w, accumulate ? 1 : 0);
+        if (e == hipSuccess) return QH_OK;
+        if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemv_fused");
+    }
+    // No fused kernel for this type/shape: the reference's sequence of separate
+    // kernels, through the caller's scratch (in_dim + max out_dim floats).
+    if (!scratch) return QH_ERR_NULL;
+    const float* xs = x;
+    if (norm_w) {
+        QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st), "hip_gemv_fused");
+        xs = scratch;
+    }
+    for (int k = 0; k < count; k++) {
+        if (out_dims[k] == 0) continue;
+        float* out = accumulate ? scratch + in_dim : y[k];
+        int rc = hip_gemv_async(type, W[k], xs, out, in_dim, out_dims[k], stream);
+        if (rc) return rc;
+        if (accumulate) QH_CHECK(qh_glue_vec(0, y[k], out, 0.f, out_dims[k], st), "hip_gemv_fused");
+    }
+    (void)max_out;
+    return QH_OK;
 }
 
 int hip_gemm_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
@@ -372,6 +418,23 @@ int hip_attention_decode(float* out, const float* q, const float* k_cache, const
                          int n_heads, int n_kv_heads, int seq_len, int head_dim, int kv_dim, float scale) {
     return hip_attention_decode_async(out, q, k_cache, v_cache, sinks, n_heads, n_kv_heads, seq_len, head_dim, kv_dim,
                                       scale, nullptr);
+}
+
+int hip_attention_step_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                             float* v_cache, const float* sinks, int n_heads, int n_kv_heads, int head_dim,
+                             int kv_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox,
+                             float scale, void* s) {
+    if (pos < 0) return QH_ERR_DIMS;
+    int rc = qh_attn_dims(n_heads, n_kv_heads, pos + 1, head_dim, kv_dim, pos + 1);
+    if (rc) return rc;
+    if (n_kv_heads > n_heads && n_heads > 0) return QH_ERR_DIMS;
+    if (n_heads == 0) return QH_OK;
+    if (!out || !q || !k || !v || !k_cache || !v_cache) return QH_ERR_NULL;
+    hipError_t e = qh_glue_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_heads, n_kv_heads, head_dim,
+                                          kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, (hipStream_t)s);
+    if (e == hipErrorNotSupported) return QH_ERR_RANGE;
+    if (e != hipSuccess) return qh_fail(e, "hip_attention_step");
+    return QH_OK;
 }
 
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* s) {

@@ -78,12 +78,13 @@ __global__ __launch_bounds__(1024) void qg_rms_norm(float* out, const float* x, 
 // of a head rotates (i, i + head_dim/2) (NEOX) or (2i, 2i+1) (NORM) by pos *
 // inv_freq(i), inv_freq ramped between theta^(-2i/d) and that / yarn_scale for
 // YaRN (beta_fast 32, beta_slow 1).  One thread per pair.
-__global__ __launch_bounds__(256) void qg_rope_yarn(float* x, int n_pairs, int head_dim, int pos, float theta,
-                                                    float yarn_scale, int yarn_orig_ctx, int neox) {
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= n_pairs) return;
-    const int half = head_dim >> 1, head = p / half, i = p - head * half;
-    float* xh = x + (size_t)head * head_dim;
+// Rotation of pair i of one head: (x[i0], x[i1]) -> by pos * inv_freq(i).
+struct QgRot {
+    int i0, i1;
+    float c, s;
+};
+QH_DEV QgRot qg_rope_rot(int i, int head_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox) {
+    const int half = head_dim >> 1;
     const float std_inv = 1.f / powf(theta, 2.f * (float)i / (float)head_dim);
     float eff_inv = std_inv;
     if (yarn_scale > 1.f && yarn_orig_ctx > 0) {
@@ -92,12 +93,23 @@ __global__ __launch_bounds__(256) void qg_rope_yarn(float* x, int n_pairs, int h
         const float ramp = fmaxf(0.f, fminf(1.f, (lfw - wavelen) / (lfw - hfw)));
         eff_inv = ramp * std_inv + (1.f - ramp) * (std_inv / yarn_scale);
     }
-    float s, c;
-    sincosf((float)pos * eff_inv, &s, &c);
-    const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
-    const float x0 = xh[i0], x1 = xh[i1];
-    xh[i0] = x0 * c - x1 * s;
-    xh[i1] = x0 * s + x1 * c;
+    QgRot r;
+    sincosf((float)pos * eff_inv, &r.s, &r.c);
+    r.i0 = neox ? i : 2 * i;
+    r.i1 = neox ? i + half : 2 * i + 1;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void qg_rope_yarn(float* x, int n_pairs, int head_dim, int pos, float theta,
+                                                    float yarn_scale, int yarn_orig_ctx, int neox) {
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= n_pairs) return;
+    const int half = head_dim >> 1, head = p / half, i = p - head * half;
+    float* xh = x + (size_t)head * head_dim;
+    const QgRot r = qg_rope_rot(i, head_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox);
+    const float x0 = xh[r.i0], x1 = xh[r.i1];
+    xh[r.i0] = x0 * r.c - x1 * r.s;
+    xh[r.i1] = x0 * r.s + x1 * r.c;
 }
 
 __global__ __launch_bounds__(256) void qg_kv_append(float* kc, float* vc, const float* k, const float* v, int pos,
@@ -208,6 +220,229 @@ __global__ __launch_bounds__(256) void qg_attention_decode(float* out, const flo
     }
 }
 
+// One decode step's attention block in one launch, split over the sequence
+// (flash decoding).  Workgroup (g, c) takes kv head g with every q head that
+// maps to it (kv_head(h) = h * n_kv / n_heads, a contiguous range of h) and the
+// 32-row slices c, c + nch, ... of the pos + 1 cached rows:
+//   * RoPE of its q heads (qg_rope_rot, as qg_rope_yarn) into LDS;
+//   * the workgroup owning row pos rotates k, appends k and v to the cache at
+//     row pos and uses them from LDS / v for that row (the others read rows
+//     < pos only, so nobody waits for the append);
+//   * per slice: K and V rows into LDS once for all the group's heads, scores
+//     (wavefront = q head, lane = row x half of head_dim), an online softmax
+//     (running max m, sum l, output o; lane owns dims lane + 64 j);
+//   * (m, l, o) per head go to the library's partial scratch with agent-scope
+//     stores; the last workgroup of kv head g to arrive (per-g counter, back at
+//     zero when it is done) merges them: M = max m_c, L = sum l_c e^(m_c - M)
+//     (+ e^(sink - M)), out = sum o_c e^(m_c - M) / L.
+// Same mathematics as cuda_attn_score_all + cuda_softmax_sink_all +
+// cuda_attn_values_all (src/cuda_kernels.cu:1199-1266); the sums are grouped by
+// slice, so f32 results differ from them by rounding only.
+#define QA_ROWS 32       // rows per slice
+#define QA_MAXCH 64      // slices in flight per kv head
+#define QA_MAXHD 256     // head_dim
+#define QA_MAXG 16       // q heads per kv head
+#define QA_MAXKV 256     // kv heads (arrival counters)
+#define QA_PART (1 << 20)  // partial scratch, floats
+static __device__ __align__(256) float qa_part[QA_PART];
+static __device__ __align__(256) unsigned int qa_cnt[QA_MAXKV];
+
+__global__ __launch_bounds__(256) void qg_attention_step(float* out, const float* q, const float* k, const float* v,
+                                                         float* kc, float* vc, const float* sinks, int n_heads,
+                                                         int n_kv, int hd, int kv_dim, int pos, float theta,
+                                                         float yarn_scale, int orig_ctx, int neox, float scale,
+                                                         float* part, unsigned int* cnt) {
+    __shared__ __align__(16) float kl[QA_ROWS * (QA_MAXHD + 4)];
+    __shared__ __align__(16) float vl[QA_ROWS * QA_MAXHD];
+    __shared__ __align__(16) float qr[QA_MAXG * QA_MAXHD];
+    __shared__ __align__(16) float kr[QA_MAXHD];
+    __shared__ int last_flag;
+    const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int h0 = (g * n_heads + n_kv - 1) / n_kv, h1 = ((g + 1) * n_heads + n_kv - 1) / n_kv, ng = h1 - h0;
+    const int seq = pos + 1, half = hd >> 1, kp = hd + 4;
+    const bool owner = ((pos / QA_ROWS) % nch) == c;
+    const float* kh = k + (size_t)g * hd;
+    const float* vh = v + (size_t)g * hd;
+    for (int p = threadIdx.x; p < ng * half; p += 256) {
+        const int j = p / half, i = p - j * half;
+        const QgRot r = qg_rope_rot(i, hd, pos, theta, yarn_scale, orig_ctx, neox);
+        const float* qh = q + (size_t)(h0 + j) * hd;
+        const float q0 = qh[r.i0], q1 = qh[r.i1];
+        qr[j * hd + r.i0] = q0 * r.c - q1 * r.s;
+        qr[j * hd + r.i1] = q0 * r.s + q1 * r.c;
+        if (owner && j == 0) {
+            const float k0 = kh[r.i0], k1 = kh[r.i1];
+            kr[r.i0] = k0 * r.c - k1 * r.s;
+            kr[r.i1] = k0 * r.s + k1 * r.c;
+        }
+    }
+    __syncthreads();
+    if (owner) {
+        float* kd = kc + (size_t)pos * kv_dim + (size_t)g * hd;
+        float* vd = vc + (size_t)pos * kv_dim + (size_t)g * hd;
+        for (int i = threadIdx.x; i < hd; i += 256) {
+            kd[i] = kr[i];
+            vd[i] = vh[i];
+        }
+    }
+    // running state of this wavefront's heads j = w, w + 4, ... (< ng)
+    float m[QA_MAXG / 4], l[QA_MAXG / 4], o[QA_MAXG / 4][QA_MAXHD / 64];
+#pragma unroll
+    for (int a = 0; a < QA_MAXG / 4; a++) {
+        m[a] = -1e30f;
+        l[a] = 0.f;
+#pragma unroll
+        for (int d = 0; d < QA_MAXHD / 64; d++) o[a][d] = 0.f;
+    }
+    const int t_l = lane & 31, hsel = lane >> 5;
+    for (int sl = c; sl * QA_ROWS < seq; sl += nch) {
+        const int t0 = sl * QA_ROWS, nv = min(QA_ROWS, seq - t0);
+        // K and V rows t0 .. t0 + nv - 1 into LDS (row pos from kr / v)
+        const int q4 = hd >> 2;
+        for (int i = threadIdx.x; i < nv * q4; i += 256) {
+            const int r = i / q4, c4 = i - r * q4, t = t0 + r;
+            float4 kk, vv;
+            if (t < pos) {
+                kk = *reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
+                vv = *reinterpret_cast<const float4*>(vc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
+            } else {
+                kk = *reinterpret_cast<const float4*>(kr + 4 * c4);
+                vv = float4{vh[4 * c4], vh[4 * c4 + 1], vh[4 * c4 + 2], vh[4 * c4 + 3]};
+            }
+            *reinterpret_cast<float4*>(kl + r * kp + 4 * c4) = kk;
+            *reinterpret_cast<float4*>(vl + r * hd + 4 * c4) = vv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < QA_MAXG / 4; a++) {
+            const int j = w + 4 * a;
+            if (j >= ng) break;  // uniform per wavefront
+            // score of row t_l: half hsel of the dot, then the two halves summed
+            const float* qj = qr + j * hd + hsel * half;
+            const float* kt = kl + t_l * kp + hsel * half;
+            float sdot = 0.f;
+            for (int i = 0; i < half; i += 4) {
+                const float4 kk = *reinterpret_cast<const float4*>(kt + i);
+                const float4 qq = *reinterpret_cast<const float4*>(qj + i);
+                sdot += (qq.x * kk.x + qq.y * kk.y) + (qq.z * kk.z + qq.w * kk.w);
+            }
+            sdot += __shfl_xor(sdot, 32);
+            const float sc = t_l < nv ? sdot * scale : -1e30f;
+            float mx = sc;
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float mn = fmaxf(m[a], mx);
+            const float corr = expf(m[a] - mn);
+            const float p = t_l < nv ? expf(sc - mn) : 0.f;
+            float ps = p;
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) ps += __shfl_xor(ps, off);
+            l[a] = l[a] * corr + ps;
+            m[a] = mn;
+#pragma unroll
+            for (int d = 0; d < QA_MAXHD / 64; d++) o[a][d] *= corr;
+            for (int t = 0; t < nv; t++) {
+                const float pt = __shfl(p, t);
+#pragma unroll
+                for (int d = 0; d < QA_MAXHD / 64; d++) {
+                    const int dd = lane + 64 * d;
+                    if (dd < hd) o[a][d] = fmaf(pt, vl[t * hd + dd], o[a][d]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    auto finish = [&](int j, float mm, float ll, const float* oo, bool from_part) {
+        (void)from_part;
+        const int h = h0 + j;
+        const float sink = sinks ? sinks[h] : -1e30f;
+        float M = mm;
+        if (sink > -1e29f) M = fmaxf(M, sink);
+        const float L = ll * expf(mm - M) + (sink > -1e29f ? expf(sink - M) : 0.f);
+        const float f = expf(mm - M) / L;
+#pragma unroll
+        for (int d = 0; d < QA_MAXHD / 64; d++) {
+            const int dd = lane + 64 * d;
+            if (dd < hd) out[(size_t)h * hd + dd] = oo[d] * f;
+        }
+    };
+    if (nch == 1) {
+#pragma unroll
+        for (int a = 0; a < QA_MAXG / 4; a++) {
+            const int j = w + 4 * a;
+            if (j >= ng) break;
+            finish(j, m[a], l[a], o[a], false);
+        }
+        return;
+    }
+    // partial record of (head h, slice c): [m, l, o[0 .. hd)]
+    const int rec = hd + 2;
+#pragma unroll
+    for (int a = 0; a < QA_MAXG / 4; a++) {
+        const int j = w + 4 * a;
+        if (j >= ng) break;
+        float* pr = part + ((size_t)(h0 + j) * nch + c) * rec;
+        if (lane == 0) {
+            __hip_atomic_store(pr, m[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pr + 1, l[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int d = 0; d < QA_MAXHD / 64; d++) {
+            const int dd = lane + 64 * d;
+            if (dd < hd) __hip_atomic_store(pr + 2 + dd, o[a][d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // Every thread's partial stores have completed before the counter moves.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_flag = __hip_atomic_fetch_add(&cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (unsigned)(nch - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    // Merge.  The partials are read with SC1 buffer loads (the coherence bit of
+    // an agent-scope load, so no stale L2 line of another launch is seen), which
+    // unlike atomic loads issue back to back: lane cc holds slice cc's (m, l).
+    const QhBuf pb = qh_buf(part, 4u * QA_PART);
+    for (int j = w; j < ng; j += 4) {
+        const uint32_t base = 4u * (uint32_t)((size_t)(h0 + j) * nch * rec);
+        const bool on = lane < nch;
+        const float mc = on ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pb.rs, (int)(base + 4u * lane * rec), 0, 16)) : -1e30f;
+        const float lc = on ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pb.rs, (int)(base + 4u * (lane * rec + 1)), 0, 16)) : 0.f;
+        float M = mc;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float e = on ? expf(mc - M) : 0.f;
+        float L = lc * e;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+        float oo[QA_MAXHD / 64];
+#pragma unroll
+        for (int d = 0; d < QA_MAXHD / 64; d++) oo[d] = 0.f;
+        for (int c0 = 0; c0 < nch; c0 += 8) {
+            // eight slices' loads in flight before any of them is used
+            float ov[8][QA_MAXHD / 64];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int d = 0; d < QA_MAXHD / 64; d++) {
+                    const int dd = lane + 64 * d, cc = c0 + u;
+                    const uint32_t off = (cc < nch && dd < hd) ? base + 4u * (cc * rec + 2 + dd) : 0x80000000u;
+                    ov[u][d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pb.rs, (int)off, 0, 16));
+                }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float ec = __shfl(e, (c0 + u) & 63);
+#pragma unroll
+                for (int d = 0; d < QA_MAXHD / 64; d++) oo[d] = fmaf(c0 + u < nch ? ov[u][d] : 0.f, ec, oo[d]);
+            }
+        }
+        finish(j, M, L, oo, true);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+}
+
 // silu(gate) * up (swiglu_f32, :670-676) and the clamped gpt-oss form
 // (swiglu_oai_f32, :660-668).
 __global__ __launch_bounds__(256) void qg_swiglu(float* out, const float* gate, const float* up, int n) {
@@ -286,6 +521,45 @@ hipError_t qh_glue_attention_decode(float* out, const float* q, const float* kc,
     if (seq <= 0 || n_heads <= 0) return hipSuccess;
     hipLaunchKernelGGL(qg_attention_decode, dim3(n_heads), dim3(256), 0, st, out, q, kc, vc, sinks, n_heads, n_kv,
                        seq, hd, kv_dim, scale);
+    return hipGetLastError();
+}
+
+// Device addresses of the attention scratch, per device (hipGetSymbolAddress once).
+struct QaScratch { float* part; unsigned int* cnt; };
+static const QaScratch* qa_scratch_ptrs() {
+    static QaScratch ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    QaScratch& p = ptrs[dev];
+    if (!p.part) {
+        void *a = nullptr, *b = nullptr;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qa_part)) != hipSuccess ||
+            hipGetSymbolAddress(&b, HIP_SYMBOL(qa_cnt)) != hipSuccess)
+            return nullptr;
+        p.cnt = static_cast<unsigned int*>(b);
+        p.part = static_cast<float*>(a);
+    }
+    return &p;
+}
+
+hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
+                                  const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
+                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st) {
+    if (pos < 0 || hd <= 0 || (hd & 3) || hd > QA_MAXHD || n_kv > QA_MAXKV || (kv_dim & 3) ||
+        ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)k & 15))
+        return hipErrorNotSupported;
+    if (n_heads <= 0) return hipSuccess;
+    // q heads per kv head (the largest group)
+    if ((n_heads + n_kv - 1) / n_kv > QA_MAXG) return hipErrorNotSupported;
+    const QaScratch* sc = qa_scratch_ptrs();
+    if (!sc) return hipErrorInvalidDevice;
+    const int slices = (pos + QA_ROWS) / QA_ROWS;
+    int nch = slices < QA_MAXCH ? slices : QA_MAXCH;
+    const int cap = QA_PART / (n_heads * (hd + 2));
+    if (nch > cap) nch = cap;
+    if (nch < 1) nch = 1;
+    hipLaunchKernelGGL(qg_attention_step, dim3(n_kv, nch), dim3(256), 0, st, out, q, k, v, kc, vc, sinks, n_heads,
+                       n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale, sc->part, sc->cnt);
     return hipGetLastError();
 }
 

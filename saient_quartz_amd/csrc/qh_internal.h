@@ -49,7 +49,7 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
                                  float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st);
 hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
-                                 const float* x, int in_dim, hipStream_t st);
+                                 const float* x, int in_dim, hipStream_t st, const float* norm_w, int accum);
 hipError_t qh_launch_mmv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                          hipStream_t st);
 // QUARTZ_HIP_KERNEL=valu selects the lane-per-unit VALU kernels instead of the
@@ -71,6 +71,9 @@ hipError_t qh_glue_attn(int op, float* dst, const float* a, const float* b, cons
                         int n_kv, int seq, int hd, int kv_dim, int max_seq, float scale, hipStream_t st);
 hipError_t qh_glue_attention_decode(float* out, const float* q, const float* kc, const float* vc, const float* sinks,
                                     int n_heads, int n_kv, int seq, int hd, int kv_dim, float scale, hipStream_t st);
+hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
+                                  const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
+                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st);
 hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* up, int n, hipStream_t st);
 hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st);  // hip_last_error() text
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

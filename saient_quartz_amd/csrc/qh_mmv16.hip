@@ -196,6 +196,13 @@ struct QhMats {
     uint32_t wbytes[QH_MULTI];  // record count of each matrix's buffer range
     int rows[QH_MULTI];
     int tstart[QH_MULTI + 1];   // tstart[nm] = total tiles; entries past nm are INT_MAX
+    // Fused prologue / epilogue of a decode step:
+    //   nw != null: x is replaced by rms_norm(x) * nw (eps 1e-5) -- the kernel
+    //     digitises x * nw and scales each row by rsqrt(mean(x^2) + eps), the sum
+    //     of squares coming from the workgroup's own x loads (K fits one chunk);
+    //   accum: y += result instead of y = result (the residual add).
+    const float* nw;
+    int accum;
 };
 
 template <class F, int W, int GPW, bool X1, bool MULTI>
@@ -208,13 +215,14 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     // Wavefront partials of finished tiles wait in a ring of two sets of QH_RING
     // tiles; the workgroup meets at a barrier only when a set is full.
     __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 +
-                                               QH_MAXT * 16 * 4];
+                                               QH_MAXT * 16 * 4 + W * 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
     unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
     unsigned char* xl = lds + W * GPW * TILE + w * (GPW * QH_XG);
     float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
     float* res = red + 2 * QH_RING * W * 16;  // finished rows of this workgroup's tiles
+    float* sqw = res + QH_MAXT * 16;           // per-wavefront sums of x^2 (fused RMS norm)
     const int ntiles = mm.tstart[QH_MULTI];
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
@@ -278,6 +286,49 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
             const qh_u32x4 v = qh_ld128(xb, 1024u * (uint32_t)(g0 + t) + 16u * lane);
             xo[t] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
         }
+    };
+    // Fused RMS norm (X1 only): this wavefront's sum of x^2 goes to sqw[w] and x
+    // becomes x * nw.  The row scale rsqrt(mean + eps) is applied at the end.
+    auto load_nw = [&](qh_u32x4* nv) {
+        if constexpr (X1) {
+            if (mm.nw) {
+                const QhBuf nb = qh_buf(mm.nw, 4u * 256u * (uint32_t)ngroups);
+#pragma unroll
+                for (int t = 0; t < GPW; t++) nv[t] = qh_ld128(nb, 1024u * (uint32_t)(w * GPW + t) + 16u * lane);
+            }
+        }
+    };
+    auto norm_x = [&](float4* xo, const qh_u32x4* nv) {
+        if constexpr (X1) {
+            if (mm.nw) {
+                float sq = 0.f;
+#pragma unroll
+                for (int t = 0; t < GPW; t++) {
+                    const qh_u32x4 v = nv[t];
+                    float4& a = xo[t];
+                    sq += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+                    a.x *= __uint_as_float(v.x);
+                    a.y *= __uint_as_float(v.y);
+                    a.z *= __uint_as_float(v.z);
+                    a.w *= __uint_as_float(v.w);
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+                if (lane == 0) sqw[w] = sq;
+            }
+        }
+    };
+    // Row scale of the fused RMS norm (1 without it); valid after a barrier.
+    auto norm_scale = [&]() -> float {
+        if constexpr (X1) {
+            if (mm.nw) {
+                float t = 0.f;
+#pragma unroll
+                for (int i = 0; i < W; i++) t += sqw[i];
+                return rsqrtf(t / (float)(256 * ngroups) + 1e-5f);
+            }
+        }
+        return 1.f;
     };
     // x -> digit planes in LDS.  One exponent per wavefront and chunk:
     // max|x| * 2^s < 2^22.  Returns 2^-s; `bad` turns NaN when x is not finite.
@@ -369,11 +420,15 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     auto put = [&](int d, int c, float r) {  // y of row c of this workgroup's tile d
         const int tile = blockIdx.x + d * gridDim.x, m = mat_of(tile);
         const int row = (tile - mm.tstart[m]) * ROWS + c;
-        if (c < ROWS && row < mm.rows[m]) mm.y[m][row] = r;
+        if (c < ROWS && row < mm.rows[m]) {
+            float* yp = mm.y[m] + row;
+            *yp = mm.accum ? *yp + r : r;
+        }
     };
     // Sum the wavefront partials of tiles d0 .. d0+cnt-1 (one set of the ring)
     // into res, or into y once the loop is over: a store inside the loop would
     // make the compiler drain all loads in flight (stores and loads share vmcnt).
+    float nsc = 1.f;  // fused RMS-norm row scale, set after the first barrier
     auto flush = [&](int d0, int cnt, bool direct) {
         if ((int)threadIdx.x < 16 * cnt) {
             const int d = d0 + ((int)threadIdx.x >> 4), c = threadIdx.x & 15;
@@ -381,6 +436,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
             float r = 0.f;
 #pragma unroll
             for (int i = 0; i < W; i++) r += rb[i * 16];
+            r *= nsc;
             if (direct) put(d, c, r);
             else res[d * 16 + c] = r;
         }
@@ -399,9 +455,12 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     qh_u32x4 wr[GPW * NH];
     float4 xv[GPW];
     float rs = 0.f, tot = 0.f;
+    qh_u32x4 nv[GPW];
     load_x(0, xv);
+    load_nw(nv);
     load_w(tile, 0, wr);
     for (;;) {
+        if (X1 && tile == blockIdx.x) norm_x(xv, nv);
         if (!X1 || (tile == blockIdx.x && ch == 0)) rs = prep_x(xv);
         stage(wr);
         int ntile = tile, nc = ch + 1;
@@ -420,6 +479,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
             done++;
             if (done % ring == 0 && ntile < ntiles) {
                 __syncthreads();
+                nsc = norm_scale();
                 flush(done - ring, ring, false);
             }
         }
@@ -428,6 +488,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
         ch = nc;
     }
     __syncthreads();
+    nsc = norm_scale();
     // The last set goes straight to y; earlier sets wait in res.
     const int last = done % ring ? done % ring : ring;
     flush(done - last, last, true);
@@ -437,7 +498,9 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
 // nm matrices (each's weights < 2^31 bytes) in one launch.
 template <class F, int W, int GPW, bool X1>
 static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
-                                    const float* x, int in_dim, uint32_t row_bytes, hipStream_t st) {
+                                    const float* x, int in_dim, uint32_t row_bytes, hipStream_t st,
+                                    const float* nw = nullptr, int accum = 0) {
+    if (nw && !X1) return hipErrorNotSupported;  // the fused norm needs all of x in one workgroup
     static int resident = 0;  // workgroups the device holds at once (per instantiation)
     if (!resident) {
         int dev = 0, per_cu = 0;
@@ -461,6 +524,8 @@ static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, 
         if (on) tiles += (outs[k] + F::ROWS - 1) / F::ROWS;
     }
     mm.tstart[QH_MULTI] = tiles;
+    mm.nw = nw;
+    mm.accum = accum;
     if (tiles == 0) return hipSuccess;
     // One workgroup per tile up to what the device holds at once (tiles go
     // round-robin, so some workgroups take one more tile than others); more
@@ -566,7 +631,7 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
 // weights must fit a 31-bit buffer range.  hipErrorNotSupported otherwise.
 template <class F>
 static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm, const float* x,
-                              int in_dim, uint32_t row_bytes, hipStream_t st) {
+                              int in_dim, uint32_t row_bytes, hipStream_t st, const float* nw, int accum) {
     int total = 0;
     for (int k = 0; k < nm; k++) {
         if ((int64_t)outs[k] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
@@ -578,20 +643,20 @@ static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const 
     (void)total;
     switch (v) {
         case 4:
-            return x1w16 ? launch_mmv16_mats<F, 16, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
-                         : launch_mmv16_mats<F, 16, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+            return x1w16 ? launch_mmv16_mats<F, 16, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
+                         : launch_mmv16_mats<F, 16, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
         case 10:
-            return x1w8 ? launch_mmv16_mats<F, 8, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
-                        : launch_mmv16_mats<F, 8, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+            return x1w8 ? launch_mmv16_mats<F, 8, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
+                        : launch_mmv16_mats<F, 8, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
         case 2:
-            return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
-                                      : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+            return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
+                                      : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
-                                 const float* x, int in_dim, hipStream_t st) {
+                                 const float* x, int in_dim, hipStream_t st, const float* nw, int accum) {
     if (nm < 1 || nm > QH_MULTI || in_dim % 256 || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     int total = 0;
@@ -599,13 +664,13 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
     switch (type) {
         case QT_Q4_K:
             return qh_rows16_better(M16Q4K::ROWS, total)
-                       ? multi_mmv16<M16Q4K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
-                       : multi_mmv16<M16Q4K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+                       ? multi_mmv16<M16Q4K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
+                       : multi_mmv16<M16Q4K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
         case QT_Q5_K:
             return qh_rows16_better(M16Q5K::ROWS, total)
-                       ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st)
-                       : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
-        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st);
+                       ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
+                       : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
         default: return hipErrorNotSupported;
     }
 }

@@ -18,7 +18,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import gemm_grouped_async, gemm_moe_async, gemv_multi_async
+from .host import gemm_grouped_async, gemm_moe_async, gemv_fused_async, gemv_multi_async
 
 Q4_K, Q6_K = 12, 14
 
@@ -160,3 +160,129 @@ class MoeLayer:
                                                           self.up[e].data_ptr(), h, f, n, sp))
             check("hip_gemm_async", self.L.hip_gemm_async(t, self.expert(self.wd, e), self.hbuf[e].data_ptr(),
                                                           self.down[e].data_ptr(), f, h, n, sp))
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """Dense LLaMA-family shape of forward_gpu_step (src/cuda.rs:507-851).  The
+    default is Llama-3-8B Q4_K_M: q/k/o/gate/up and the embedding in Q4_K, v,
+    down and the output head in Q6_K; RoPE NORM pairing (rope_neox false),
+    theta 500000, no YaRN, no biases, no QK-norm, no sliding window."""
+    hidden: int = 4096
+    n_heads: int = 32
+    n_kv: int = 8
+    head_dim: int = 128
+    ffn: int = 14336
+    vocab: int = 128256
+    layers: int = 32
+    theta: float = 500000.0
+    neox: int = 0
+    max_seq: int = 1024
+    types: tuple = (("q", Q4_K), ("k", Q4_K), ("v", Q6_K), ("o", Q4_K), ("gate", Q4_K), ("up", Q4_K),
+                    ("down", Q6_K), ("head", Q6_K), ("embed", Q4_K))
+
+    def type_of(self, name):
+        return dict(self.types)[name]
+
+    def mats(self):
+        """(name, out_dim, in_dim) of one layer's matrices."""
+        h, q, kv, f = self.hidden, self.n_heads * self.head_dim, self.n_kv * self.head_dim, self.ffn
+        return [("q", q, h), ("k", kv, h), ("v", kv, h), ("o", h, q), ("gate", f, h), ("up", f, h), ("down", h, f)]
+
+    def weight_bytes(self) -> int:
+        from . import type_size
+        per_layer = sum(type_size(self.type_of(n), o * i) for n, o, i in self.mats())
+        return per_layer * self.layers + type_size(self.type_of("head"), self.vocab * self.hidden)
+
+
+class ForwardStep:
+    """One token of forward_gpu_step (src/cuda.rs:507-851, dense path) on the
+    device, through the C ABI, in 7 launches per layer instead of the
+    reference's 18:
+
+      hip_gemv_fused  q,k (one launch per weight type)  rms_norm(hidden) fused in
+      hip_gemv_fused  v
+      hip_attention_step   RoPE q/k + K/V append + attention over pos + 1 rows
+      hip_gemv_fused  o    hidden += W_o att (residual fused in)
+      hip_gemv_fused  gate,up   rms_norm(hidden) fused in
+      hip_swiglu
+      hip_gemv_fused  down hidden += W_down act
+
+    then the final norm fused into the head GEMV.  The embedding row comes from
+    hip_embed_lookup (the reference dequantizes it on the CPU and uploads it).
+    Weights: `w[name][layer]` uint8 device tensors in GGUF layout; norms f32."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict):
+        import math
+        self.cfg, self.L, self.w = cfg, lib(), weights
+        c = cfg
+        qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+        f32 = dict(device="cuda", dtype=torch.float32)
+        self.hidden = torch.zeros(c.hidden, **f32)
+        self.q = torch.zeros(qd, **f32)
+        self.k = torch.zeros(kvd, **f32)
+        self.v = torch.zeros(kvd, **f32)
+        self.att = torch.zeros(qd, **f32)
+        self.gate = torch.zeros(c.ffn, **f32)
+        self.up = torch.zeros(c.ffn, **f32)
+        self.act = torch.zeros(c.ffn, **f32)
+        self.logits = torch.zeros(c.vocab, **f32)
+        # fallback scratch of hip_gemv_fused (in_dim + max out_dim floats)
+        big = max(c.hidden, c.ffn, qd)
+        self.scratch = torch.zeros(big + max(big, c.vocab), **f32)
+        self.kc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
+        self.vc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+
+    @staticmethod
+    def random_weights(cfg: ModelConfig, seed: int = 20261204) -> dict:
+        """Random-init weights generated on the device (synth_device)."""
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        w = {n: [] for n, _, _ in cfg.mats()}
+        for l in range(cfg.layers):
+            for j, (n, o, i) in enumerate(cfg.mats()):
+                w[n].append(synth_device.weights(cfg.type_of(n), o, i, seed + 16 * l + j))
+        w["head"] = synth_device.weights(cfg.type_of("head"), cfg.vocab, cfg.hidden, seed - 1)
+        # the lookup touches one row; a small table keeps the bench's memory down
+        w["embed"] = synth_device.weights(cfg.type_of("embed"), min(cfg.vocab, 1024), cfg.hidden, seed - 2)
+        norm = lambda: (1.0 + 0.1 * torch.randn(cfg.hidden, device="cuda", generator=g))
+        w["attn_norm"] = [norm() for _ in range(cfg.layers)]
+        w["ffn_norm"] = [norm() for _ in range(cfg.layers)]
+        w["out_norm"] = norm()
+        return w
+
+    def _fused(self, names, layer, x, ys, in_dim, norm, accumulate, sp):
+        """hip_gemv_fused over the matrices `names` (grouped by weight type)."""
+        by_type = {}
+        for n, y in zip(names, ys):
+            by_type.setdefault(self.cfg.type_of(n), []).append((n, y))
+        for t, group in by_type.items():
+            ws = [(self.w[n][layer] if layer is not None else self.w[n]).data_ptr() for n, _ in group]
+            gemv_fused_async(self.L, t, ws, [y.data_ptr() for _, y in group], [y.numel() for _, y in group],
+                             x.data_ptr(), in_dim, sp, norm_ptr=None if norm is None else norm.data_ptr(),
+                             accumulate=accumulate, scratch_ptr=self.scratch.data_ptr())
+
+    def issue(self, token: int, pos: int, stream=None, logits: bool = True):
+        """Enqueue one decode step (token at position pos) on `stream`."""
+        c, L = self.cfg, self.L
+        assert 0 <= pos < c.max_seq
+        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        kvd = c.n_kv * c.head_dim
+        check("hip_embed_lookup_async", L.hip_embed_lookup_async(self.hidden.data_ptr(), self.w["embed"].data_ptr(),
+                                                                 c.type_of("embed"), token, c.hidden, sp))
+        for l in range(c.layers):
+            self._fused(("q", "k", "v"), l, self.hidden, (self.q, self.k, self.v), c.hidden,
+                        self.w["attn_norm"][l], False, sp)
+            check("hip_attention_step_async", L.hip_attention_step_async(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
+                self.vc[l].data_ptr(), None, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta, 1.0, 0, c.neox,
+                self.scale, sp))
+            self._fused(("o",), l, self.att, (self.hidden,), c.n_heads * c.head_dim, None, True, sp)
+            self._fused(("gate", "up"), l, self.hidden, (self.gate, self.up), c.hidden, self.w["ffn_norm"][l],
+                        False, sp)
+            check("hip_swiglu_async", L.hip_swiglu_async(self.act.data_ptr(), self.gate.data_ptr(),
+                                                         self.up.data_ptr(), c.ffn, sp))
+            self._fused(("down",), l, self.act, (self.hidden,), c.ffn, None, True, sp)
+        if logits:
+            self._fused(("head",), None, self.hidden, (self.logits,), c.hidden, self.w["out_norm"], False, sp)

@@ -155,3 +155,64 @@ def test_embed_lookup_bit_exact(qh, oracle, t):
     sync(qh)
     ref = oracle.dequant(t, data, vocab * dim).reshape(vocab, dim)[5]
     assert np.array_equal(out.download(np.uint32)[:dim], ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("heads", [(32, 8), (4, 2), (8, 8), (6, 4), (16, 1)], ids=str)
+@pytest.mark.parametrize("pos", [0, 5, 31, 32, 33, 100, 1000, 2047, 5000])
+def test_attention_step(qh, heads, pos):
+    """hip_attention_step (RoPE q/k + K/V append at pos + attention over pos + 1
+    rows, split over 32-row slices and merged by the last workgroup per kv head)
+    against the oracle's rope_yarn + kv_append + attention: 1e-5 relative L2 on
+    the output (2e-4 at pos >= 1000, the f32 RoPE angle's rounding), the
+    appended k row at the same bar and the v row bit-exact; rows before pos are
+    left untouched."""
+    nh, nkv = heads
+    hd, theta = 128, 500000.0
+    kvd = nkv * hd
+    neox = pos % 2
+    rng = np.random.default_rng(pos * 7 + nh)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    max_seq = pos + 3
+    kc = rng.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = rng.standard_normal((max_seq, kvd)).astype(np.float32)
+    sinks = rng.standard_normal(nh).astype(np.float32) if pos % 3 == 0 else None
+    dq, dk, dv, dkc, dvc, do = up(q), up(k), up(v), up(kc), up(vc), GpuBuf.alloc_f32(nh * hd)
+    ds = up(sinks) if sinks is not None else None
+    scale = 1.0 / np.sqrt(hd)
+    check("attention_step", qh.hip_attention_step_async(do.ptr, dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr,
+                                                        ds.ptr if ds else None, nh, nkv, hd, kvd, pos, theta, 1.0, 0,
+                                                        neox, scale, None))
+    sync(qh)
+    qr = g.rope_yarn(q, nh, hd, pos, theta, neox=bool(neox))
+    kr = g.rope_yarn(k, nkv, hd, pos, theta, neox=bool(neox))
+    kc64, vc64 = kc.astype(np.float64), vc.astype(np.float64)
+    kc64[pos], vc64[pos] = kr, v
+    _, ref = g.attention(qr, kc64, vc64, nh, nkv, pos + 1, hd, kvd, scale, sinks)
+    tol = 1e-5 if pos < 1000 else 2e-4
+    assert cf.rel_l2(down(do, nh * hd), ref) < tol
+    kc_got = dkc.download(np.float32).reshape(max_seq, kvd)
+    vc_got = dvc.download(np.float32).reshape(max_seq, kvd)
+    assert cf.rel_l2(kc_got[pos], kr) < tol
+    assert np.array_equal(vc_got[pos], v)
+    assert np.array_equal(kc_got[:pos], kc[:pos]) and np.array_equal(vc_got[:pos], vc[:pos])
+    assert np.array_equal(kc_got[pos + 1:], kc[pos + 1:])
+
+
+def test_attention_step_repeat(qh):
+    """Two launches in a row (the per-kv-head arrival counters are back at zero
+    after each) give the same output."""
+    nh, nkv, hd, pos = 8, 2, 128, 700
+    rng = np.random.default_rng(3)
+    bufs = [up(rng.standard_normal(n).astype(np.float32)) for n in (nh * hd, nkv * hd, nkv * hd)]
+    kc, vc = up(rng.standard_normal((pos + 1) * nkv * hd)), up(rng.standard_normal((pos + 1) * nkv * hd))
+    outs = []
+    for _ in range(2):
+        o = GpuBuf.alloc_f32(nh * hd)
+        check("attention_step", qh.hip_attention_step_async(o.ptr, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, kc.ptr,
+                                                            vc.ptr, None, nh, nkv, hd, nkv * hd, pos, 10000.0, 1.0, 0,
+                                                            0, 0.088, None))
+        sync(qh)
+        outs.append(down(o, nh * hd))
+    assert np.array_equal(outs[0], outs[1])
