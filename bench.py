@@ -226,7 +226,7 @@ def forward_leg(torch, reps, wbytes):
         out[f"n1_full_pos{pos}"] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
                                     "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
                                     "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-                                    "launches": 1 + 7 * cfg.layers + 1}
+                                    "launches": 1 + 5 * cfg.layers + 1}
         del g
     del step
     torch.cuda.empty_cache()

@@ -209,6 +209,27 @@ int hip_swiglu(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* stream);
 int hip_swiglu_oai(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_oai_async(float* out, const float* gate, const float* up, int n, void* stream);
+/* hip_gemv_fused over count (1..8) matrices of any types sharing x (per-matrix
+ * types[k]): the projections of one input, e.g. a Q4_K_M layer's q and k
+ * (Q4_K) with v (Q6_K).  Two matrix-core types (Q4_K, Q5_K, Q6_K; <= 4
+ * matrices each) go out as one launch whose workgroups split between the two
+ * formats; otherwise one hip_gemv_fused call per type.  No counterpart in the
+ * reference (one cuda_gemv per matrix, src/cuda.rs:556-562); results equal
+ * hip_gemv_fused's per type within the GEMV tolerance. */
+int hip_gemv_group_async(int count, const uint32_t* types, const uint8_t* const* W, float* const* y,
+                         const int* out_dims, const float* d_x, const float* norm_w, int accumulate, int in_dim,
+                         float* scratch, void* stream);
+
+/* act = silu(W_gate x') * (W_up x'), x' = rms_norm(x) * norm_w (norm_w NULL: x'
+ * = x): the dense FFN's cuda_rms_norm + two cuda_gemv + cuda_swiglu
+ * (src/cuda.rs:729-733, :773-792) in one launch for Q4_K/Q5_K/Q6_K (the gate
+ * and up tiles of a row block go to one workgroup, which applies the SwiGLU
+ * before writing).  Other types / shapes run the separate kernels on scratch
+ * (in_dim + 2 * ffn_dim floats; NULL is QH_ERR_NULL then).  x must not alias
+ * act. */
+int hip_gemv_swiglu_async(uint32_t ggml_type, const uint8_t* W_gate, const uint8_t* W_up, float* act, int ffn_dim,
+                          const float* d_x, const float* norm_w, int in_dim, float* scratch, void* stream);
+
 /* The attention block of one decode step in one launch: RoPE (as hip_rope_yarn)
  * on q (n_heads heads) and k (n_kv_heads heads), the K/V-cache append of the
  * rotated k and of v at row pos (as hip_kv_append), then attention over pos + 1

@@ -173,6 +173,92 @@ int hip_gemv_fused_async(uint32_t type, int count, const uint8_t* const* W, floa
     return QH_OK;
 }
 
+int hip_gemv_group_async(int count, const uint32_t* types, const uint8_t* const* W, float* const* y,
+                         const int* out_dims, const float* x, const float* norm_w, int accumulate, int in_dim,
+                         float* scratch, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 1 || count > 8 || !types || !W || !y || !out_dims) return QH_ERR_RANGE;
+    // the distinct types in first-seen order, each with its matrices
+    uint32_t ut[8];
+    int nut = 0, idx[8][8], cnt[8] = {0};
+    for (int k = 0; k < count; k++) {
+        int u = 0;
+        while (u < nut && ut[u] != types[k]) u++;
+        if (u == nut) ut[nut++] = types[k];
+        idx[u][cnt[u]++] = k;
+    }
+    auto gather = [&](int u, const uint8_t** w, float** yy, int* o) {
+        for (int i = 0; i < cnt[u]; i++) {
+            w[i] = W[idx[u][i]];
+            yy[i] = y[idx[u][i]];
+            o[i] = out_dims[idx[u][i]];
+        }
+    };
+    if (nut == 2 && cnt[0] <= 4 && cnt[1] <= 4 && x && !qh_force_valu()) {
+        bool ok = true;
+        for (int k = 0; k < count; k++)
+            ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
+        if (ok) {
+            const uint8_t *w0[4], *w1[4];
+            float *y0[4], *y1[4];
+            int o0[4], o1[4];
+            gather(0, w0, y0, o0);
+            gather(1, w1, y1, o1);
+            hipError_t e = qh_launch_mmv16_mix(ut[0], w0, y0, o0, cnt[0], ut[1], w1, y1, o1, cnt[1], x, in_dim,
+                                               norm_w, accumulate ? 1 : 0, st);
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemv_group");
+        }
+    }
+    for (int u = 0; u < nut; u++) {
+        const uint8_t* w[8];
+        float* yy[8];
+        int o[8];
+        gather(u, w, yy, o);
+        for (int i0 = 0; i0 < cnt[u]; i0 += 4) {
+            const int n = cnt[u] - i0 < 4 ? cnt[u] - i0 : 4;
+            int rc = hip_gemv_fused_async(ut[u], n, w + i0, yy + i0, o + i0, x, norm_w, accumulate, in_dim, scratch,
+                                          stream);
+            if (rc) return rc;
+        }
+    }
+    return QH_OK;
+}
+
+int hip_gemv_swiglu_async(uint32_t type, const uint8_t* W_gate, const uint8_t* W_up, float* act, int ffn_dim,
+                          const float* x, const float* norm_w, int in_dim, float* scratch, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    int rc = qh_check_dims(type, in_dim, ffn_dim);
+    if (rc == QH_ERR_TYPE) return qh_unknown_type("hip_gemv_swiglu", type, ffn_dim > 0 ? act : nullptr,
+                                                  (size_t)(ffn_dim > 0 ? ffn_dim : 0), st);
+    if (rc) return rc;
+    if (ffn_dim == 0) return QH_OK;
+    if (!W_gate || !W_up || !act || !x) return QH_ERR_NULL;
+    if (!qh_force_valu()) {
+        const uint8_t* W[2] = {W_gate, W_up};
+        float* y[2] = {act, act};
+        const int outs[2] = {ffn_dim, ffn_dim};
+        hipError_t e = qh_launch_mmv16_multi(type, W, y, outs, 2, x, in_dim, st, norm_w, 0, true);
+        if (e == hipSuccess) return QH_OK;
+        if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemv_swiglu");
+    }
+    // separate kernels through scratch: [normed x (in_dim)] [gate (ffn)] [up (ffn)]
+    if (!scratch) return QH_ERR_NULL;
+    const float* xs = x;
+    if (norm_w) {
+        QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st), "hip_gemv_swiglu");
+        xs = scratch;
+    }
+    float* g = scratch + in_dim;
+    float* u = g + ffn_dim;
+    rc = hip_gemv_async(type, W_gate, xs, g, in_dim, ffn_dim, stream);
+    if (rc) return rc;
+    rc = hip_gemv_async(type, W_up, xs, u, in_dim, ffn_dim, stream);
+    if (rc) return rc;
+    QH_CHECK(qh_glue_swiglu(0, act, g, u, ffn_dim, st), "hip_gemv_swiglu");
+    return QH_OK;
+}
+
 int hip_gemm_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                    void* stream) {
     hipStream_t st = (hipStream_t)stream;

@@ -459,14 +459,25 @@ __global__ __launch_bounds__(256) void qg_swiglu_oai(float* out, const float* ga
 }
 
 // Row `token` of an embedding matrix of any supported type, decoded bit-exactly
-// (embed_lookup_*, :678-731 handle Q5_1, IQ4_NL and BF16): one thread per block.
+// (embed_lookup_*, :678-731 handle Q5_1, IQ4_NL and BF16).  A workgroup takes
+// up to 4096 output values: it stages their blocks' bytes in LDS with coalesced
+// loads, one thread per block decodes from LDS into LDS (qh_decode_block), and
+// the values leave in coalesced stores.
+#define QG_EMB_OUT 4096
+#define QG_EMB_RAW 4608
 __global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t* data, uint32_t type, int token,
-                                                       int embed_dim, int qk, uint32_t bb) {
-    const int b = blockIdx.x * 256 + threadIdx.x, nb = embed_dim / qk;
-    if (b >= nb) return;
-    float v[256];
-    qh_decode_block(type, data + ((size_t)token * nb + b) * bb, v);
-    for (int i = 0; i < qk; i++) out[(size_t)b * qk + i] = v[i];
+                                                       int embed_dim, int qk, uint32_t bb, int bpw) {
+    __shared__ __align__(16) uint8_t raw[QG_EMB_RAW];
+    __shared__ __align__(16) float dec[QG_EMB_OUT];
+    const int nb = embed_dim / qk, b0 = blockIdx.x * bpw;
+    const int nbw = min(bpw, nb - b0);
+    const uint8_t* src = data + ((size_t)token * nb + b0) * bb;
+    for (int i = threadIdx.x; i < nbw * (int)bb; i += 256) raw[i] = src[i];
+    __syncthreads();
+    if ((int)threadIdx.x < nbw) qh_decode_block(type, raw + threadIdx.x * bb, dec + threadIdx.x * qk);
+    __syncthreads();
+    float* o = out + (size_t)b0 * qk;
+    for (int i = threadIdx.x; i < nbw * qk; i += 256) o[i] = dec[i];
 }
 
 static unsigned qg_blocks(int n) { return (unsigned)((n + 255) / 256); }
@@ -572,8 +583,12 @@ hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* u
 
 hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st) {
     const int qk = qh_block_elems(type);
+    const uint32_t bb = qh_block_bytes(type);
     const int nb = embed_dim / qk;
-    hipLaunchKernelGGL(qg_embed_lookup, dim3(qg_blocks(nb)), dim3(256), 0, st, out, data, type, token, embed_dim, qk,
-                       qh_block_bytes(type));
+    int bpw = QG_EMB_OUT / qk;
+    if (bpw > 256) bpw = 256;
+    if ((uint32_t)bpw * bb > QG_EMB_RAW) bpw = QG_EMB_RAW / bb;
+    hipLaunchKernelGGL(qg_embed_lookup, dim3((unsigned)((nb + bpw - 1) / bpw)), dim3(256), 0, st, out, data, type,
+                       token, embed_dim, qk, bb, bpw);
     return hipGetLastError();
 }

@@ -205,17 +205,24 @@ struct QhMats {
     int accum;
 };
 
-template <class F, int W, int GPW, bool X1, bool MULTI>
-__global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float* __restrict__ x, uint32_t row_bytes,
-                                                   int ngroups) {
+// LDS of one workgroup: GPW staging tiles and x digit planes per wavefront, the
+// ring of wavefront partials, finished rows and the per-wavefront sums of x^2.
+template <class F, int W, int GPW>
+constexpr int qh_mmv16_lds() {
+    return W * GPW * (F::ROWS * QH_RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4;
+}
+
+// The kernel body for workgroup `bid` of `nblk` working on mm's tiles (a
+// launch may run two bodies of different formats side by side, see qh_mmv16_mix).
+template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR>
+__device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __restrict__ x, uint32_t row_bytes,
+                                              int ngroups, unsigned char* lds, const int bid, const int nblk) {
     constexpr int ROWS = F::ROWS, CH = F::CH;
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
     static_assert(ROWS <= 16 && 16 * CH < QH_RS, "tile shape");
     constexpr int TILE = ROWS * QH_RS + 16;  // staging tile of one group + 16 spare bytes
     // Wavefront partials of finished tiles wait in a ring of two sets of QH_RING
     // tiles; the workgroup meets at a barrier only when a set is full.
-    __shared__ __align__(16) unsigned char lds[W * GPW * TILE + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 +
-                                               QH_MAXT * 16 * 4 + W * 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
     unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
@@ -227,11 +234,22 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
         int m = 0;
-        if constexpr (MULTI) {
+        if constexpr (PAIR) {
+            m = tile & 1;
+        } else if constexpr (MULTI) {
 #pragma unroll
             for (int k = 1; k < QH_MULTI; k++) m += tile >= mm.tstart[k];
         }
         return m;
+    };
+    // Tile of matrix m's index space (PAIR: tiles alternate gate, up).
+    auto local_tile = [&](int tile, int m) { return PAIR ? tile >> 1 : (MULTI ? tile - mm.tstart[m] : tile); };
+    // The k-th tile of this workgroup.  PAIR (SwiGLU of two matrices): the
+    // gate and up tiles of one row block follow each other, so both results
+    // meet in this workgroup's LDS.
+    auto wg_tile = [&](int k) -> int {
+        if constexpr (PAIR) return 2 * (bid + (k >> 1) * nblk) + (k & 1);
+        return bid + k * nblk;
     };
     const QhBuf wb0 = qh_buf(mm.w[0], mm.wbytes[0]);  // the one-matrix case, hoisted
     const int nch = (ngroups + W * GPW - 1) / (W * GPW);
@@ -269,7 +287,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
         const int m = mat_of(tile);
         const QhBuf wb = MULTI ? qh_buf(mm.w[m], mm.wbytes[m]) : wb0;
         const int out_dim = mm.rows[m];
-        if (MULTI) tile -= mm.tstart[m];
+        if (MULTI) tile = local_tile(tile, m);
         const uint32_t base = (uint32_t)(tile * ROWS) * row_bytes;
 #pragma unroll
         for (int t = 0; t < GPW; t++)
@@ -418,8 +436,8 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
     };
 
     auto put = [&](int d, int c, float r) {  // y of row c of this workgroup's tile d
-        const int tile = blockIdx.x + d * gridDim.x, m = mat_of(tile);
-        const int row = (tile - mm.tstart[m]) * ROWS + c;
+        const int tile = wg_tile(d), m = mat_of(tile);
+        const int row = local_tile(tile, m) * ROWS + c;
         if (c < ROWS && row < mm.rows[m]) {
             float* yp = mm.y[m] + row;
             *yp = mm.accum ? *yp + r : r;
@@ -441,34 +459,43 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
             else res[d * 16 + c] = r;
         }
     };
-    int tile = blockIdx.x, ch = 0, done = 0;
+    int tile = wg_tile(0), done = 0;
     if (tile >= ntiles) return;  // uniform over the workgroup
     // Few tiles per workgroup: meet every QH_RING tiles (the end-of-kernel wait
     // for the slowest wavefront is what short launches pay).  Many tiles: meet
-    // at every tile, which keeps the wavefronts on one tile's rows at a time.
-    const int ring = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x <= 2 * QH_RING ? QH_RING : 1;
+    // at every tile (PAIR: every pair), which keeps the wavefronts on one tile's
+    // rows at a time.
+    const int my_tiles = PAIR ? 2 * ((ntiles / 2 - bid + nblk - 1) / nblk)
+                              : (ntiles - bid + nblk - 1) / nblk;
+    const int ring = my_tiles <= 2 * QH_RING ? QH_RING : (PAIR ? 2 : 1);
     // Pipeline: the registers of an item are staged into LDS as soon as they
-    // arrive and then receive the next item's loads, which stay in flight while
-    // the staged item is computed.  No loaded value is carried around the loop
-    // in registers (a copy between register sets would make the compiler drain
-    // every load in flight); a deeper, two-set pipeline measured slower.
-    qh_u32x4 wr[GPW * NH];
-    float4 xv[GPW];
+    // arrive and then receive the loads of the next item, which stay in flight
+    // while the staged item is computed.  No loaded value is copied between
+    // registers (a copy would make the compiler drain every load in flight; a
+    // two-set pipeline measured slower).  Items are numbered per workgroup:
+    // item it = chunk it % cpt of tile it / cpt.
+    const int cpt = X1 ? 1 : nch;
+    auto item_tile = [&](int it) { return wg_tile(it / cpt); };
+    auto item_ch = [&](int it) { return it - (it / cpt) * cpt; };
+    qh_u32x4 wra[GPW * NH];
+    float4 xva[GPW];
     float rs = 0.f, tot = 0.f;
     qh_u32x4 nv[GPW];
-    load_x(0, xv);
+    load_x(0, xva);
     load_nw(nv);
-    load_w(tile, 0, wr);
-    for (;;) {
-        if (X1 && tile == blockIdx.x) norm_x(xv, nv);
-        if (!X1 || (tile == blockIdx.x && ch == 0)) rs = prep_x(xv);
+    load_w(tile, 0, wra);
+    int it = 0;
+    auto body = [&](qh_u32x4* wr, float4* xv) -> bool {
+        const int ch = item_ch(it);
+        if (X1 && it == 0) norm_x(xv, nv);
+        if (!X1 || it == 0) rs = prep_x(xv);
         stage(wr);
-        int ntile = tile, nc = ch + 1;
-        if (X1 || nc == nch) { nc = 0; ntile += gridDim.x; }
-        if (!X1) load_x(nc, xv);
-        load_w(ntile, nc, wr);
+        const int ld = it + 1;  // the item these registers load next
+        if (!X1) load_x(item_ch(ld), xv);
+        load_w(item_tile(ld), item_ch(ld), wr);
         tot += compute(rs);
-        if (nc == 0) {
+        const int nt = item_tile(it + 1);
+        if (ch == cpt - 1) {
             // Tile finished: sum the four lanes of each column into this
             // wavefront's slot; the sum over wavefronts waits for a full set.
             float v = tot + bad;
@@ -477,41 +504,104 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
             if (lane < 16) red[((done % (2 * QH_RING)) * W + w) * 16 + lane] = v;
             tot = 0.f;
             done++;
-            if (done % ring == 0 && ntile < ntiles) {
+            if (done % ring == 0 && nt < ntiles) {
                 __syncthreads();
                 nsc = norm_scale();
                 flush(done - ring, ring, false);
             }
         }
-        if (ntile >= ntiles) break;
-        tile = ntile;
-        ch = nc;
+        it++;
+        return nt < ntiles;
+    };
+    while (body(wra, xva)) {
     }
     __syncthreads();
     nsc = norm_scale();
-    // The last set goes straight to y; earlier sets wait in res.
     const int last = done % ring ? done % ring : ring;
+    if constexpr (PAIR) {
+        // act = silu(gate) * up (qg_swiglu's expression) for every pair
+        flush(done - last, last, false);
+        __syncthreads();
+        for (int i = threadIdx.x; i < (done >> 1) * 16; i += 64 * W) {
+            const int q = i >> 4, c = i & 15, row = local_tile(wg_tile(2 * q), 0) * ROWS + c;
+            if (c < ROWS && row < mm.rows[0]) {
+                const float g = res[(2 * q) * 16 + c], u = res[(2 * q + 1) * 16 + c];
+                mm.y[0][row] = (g / (1.f + expf(-g))) * u;
+            }
+        }
+        return;
+    }
+    // The last set goes straight to y; earlier sets wait in res.
     flush(done - last, last, true);
     for (int i = threadIdx.x; i < (done - last) * 16; i += 64 * W) put(i >> 4, i & 15, res[i]);
 }
 
+template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false>
+__global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float* __restrict__ x, uint32_t row_bytes,
+                                                   int ngroups) {
+    __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW>()];
+    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR>(mm, x, row_bytes, ngroups, lds, (int)blockIdx.x, (int)gridDim.x);
+}
+
+// Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
+// workgroups below g1 run F1's body on mm1's matrices, the others F2's on mm2's.
+template <class F1, class F2, int W, int GPW, bool X1>
+__global__ __launch_bounds__(64 * W) void qh_mmv16_mix(const QhMats mm1, const QhMats mm2, const float* __restrict__ x,
+                                                       uint32_t rb1, uint32_t rb2, int ngroups, int g1) {
+    constexpr int L1 = qh_mmv16_lds<F1, W, GPW>(), L2 = qh_mmv16_lds<F2, W, GPW>();
+    __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
+    if ((int)blockIdx.x < g1)
+        qh_mmv16_body<F1, W, GPW, X1, true, false>(mm1, x, rb1, ngroups, lds, (int)blockIdx.x, g1);
+    else
+        qh_mmv16_body<F2, W, GPW, X1, true, false>(mm2, x, rb2, ngroups, lds, (int)blockIdx.x - g1,
+                                                   (int)gridDim.x - g1);
+}
+
 // nm matrices (each's weights < 2^31 bytes) in one launch.
 template <class F, int W, int GPW, bool X1>
-static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
-                                    const float* x, int in_dim, uint32_t row_bytes, hipStream_t st,
-                                    const float* nw = nullptr, int accum = 0) {
-    if (nw && !X1) return hipErrorNotSupported;  // the fused norm needs all of x in one workgroup
+static hipError_t launch_mmv16_grid(const QhMats& mm, int nm, const float* x, int in_dim, uint32_t row_bytes,
+                                     hipStream_t st, bool pair) {
     static int resident = 0;  // workgroups the device holds at once (per instantiation)
     if (!resident) {
         int dev = 0, per_cu = 0;
         hipDeviceProp_t prop;
         if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, GPW, X1, false>, 64 * W, 0) !=
-                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, GPW, X1, false, false>,
+                                                         64 * W, 0) != hipSuccess ||
             per_cu < 1)
             return hipErrorNotSupported;
         resident = per_cu * prop.multiProcessorCount;
     }
+    const int tiles = mm.tstart[QH_MULTI];
+    if (pair) {
+        const int pairs = tiles / 2;
+        int grid = pairs < resident ? pairs : resident;
+        if ((pairs + grid - 1) / grid > QH_MAXT / 2) grid = (pairs + QH_MAXT / 2 - 1) / (QH_MAXT / 2);
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, true>), dim3((unsigned)grid), dim3(64 * W), 0, st,
+                           mm, x, row_bytes, in_dim / 256);
+        return hipGetLastError();
+    }
+    // One workgroup per tile up to what the device holds at once (tiles go
+    // round-robin, so some workgroups take one more tile than others); more
+    // only when a workgroup would exceed QH_MAXT tiles.
+    int grid = tiles < resident ? tiles : resident;
+    if ((tiles + grid - 1) / grid > QH_MAXT) grid = (tiles + QH_MAXT - 1) / QH_MAXT;
+    if (nm > 1)
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, false>), dim3((unsigned)grid), dim3(64 * W), 0, st,
+                           mm, x, row_bytes, in_dim / 256);
+    else
+        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, false, false>), dim3((unsigned)grid), dim3(64 * W), 0,
+                           st, mm, x, row_bytes, in_dim / 256);
+    return hipGetLastError();
+}
+
+template <class F, int W, int GPW, bool X1>
+static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
+                                    const float* x, int in_dim, uint32_t row_bytes, hipStream_t st,
+                                    const float* nw = nullptr, int accum = 0, bool pair = false) {
+    if (nw && !X1) return hipErrorNotSupported;  // the fused norm needs all of x in one workgroup
+    // SwiGLU pairs: ys[0] = silu(Ws[0] x) * (Ws[1] x), two matrices of equal rows
+    if (pair && (nm != 2 || outs[0] != outs[1] || accum)) return hipErrorNotSupported;
     QhMats mm;
     int tiles = 0;
     for (int k = 0; k < QH_MULTI; k++) {
@@ -527,18 +617,7 @@ static hipError_t launch_mmv16_mats(const uint8_t* const* Ws, float* const* ys, 
     mm.nw = nw;
     mm.accum = accum;
     if (tiles == 0) return hipSuccess;
-    // One workgroup per tile up to what the device holds at once (tiles go
-    // round-robin, so some workgroups take one more tile than others); more
-    // only when a workgroup would exceed QH_MAXT tiles.
-    int grid = tiles < resident ? tiles : resident;
-    if ((tiles + grid - 1) / grid > QH_MAXT) grid = (tiles + QH_MAXT - 1) / QH_MAXT;
-    if (nm > 1)
-        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
-                           row_bytes, in_dim / 256);
-    else
-        hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, false>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
-                           row_bytes, in_dim / 256);
-    return hipGetLastError();
+    return launch_mmv16_grid<F, W, GPW, X1>(mm, nm, x, in_dim, row_bytes, st, pair);
 }
 
 template <class F, int W, int GPW, bool X1>
@@ -631,7 +710,8 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
 // weights must fit a 31-bit buffer range.  hipErrorNotSupported otherwise.
 template <class F>
 static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const int* outs, int nm, const float* x,
-                              int in_dim, uint32_t row_bytes, hipStream_t st, const float* nw, int accum) {
+                              int in_dim, uint32_t row_bytes, hipStream_t st, const float* nw, int accum,
+                              bool pair) {
     int total = 0;
     for (int k = 0; k < nm; k++) {
         if ((int64_t)outs[k] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
@@ -643,20 +723,21 @@ static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const 
     (void)total;
     switch (v) {
         case 4:
-            return x1w16 ? launch_mmv16_mats<F, 16, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
-                         : launch_mmv16_mats<F, 16, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+            return x1w16 ? launch_mmv16_mats<F, 16, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                         : launch_mmv16_mats<F, 16, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case 10:
-            return x1w8 ? launch_mmv16_mats<F, 8, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
-                        : launch_mmv16_mats<F, 8, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+            return x1w8 ? launch_mmv16_mats<F, 8, 1, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                        : launch_mmv16_mats<F, 8, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case 2:
-            return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
-                                      : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+            return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                                      : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
-                                 const float* x, int in_dim, hipStream_t st, const float* nw, int accum) {
+                                 const float* x, int in_dim, hipStream_t st, const float* nw, int accum,
+                                 bool pair) {
     if (nm < 1 || nm > QH_MULTI || in_dim % 256 || ((uintptr_t)x & 15u)) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
     int total = 0;
@@ -664,13 +745,100 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
     switch (type) {
         case QT_Q4_K:
             return qh_rows16_better(M16Q4K::ROWS, total)
-                       ? multi_mmv16<M16Q4K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
-                       : multi_mmv16<M16Q4K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+                       ? multi_mmv16<M16Q4K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                       : multi_mmv16<M16Q4K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q5_K:
             return qh_rows16_better(M16Q5K::ROWS, total)
-                       ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum)
-                       : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
-        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum);
+                       ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                       : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         default: return hipErrorNotSupported;
     }
+}
+
+// Two formats sharing x in one launch: matrices Ws1 (format F1) and Ws2 (F2),
+// each group <= QH_MULTI matrices < 2^31 bytes.  The resident workgroups are
+// split between the two bodies in proportion to their weight bytes.
+template <class F1, class F2, int W, int GPW, bool X1>
+static hipError_t launch_mmv16_mix(const uint8_t* const* Ws1, float* const* ys1, const int* outs1, int n1,
+                                   const uint8_t* const* Ws2, float* const* ys2, const int* outs2, int n2,
+                                   const float* x, int in_dim, uint32_t rb1, uint32_t rb2, const float* nw, int accum,
+                                   hipStream_t st) {
+    if (nw && !X1) return hipErrorNotSupported;
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16_mix<F1, F2, W, GPW, X1>, 64 * W, 0) !=
+                hipSuccess ||
+            per_cu < 1)
+            return hipErrorNotSupported;
+        resident = per_cu * prop.multiProcessorCount;
+    }
+    auto fill = [&](QhMats& mm, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm, uint32_t rb,
+                    int rows_per_tile) {
+        int tiles = 0;
+        for (int k = 0; k < QH_MULTI; k++) {
+            const bool on = k < nm;
+            mm.w[k] = on ? Ws[k] : nullptr;
+            mm.y[k] = on ? ys[k] : nullptr;
+            mm.rows[k] = on ? outs[k] : 0;
+            mm.wbytes[k] = on ? (uint32_t)(((uint64_t)outs[k] * rb + 3) & ~(uint64_t)3) : 0;
+            mm.tstart[k] = on ? tiles : INT_MAX;
+            if (on) tiles += (outs[k] + rows_per_tile - 1) / rows_per_tile;
+        }
+        mm.tstart[QH_MULTI] = tiles;
+        mm.nw = nw;
+        mm.accum = accum;
+        return tiles;
+    };
+    QhMats mm1, mm2;
+    const int t1 = fill(mm1, Ws1, ys1, outs1, n1, rb1, F1::ROWS), t2 = fill(mm2, Ws2, ys2, outs2, n2, rb2, F2::ROWS);
+    if (t1 == 0 || t2 == 0) return hipErrorNotSupported;  // one format: the plain launch
+    const double b1 = (double)t1 * F1::ROWS * rb1, b2 = (double)t2 * F2::ROWS * rb2;
+    int g1 = (int)(resident * b1 / (b1 + b2) + 0.5);
+    g1 = g1 < 1 ? 1 : (g1 > t1 ? t1 : g1);
+    int g2 = resident - g1;
+    g2 = g2 < 1 ? 1 : (g2 > t2 ? t2 : g2);
+    if ((t1 + g1 - 1) / g1 > QH_MAXT) g1 = (t1 + QH_MAXT - 1) / QH_MAXT;
+    if ((t2 + g2 - 1) / g2 > QH_MAXT) g2 = (t2 + QH_MAXT - 1) / QH_MAXT;
+    hipLaunchKernelGGL((qh_mmv16_mix<F1, F2, W, GPW, X1>), dim3((unsigned)(g1 + g2)), dim3(64 * W), 0, st, mm1, mm2, x,
+                       rb1, rb2, in_dim / 256, g1);
+    return hipGetLastError();
+}
+
+template <class F1, class F2>
+static hipError_t dispatch_mix(const uint8_t* const* Ws1, float* const* ys1, const int* outs1, int n1,
+                               const uint8_t* const* Ws2, float* const* ys2, const int* outs2, int n2, const float* x,
+                               int in_dim, uint32_t rb1, uint32_t rb2, const float* nw, int accum, hipStream_t st) {
+    if (in_dim <= 256 * 16)
+        return launch_mmv16_mix<F1, F2, 16, 1, true>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw,
+                                                     accum, st);
+    return launch_mmv16_mix<F1, F2, 8, 1, false>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw,
+                                                 accum, st);
+}
+
+// GEMVs of two matrix-core types sharing x in one launch; hipErrorNotSupported
+// for other type pairs / shapes (the caller then launches per type).
+hipError_t qh_launch_mmv16_mix(uint32_t t1, const uint8_t* const* Ws1, float* const* ys1, const int* outs1, int n1,
+                               uint32_t t2, const uint8_t* const* Ws2, float* const* ys2, const int* outs2, int n2,
+                               const float* x, int in_dim, const float* nw, int accum, hipStream_t st) {
+    if (n1 < 1 || n1 > QH_MULTI || n2 < 1 || n2 > QH_MULTI || in_dim % 256 || ((uintptr_t)x & 15u) ||
+        qh_mmv16_variant_env() >= 0)
+        return hipErrorNotSupported;
+    const uint32_t rb1 = (uint32_t)qh_type_size(t1, (size_t)in_dim), rb2 = (uint32_t)qh_type_size(t2, (size_t)in_dim);
+    for (int k = 0; k < n1; k++)
+        if ((int64_t)outs1[k] * rb1 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+    for (int k = 0; k < n2; k++)
+        if ((int64_t)outs2[k] * rb2 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+    if (t1 > t2)
+        return qh_launch_mmv16_mix(t2, Ws2, ys2, outs2, n2, t1, Ws1, ys1, outs1, n1, x, in_dim, nw, accum, st);
+    if (t1 == QT_Q4_K && t2 == QT_Q6_K)
+        return dispatch_mix<M16Q4K, M16Q6K>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw, accum, st);
+    if (t1 == QT_Q5_K && t2 == QT_Q6_K)
+        return dispatch_mix<M16Q5K, M16Q6K>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw, accum, st);
+    if (t1 == QT_Q4_K && t2 == QT_Q5_K)
+        return dispatch_mix<M16Q4K, M16Q5K>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw, accum, st);
+    return hipErrorNotSupported;
 }

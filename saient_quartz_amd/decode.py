@@ -18,7 +18,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import gemm_grouped_async, gemm_moe_async, gemv_fused_async, gemv_multi_async
+from .host import gemm_grouped_async, gemm_moe_async, gemv_group_async, gemv_multi_async
 
 Q4_K, Q6_K = 12, 14
 
@@ -197,16 +197,14 @@ class ModelConfig:
 
 class ForwardStep:
     """One token of forward_gpu_step (src/cuda.rs:507-851, dense path) on the
-    device, through the C ABI, in 7 launches per layer instead of the
+    device, through the C ABI, in 5 launches per layer instead of the
     reference's 18:
 
-      hip_gemv_fused  q,k (one launch per weight type)  rms_norm(hidden) fused in
-      hip_gemv_fused  v
+      hip_gemv_group  q,k,v (Q4_K + Q6_K in one launch)  rms_norm(hidden) fused in
       hip_attention_step   RoPE q/k + K/V append + attention over pos + 1 rows
-      hip_gemv_fused  o    hidden += W_o att (residual fused in)
-      hip_gemv_fused  gate,up   rms_norm(hidden) fused in
-      hip_swiglu
-      hip_gemv_fused  down hidden += W_down act
+      hip_gemv_group  o    hidden += W_o att (residual fused in)
+      hip_gemv_swiglu gate,up   rms_norm(hidden) and silu(gate) * up fused in
+      hip_gemv_group  down hidden += W_down act
 
     then the final norm fused into the head GEMV.  The embedding row comes from
     hip_embed_lookup (the reference dequantizes it on the CPU and uploads it).
@@ -229,7 +227,7 @@ class ForwardStep:
         self.logits = torch.zeros(c.vocab, **f32)
         # fallback scratch of hip_gemv_fused (in_dim + max out_dim floats)
         big = max(c.hidden, c.ffn, qd)
-        self.scratch = torch.zeros(big + max(big, c.vocab), **f32)
+        self.scratch = torch.zeros(big + max(2 * big, c.vocab), **f32)
         self.kc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
         self.vc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
         self.scale = 1.0 / math.sqrt(c.head_dim)
@@ -253,15 +251,12 @@ class ForwardStep:
         return w
 
     def _fused(self, names, layer, x, ys, in_dim, norm, accumulate, sp):
-        """hip_gemv_fused over the matrices `names` (grouped by weight type)."""
-        by_type = {}
-        for n, y in zip(names, ys):
-            by_type.setdefault(self.cfg.type_of(n), []).append((n, y))
-        for t, group in by_type.items():
-            ws = [(self.w[n][layer] if layer is not None else self.w[n]).data_ptr() for n, _ in group]
-            gemv_fused_async(self.L, t, ws, [y.data_ptr() for _, y in group], [y.numel() for _, y in group],
-                             x.data_ptr(), in_dim, sp, norm_ptr=None if norm is None else norm.data_ptr(),
-                             accumulate=accumulate, scratch_ptr=self.scratch.data_ptr())
+        """hip_gemv_group over the matrices `names` (any mix of weight types)."""
+        ws = [(self.w[n][layer] if layer is not None else self.w[n]).data_ptr() for n in names]
+        gemv_group_async(self.L, [self.cfg.type_of(n) for n in names], ws, [y.data_ptr() for y in ys],
+                         [y.numel() for y in ys], x.data_ptr(), in_dim, sp,
+                         norm_ptr=None if norm is None else norm.data_ptr(), accumulate=accumulate,
+                         scratch_ptr=self.scratch.data_ptr())
 
     def issue(self, token: int, pos: int, stream=None, logits: bool = True):
         """Enqueue one decode step (token at position pos) on `stream`."""
@@ -279,10 +274,16 @@ class ForwardStep:
                 self.vc[l].data_ptr(), None, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta, 1.0, 0, c.neox,
                 self.scale, sp))
             self._fused(("o",), l, self.att, (self.hidden,), c.n_heads * c.head_dim, None, True, sp)
-            self._fused(("gate", "up"), l, self.hidden, (self.gate, self.up), c.hidden, self.w["ffn_norm"][l],
-                        False, sp)
-            check("hip_swiglu_async", L.hip_swiglu_async(self.act.data_ptr(), self.gate.data_ptr(),
-                                                         self.up.data_ptr(), c.ffn, sp))
+            if c.type_of("gate") == c.type_of("up"):
+                check("hip_gemv_swiglu_async", L.hip_gemv_swiglu_async(
+                    c.type_of("gate"), self.w["gate"][l].data_ptr(), self.w["up"][l].data_ptr(), self.act.data_ptr(),
+                    c.ffn, self.hidden.data_ptr(), self.w["ffn_norm"][l].data_ptr(), c.hidden,
+                    self.scratch.data_ptr(), sp))
+            else:
+                self._fused(("gate", "up"), l, self.hidden, (self.gate, self.up), c.hidden, self.w["ffn_norm"][l],
+                            False, sp)
+                check("hip_swiglu_async", L.hip_swiglu_async(self.act.data_ptr(), self.gate.data_ptr(),
+                                                             self.up.data_ptr(), c.ffn, sp))
             self._fused(("down",), l, self.act, (self.hidden,), c.ffn, None, True, sp)
         if logits:
             self._fused(("head",), None, self.hidden, (self.logits,), c.hidden, self.w["out_norm"], False, sp)

@@ -129,6 +129,18 @@ def gemv_fused_async(L, ggml_type, w_ptrs, y_ptrs, out_dims, x_ptr, in_dim, stre
                                  scratch_ptr, stream_ptr))
 
 
+def gemv_group_async(L, types, w_ptrs, y_ptrs, out_dims, x_ptr, in_dim, stream_ptr, norm_ptr=None,
+                     accumulate=False, scratch_ptr=None):
+    """hip_gemv_group_async: GEMVs of per-matrix types sharing x (fused norm /
+    residual optional), host arrays built from Python ints."""
+    import ctypes as C
+    k = len(w_ptrs)
+    check("hip_gemv_group_async",
+          L.hip_gemv_group_async(k, (C.c_uint32 * k)(*types), (C.c_void_p * k)(*w_ptrs), (C.c_void_p * k)(*y_ptrs),
+                                 (C.c_int * k)(*out_dims), x_ptr, norm_ptr, 1 if accumulate else 0, in_dim,
+                                 scratch_ptr, stream_ptr))
+
+
 def gemm_grouped_async(L, ggml_type, w_ptrs, x_ptrs, y_ptrs, ns, out_dims, in_dim, stream_ptr):
     """hip_gemm_grouped_async with host arrays built from Python ints (device pointers)."""
     import ctypes as C

@@ -57,3 +57,67 @@ def test_gemv_fused_needs_scratch_only_on_fallback(qh):
                                      x.ptr, n.ptr, 0, 4096, None, None)
         assert rc == want
     check("hip_sync", qh.hip_sync())
+
+
+def silu(g):
+    return g / (1.0 + np.exp(-g))
+
+
+@pytest.mark.parametrize("t", [12, 13, 14, 8])
+@pytest.mark.parametrize("ffn, in_dim", [(1024, 512), (14336, 4096), (999, 1024), (40000, 512), (300, 4352)],
+                         ids=str)
+@pytest.mark.parametrize("norm", [True, False])
+def test_gemv_swiglu(qh, oracle, t, ffn, in_dim, norm):
+    """hip_gemv_swiglu: silu(W_gate x') * (W_up x') in one launch (gate and up
+    tiles paired per workgroup; 40000 rows exercises many pairs per workgroup)
+    or through the separate kernels (Q8_0, in_dim past one workgroup's chunk)."""
+    if ffn * in_dim > 14336 * 4096 and t != 12:
+        pytest.skip("large shape only for Q4_K")
+    rng = np.random.default_rng(ffn + in_dim + t)
+    x = (rng.standard_normal(in_dim) * 1.5).astype(np.float32)
+    nw = (1 + 0.2 * rng.standard_normal(in_dim)).astype(np.float32)
+    wg, wu = synth.weights(t, ffn, in_dim, seed=11), synth.weights(t, ffn, in_dim, seed=12)
+    dg, du = GpuBuf.upload(wg), GpuBuf.upload(wu)
+    dx, dn, act = GpuBuf.upload_f32(x), GpuBuf.upload_f32(nw), GpuBuf.alloc_f32(ffn)
+    scratch = GpuBuf.alloc_f32(in_dim + 2 * ffn)
+    check("hip_gemv_swiglu_async", qh.hip_gemv_swiglu_async(t, dg.ptr, du.ptr, act.ptr, ffn, dx.ptr,
+                                                            dn.ptr if norm else None, in_dim, scratch.ptr, None))
+    check("hip_sync", qh.hip_sync())
+    xin = rms(x, nw) if norm else x.astype(np.float64)
+    g = oracle.dequant(t, wg, ffn * in_dim).astype(np.float64).reshape(ffn, in_dim) @ xin
+    u = oracle.dequant(t, wu, ffn * in_dim).astype(np.float64).reshape(ffn, in_dim) @ xin
+    ref = silu(g) * u
+    got = act.download(np.float32)[:ffn]
+    assert np.all(np.isfinite(got))
+    assert cf.rel_l2(got, ref) < 1e-3, cf.rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("types, dims", [((12, 12, 14), (4096, 1024, 1024)), ((14, 12), (300, 700)),
+                                         ((13, 14), (1000, 37)), ((12, 13), (64, 4096)), ((12, 8), (500, 500)),
+                                         ((12, 14, 13), (100, 200, 300))], ids=str)
+@pytest.mark.parametrize("in_dim", [4096, 1024, 14336])
+@pytest.mark.parametrize("norm, acc", [(True, False), (False, True), (False, False)])
+def test_gemv_group(qh, oracle, types, dims, in_dim, norm, acc):
+    """hip_gemv_group: per-matrix types sharing x; two matrix-core types run as
+    one split launch, other mixes per type.  Each y against the oracle."""
+    from saient_quartz_amd.host import gemv_group_async
+    if norm and in_dim > 4096:
+        pytest.skip("covered by the fused tests")
+    rng = np.random.default_rng(in_dim + sum(dims))
+    x = (rng.standard_normal(in_dim) * 2).astype(np.float32)
+    nw = (1 + 0.2 * rng.standard_normal(in_dim)).astype(np.float32)
+    datas = [synth.weights(t, o, in_dim, seed=70 + k) for k, (t, o) in enumerate(zip(types, dims))]
+    y0 = [rng.standard_normal(o).astype(np.float32) for o in dims]
+    ws = [GpuBuf.upload(d) for d in datas]
+    ys = [GpuBuf.upload_f32(a) for a in y0]
+    dx, dn = GpuBuf.upload_f32(x), GpuBuf.upload_f32(nw)
+    scratch = GpuBuf.alloc_f32(in_dim + max(dims))
+    gemv_group_async(qh, list(types), [w.ptr for w in ws], [y.ptr for y in ys], list(dims), dx.ptr, in_dim, None,
+                     norm_ptr=dn.ptr if norm else None, accumulate=acc, scratch_ptr=scratch.ptr)
+    check("hip_sync", qh.hip_sync())
+    xin = rms(x, nw) if norm else x.astype(np.float64)
+    for k, (t, o) in enumerate(zip(types, dims)):
+        w = oracle.dequant(t, datas[k], o * in_dim).astype(np.float64).reshape(o, in_dim)
+        ref = w @ xin + (y0[k] if acc else 0.0)
+        got = ys[k].download(np.float32)[:o]
+        assert cf.rel_l2(got, ref) < 1e-3, (k, t, cf.rel_l2(got, ref))
