@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the 8B-shape decode-step leg")
     ap.add_argument("--decode-reps", type=int, default=20)
+    ap.add_argument("--only-forward", action="store_true",
+                    help="only run the end-to-end decode-step leg (for profiling its kernels)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 256 MiB (torch copy kernel), to calibrate the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes")
@@ -56,6 +58,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel(), "copies": 5}))
+        return
+
+    if args.only_forward:
+        from saient_quartz_amd.decode import ModelConfig
+        wbytes = ModelConfig().weight_bytes()
+        print(json.dumps({"forward": forward_leg(torch, args.decode_reps, wbytes)}), flush=True)
         return
 
     from saient_quartz_amd import lib, synth_device, type_size
