@@ -36,7 +36,7 @@ typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
 #define QH_XG_SUM 768
 #define QH_XG_ZERO 832
 #define QH_RS 240   // LDS line per row: 15 x 16 bytes, conflict-free b128 reads over 16 rows
-#define QH_MAXT 32  // row tiles per workgroup (their results wait in LDS until the end)
+#define QH_MAXT 64  // row tiles per workgroup (their results wait in LDS until the end)
 #define QH_RING 4   // finished tiles per workgroup barrier (launches with few tiles)
 
 QH_DEV uint32_t qh_lo4(uint32_t q) { return q & 0x0F0F0F0Fu; }
@@ -55,9 +55,10 @@ QH_DEV uint32_t qh_hi4(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
 // (MFMAs 2, 3).  qs chunk c holds sub-blocks 2(c/2) (low) and 2(c/2)+1 (high),
 // positions 16(c%2) .. +15.
 struct M16Q4K {
-    static constexpr int BYTES = 144, CH = 9, ROWS = 14, LAST = 128;
+    static constexpr int BYTES = 144, CH = 9, ROWS = 14, LAST = 128, RS = QH_RS;
+    static constexpr bool FLOAT_D = false;
     struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
-    static QH_DEV H hdr(const unsigned char* r) {
+    static QH_DEV H hdr(const unsigned char* r, int) {
         const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
         H o;
         o.sc0 = h.y & 0x3F3F3F3Fu;
@@ -96,9 +97,10 @@ struct M16Q4K {
 // Weight of sub-block j, position l: d*sc*(nibble + 16*bit_j(qh[l])) - dmin*m.
 // Chunks as Q4_K (qs at byte 48); both of lane kg's chunks use qh[16(kg%2) ..].
 struct M16Q5K {
-    static constexpr int BYTES = 176, CH = 11, ROWS = 11, LAST = 160;
+    static constexpr int BYTES = 176, CH = 11, ROWS = 11, LAST = 160, RS = QH_RS;
+    static constexpr bool FLOAT_D = false;
     using H = M16Q4K::H;
-    static QH_DEV H hdr(const unsigned char* r) { return M16Q4K::hdr(r); }
+    static QH_DEV H hdr(const unsigned char* r, int kg) { return M16Q4K::hdr(r, kg); }
     static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
         const qh_u32x4 q0 = *reinterpret_cast<const qh_u32x4*>(r + 48 + 16 * kg);
         const qh_u32x4 q1 = *reinterpret_cast<const qh_u32x4*>(r + 112 + 16 * kg);
@@ -131,9 +133,10 @@ struct M16Q6K {
     static constexpr int BYTES = 210, CH = 14, ROWS = 16;
     // The 14th slice is loaded from block bytes 194-209 (not 208-223), so no load
     // leaves the block: the LDS line then holds bytes 0-207 at 0-207 and d at 222.
-    static constexpr int LAST = 194;
+    static constexpr int LAST = 194, RS = QH_RS;
+    static constexpr bool FLOAT_D = false;
     struct H { qh_u32x4 s; float d, dm; };
-    static QH_DEV H hdr(const unsigned char* r) {
+    static QH_DEV H hdr(const unsigned char* r, int) {
         H o;
         o.s = *reinterpret_cast<const qh_u32x4*>(r + 192);
         o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 222));
@@ -163,11 +166,46 @@ struct M16Q6K {
     static QH_DEV int mn(const H& h, int kg) { return scl<S>(h, kg); }
 };
 
+// Q8_0: blocks of [d f16][32 x int8] (src/dequant.rs:1450-1463); a group is 8
+// blocks (272 bytes, so groups stay 16-byte aligned in a row).  Piece p (16
+// weights) is half p % 2 of block p / 2: its quants are the B operand as they
+// are (int8), read with an unaligned ds_read_b128 at block byte 2 + 16 (p % 2);
+// each piece has its own f32 scale d (FLOAT_D), no mins.  Line stride 272 B
+// puts the 16 rows of a column 4 banks apart.
+struct M16Q80 {
+    static constexpr int BYTES = 272, CH = 17, ROWS = 15, LAST = 256, RS = 272;
+    static constexpr bool FLOAT_D = true;
+    struct H { float d[4]; float dm; };
+    template <int S>
+    static QH_DEV int piece(int kg) { return 4 * S + kg; }
+    static QH_DEV H hdr(const unsigned char* r, int kg) {
+        H o;
+#pragma unroll
+        for (int s = 0; s < 4; s++) o.d[s] = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 34 * ((4 * s + kg) >> 1)));
+        o.dm = 0.f;
+        return o;
+    }
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int p = 4 * s + kg;
+            __builtin_memcpy(&B[s], r + 34 * (p >> 1) + 2 + 16 * (p & 1), 16);
+        }
+    }
+    template <int S>
+    static QH_DEV int scl(const H&, int) { return 1; }
+    template <int S>
+    static QH_DEV int mn(const H&, int) { return 0; }
+    template <int S>
+    static QH_DEV float dsc(const H& h) { return h.d[S]; }
+};
+
 // 16-row tiles of the same formats (3 loads per lane and group instead of 2):
 // chosen when they spread the tiles more evenly over the CUs (4096 rows = 256
 // tiles = one per CU).
 struct M16Q4K16 : M16Q4K { static constexpr int ROWS = 16; };
 struct M16Q5K16 : M16Q5K { static constexpr int ROWS = 16; };
+struct M16Q8016 : M16Q80 { static constexpr int ROWS = 16; };
 
 // ---------------------------------------------------------------- kernel
 
@@ -209,7 +247,7 @@ struct QhMats {
 // ring of wavefront partials, finished rows and the per-wavefront sums of x^2.
 template <class F, int W, int GPW>
 constexpr int qh_mmv16_lds() {
-    return W * GPW * (F::ROWS * QH_RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4;
+    return W * GPW * (F::ROWS * F::RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4;
 }
 
 // The kernel body for workgroup `bid` of `nblk` working on mm's tiles (a
@@ -219,8 +257,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                                               int ngroups, unsigned char* lds, const int bid, const int nblk) {
     constexpr int ROWS = F::ROWS, CH = F::CH;
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
-    static_assert(ROWS <= 16 && 16 * CH < QH_RS, "tile shape");
-    constexpr int TILE = ROWS * QH_RS + 16;  // staging tile of one group + 16 spare bytes
+    constexpr int RS = F::RS;                // LDS line per row
+    static_assert(ROWS <= 16 && 16 * CH <= RS, "tile shape");
+    constexpr int TILE = ROWS * RS + 16;  // staging tile of one group + 16 spare bytes
     // Wavefront partials of finished tiles wait in a ring of two sets of QH_RING
     // tiles; the workgroup meets at a barrier only when a set is full.
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -264,7 +303,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         rr[h] = q < ROWS * CH ? r : 1 << 30;
         goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         // Lanes past ROWS * CH store into the spare bytes after the tile's last line.
-        soff[h] = q < ROWS * CH ? (uint32_t)(r * QH_RS + 16 * c) : (uint32_t)(ROWS * QH_RS);
+        soff[h] = q < ROWS * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(ROWS * RS);
     }
     const int n = lane & 15, kg = lane >> 4;
     // A operand of MFMA s: digit plane n%4 of lane kg's piece in rows 4kg..4kg+2.
@@ -405,8 +444,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         float acc = 0.f, accm = 0.f;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
-            const unsigned char* wrow = wl + t * TILE + (n < ROWS ? n : 0) * QH_RS;
-            const typename F::H hd = F::hdr(wrow);
+            const unsigned char* wrow = wl + t * TILE + (n < ROWS ? n : 0) * RS;
+            const typename F::H hd = F::hdr(wrow, kg);
             qh_i32x4 B[4];
             F::bops(wrow, kg, hd, B);
             int i0 = 0, i1 = 0, i2 = 0;
@@ -416,21 +455,29 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                 constexpr int S = decltype(SC)::value;
                 const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xt + aoff[S]);
                 const qh_i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[S], qh_i32x4{0, 0, 0, 0}, 0, 0, 0);
-                const int sc = F::template scl<S>(hd, kg);
-                i0 += __mul24(sc, D[0]);
-                i1 += __mul24(sc, D[1]);
-                i2 += __mul24(sc, D[2]);
-                const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
-                fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+                if constexpr (F::FLOAT_D) {
+                    // each piece has its own f32 scale (the digit dots are exact in f32)
+                    const float P = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
+                    acc = fmaf(F::template dsc<S>(hd), P, acc);
+                } else {
+                    const int sc = F::template scl<S>(hd, kg);
+                    i0 += __mul24(sc, D[0]);
+                    i1 += __mul24(sc, D[1]);
+                    i2 += __mul24(sc, D[2]);
+                    const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
+                    fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             };
             mfma(std::integral_constant<int, 0>{});
             mfma(std::integral_constant<int, 1>{});
             mfma(std::integral_constant<int, 2>{});
             mfma(std::integral_constant<int, 3>{});
-            const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
-            acc = fmaf(hd.d, P, acc);
-            accm = fmaf(hd.dm, fm, accm);
+            if constexpr (!F::FLOAT_D) {
+                const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
+                acc = fmaf(hd.d, P, acc);
+                accm = fmaf(hd.dm, fm, accm);
+            }
         }
         return fmaf(acc, rs, -accm);
     };
@@ -702,6 +749,10 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
                        ? dispatch_mmv16<M16Q5K16>(W, x, y, in_dim, out_dim, row_bytes, st)
                        : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q8_0:
+            return qh_rows16_better(M16Q80::ROWS, out_dim)
+                       ? dispatch_mmv16<M16Q8016>(W, x, y, in_dim, out_dim, row_bytes, st)
+                       : dispatch_mmv16<M16Q80>(W, x, y, in_dim, out_dim, row_bytes, st);
         default: return hipErrorNotSupported;
     }
 }
@@ -752,6 +803,10 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
                        ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
                        : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_Q8_0:
+            return qh_rows16_better(M16Q80::ROWS, total)
+                       ? multi_mmv16<M16Q8016>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                       : multi_mmv16<M16Q80>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         default: return hipErrorNotSupported;
     }
 }

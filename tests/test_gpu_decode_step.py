@@ -27,8 +27,10 @@ pytestmark = pytest.mark.gpu
 Q4_K, Q6_K, Q8_0, Q5_K = 12, 14, 8, 13
 LLAMA_TYPES = (("q", Q4_K), ("k", Q4_K), ("v", Q6_K), ("o", Q4_K), ("gate", Q4_K), ("up", Q4_K),
                ("down", Q6_K), ("head", Q6_K), ("embed", Q4_K))
-# no fused kernel for Q8_0: every GEMV takes the separate-kernel fallback through the scratch buffer
 Q8_TYPES = tuple((n, Q8_0) for n, _ in LLAMA_TYPES)
+# no fused kernel for Q5_0: every GEMV takes the separate-kernel fallback through the scratch buffer
+Q5_0 = 6
+Q50_TYPES = tuple((n, Q5_0) for n, _ in LLAMA_TYPES)
 MIXED_TYPES = (("q", Q5_K), ("k", Q4_K), ("v", Q8_0), ("o", Q6_K), ("gate", Q4_K), ("up", Q5_K),
                ("down", Q4_K), ("head", Q4_K), ("embed", Q6_K))
 
@@ -78,7 +80,8 @@ def oracle_model(oracle, cfg, raw, norms):
 
 CASES = {
     "llama_q4km": dict(types=LLAMA_TYPES),
-    "q8_0_fallback": dict(types=Q8_TYPES),
+    "q8_0": dict(types=Q8_TYPES),
+    "q5_0_fallback": dict(types=Q50_TYPES),
     "mixed": dict(types=MIXED_TYPES),
     # norm x past one workgroup's chunk (hidden > 4096): the unfused norm path for q/k/v/gate/up/head
     "wide": dict(types=LLAMA_TYPES, hidden=4352, n_heads=2, n_kv=1, ffn=512, vocab=64, layers=1),
