@@ -166,15 +166,15 @@ def decode_leg(torch, reps):
     weight GEMVs of one step (32 layers x 7 + head) captured in one HIP graph,
     timed over `reps` replays, for N = 1, 4, 16 tokens.  At N = 1 the q+k and
     gate+up projections go out as one hip_gemv_multi launch each ("n1"; "n1_unfused"
-    is one launch per matrix).  Weight streaming only: the glue kernels between
-    GEMVs are not part of this library yet."""
+    is one launch per matrix).  Weight streaming only; the end-to-end steps with
+    the glue are forward_leg's n*_full_* entries."""
     from saient_quartz_amd.decode import DecodeStep, Shape
 
     shape = Shape()
     wbytes = shape.weight_bytes()
     step = DecodeStep(shape, n_max=16)
-    out = {"workload": "Llama-3-8B-shaped Q4_K_M decode step, weight GEMVs only (32 layers x q,k,v,o,gate,up,down "
-                       "+ Q6_K head), random-init weights, synthetic activations",
+    out = {"workload": "Llama-3-8B-shaped Q4_K_M decode step, random-init weights: n*_full_* end to end (embedding "
+                       "to logits, N sequences in lockstep), n1/n4/n16 the weight GEMVs/GEMMs alone",
            "weight_bytes": wbytes, "roofline_tok_s_n1": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)}
     full = forward_leg(torch, reps, wbytes)
     out.update(full)
@@ -204,39 +204,51 @@ def decode_leg(torch, reps):
 
 
 def forward_leg(torch, reps, wbytes):
-    """End-to-end Llama-3-8B-shaped decode step (ForwardStep: embedding lookup,
-    32 x [fused norm + q/k/v, RoPE + KV append + attention, o + residual, fused
-    norm + gate/up, swiglu, down + residual], fused final norm + head), one HIP
-    graph per position, timed over `reps` replays at KV position 0 and 511."""
-    from saient_quartz_amd.decode import ForwardStep, ModelConfig
+    """End-to-end Llama-3-8B-shaped decode steps, one HIP graph per (N, position),
+    timed over `reps` replays at KV position 0 and 511:
+      N = 1: ForwardStep (embedding lookup, 32 x [fused norm + q/k/v, RoPE + KV
+             append + attention, o + residual, fused norm + gate/up + SwiGLU,
+             down + residual], fused final norm + head; 5 launches per layer);
+      N = 4, 16: BatchStep, N sequences in lockstep with their own K/V caches
+             (batched matrix-core GEMMs, one weight pass per 16 tokens, and
+             batched glue)."""
+    from saient_quartz_amd.decode import BatchStep, ForwardStep, ModelConfig
 
     cfg = ModelConfig(max_seq=1024)
-    step = ForwardStep(cfg, ForwardStep.random_weights(cfg))
+    weights = ForwardStep.random_weights(cfg)
     out = {}
-    for pos in (0, 511):
-        step.issue(1, pos)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step.issue(1, pos)
-        g.replay()
-        torch.cuda.synchronize()
-        if not torch.isfinite(step.logits).all():
-            raise SystemExit("decode step produced non-finite logits")
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(reps):
+    for n in (1, 4, 16):
+        step = ForwardStep(cfg, weights) if n == 1 else BatchStep(cfg, weights, n)
+        tokens = [(7 * i + 3) % 1000 for i in range(n)]
+        issue = (lambda pos: step.issue(tokens[0], pos)) if n == 1 else (lambda pos: step.issue(tokens, pos))
+        for pos in (0, 511):
+            issue(pos)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                issue(pos)
             g.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / reps
-        out[f"n1_full_pos{pos}"] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
-                                    "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
-                                    "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-                                    "launches": 1 + 5 * cfg.layers + 1}
-        del g
-    del step
+            torch.cuda.synchronize()
+            if not torch.isfinite(step.logits).all():
+                raise SystemExit("decode step produced non-finite logits")
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(reps):
+                g.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / reps
+            rec = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
+                   "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                   "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+            if n == 1:
+                rec["launches"] = 1 + 5 * cfg.layers + 1
+            out[f"n{n}_full_pos{pos}"] = rec
+            del g
+        del step
+        torch.cuda.empty_cache()
+    del weights
     torch.cuda.empty_cache()
     return out
 

@@ -177,6 +177,8 @@ int hip_vec_zero(float* dst, int n);
 int hip_vec_zero_async(float* dst, int n, void* stream);
 int hip_rms_norm(float* out, const float* x, const float* w, int n);                    /* eps 1e-5; out may be x */
 int hip_rms_norm_async(float* out, const float* x, const float* w, int n, void* stream);
+/* rows token-major rows of n: out[r] = rms_norm(x[r]) * w, one launch (batched decode). */
+int hip_rms_norm_rows_async(float* out, const float* x, const float* w, int rows, int n, void* stream);
 int hip_rope_yarn(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx,
                   int neox);
 int hip_rope_yarn_async(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale,
@@ -247,6 +249,14 @@ int hip_attention_step_async(float* out, const float* q, const float* k, const f
                              float* v_cache, const float* sinks, int n_heads, int n_kv_heads, int head_dim,
                              int kv_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox,
                              float scale, void* stream);
+/* hip_attention_step for n_seq sequences decoding in lockstep (all at row pos):
+ * sequence z uses q + z*n_heads*head_dim, k/v + z*kv_dim, out + z*n_heads*head_dim
+ * and its own caches k_cache/v_cache + z*cache_stride (floats, >= (pos+1)*kv_dim).
+ * One launch; n_seq * n_kv_heads <= 256. */
+int hip_attention_step_batched_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                                     float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                                     int n_kv_heads, int head_dim, int kv_dim, int pos, float theta, float yarn_scale,
+                                     int yarn_orig_ctx, int neox, float scale, void* stream);
 int hip_embed_lookup(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim);
 int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim,
                            void* stream);

@@ -52,6 +52,9 @@ _SIGS = {
                                        C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "hip_gemv_group_async": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "hip_rms_norm_rows_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "hip_attention_step_batched_async": (C.c_int, [C.c_void_p] * 7 + [C.c_int, C.c_size_t] + [C.c_int] * 5 +
+                                         [C.c_float, C.c_float, C.c_int, C.c_int, C.c_float, C.c_void_p]),
     "hip_gemv_swiglu_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                         C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     "hip_attention_step_async": (C.c_int, [C.c_void_p] * 7 + [C.c_int] * 5 + [C.c_float, C.c_float, C.c_int, C.c_int,

@@ -402,6 +402,11 @@ int hip_rms_norm_async(float* out, const float* x, const float* w, int n, void* 
     QH_GLUE(qh_glue_rms_norm(out, x, w, n, (hipStream_t)s), "hip_rms_norm");
 }
 int hip_rms_norm(float* out, const float* x, const float* w, int n) { return hip_rms_norm_async(out, x, w, n, nullptr); }
+int hip_rms_norm_rows_async(float* out, const float* x, const float* w, int rows, int n, void* s) {
+    if (n <= 0 || rows < 0) return (n == 0 || rows == 0) && rows >= 0 && n >= 0 ? QH_OK : QH_ERR_DIMS;
+    if (!out || !x || !w) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_rms_norm(out, x, w, n, (hipStream_t)s, rows), "hip_rms_norm_rows");
+}
 
 int hip_rope_yarn_async(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale,
                         int yarn_orig_ctx, int neox, void* s) {
@@ -506,21 +511,31 @@ int hip_attention_decode(float* out, const float* q, const float* k_cache, const
                                       scale, nullptr);
 }
 
+int hip_attention_step_batched_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                                     float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                                     int n_kv_heads, int head_dim, int kv_dim, int pos, float theta, float yarn_scale,
+                                     int yarn_orig_ctx, int neox, float scale, void* s) {
+    if (pos < 0 || n_seq < 0) return QH_ERR_DIMS;
+    int rc = qh_attn_dims(n_heads, n_kv_heads, pos + 1, head_dim, kv_dim, pos + 1);
+    if (rc) return rc;
+    if (n_kv_heads > n_heads && n_heads > 0) return QH_ERR_DIMS;
+    if (n_seq > 1 && cache_stride < (size_t)(pos + 1) * (size_t)kv_dim) return QH_ERR_DIMS;
+    if (n_heads == 0 || n_seq == 0) return QH_OK;
+    if (!out || !q || !k || !v || !k_cache || !v_cache) return QH_ERR_NULL;
+    hipError_t e = qh_glue_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_heads, n_kv_heads, head_dim,
+                                          kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, (hipStream_t)s,
+                                          n_seq, cache_stride);
+    if (e == hipErrorNotSupported) return QH_ERR_RANGE;
+    if (e != hipSuccess) return qh_fail(e, "hip_attention_step");
+    return QH_OK;
+}
+
 int hip_attention_step_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
                              float* v_cache, const float* sinks, int n_heads, int n_kv_heads, int head_dim,
                              int kv_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox,
                              float scale, void* s) {
-    if (pos < 0) return QH_ERR_DIMS;
-    int rc = qh_attn_dims(n_heads, n_kv_heads, pos + 1, head_dim, kv_dim, pos + 1);
-    if (rc) return rc;
-    if (n_kv_heads > n_heads && n_heads > 0) return QH_ERR_DIMS;
-    if (n_heads == 0) return QH_OK;
-    if (!out || !q || !k || !v || !k_cache || !v_cache) return QH_ERR_NULL;
-    hipError_t e = qh_glue_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_heads, n_kv_heads, head_dim,
-                                          kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, (hipStream_t)s);
-    if (e == hipErrorNotSupported) return QH_ERR_RANGE;
-    if (e != hipSuccess) return qh_fail(e, "hip_attention_step");
-    return QH_OK;
+    return hip_attention_step_batched_async(out, q, k, v, k_cache, v_cache, sinks, 1, 0, n_heads, n_kv_heads,
+                                            head_dim, kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, s);
 }
 
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* s) {

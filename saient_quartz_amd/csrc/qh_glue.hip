@@ -67,6 +67,9 @@ __global__ __launch_bounds__(256) void qg_vec_zero(float* dst, int n) {
 // In-place (out == x) is safe: every read of x precedes the reduction's barriers.
 __global__ __launch_bounds__(1024) void qg_rms_norm(float* out, const float* x, const float* w, int n) {
     __shared__ float sm[16];
+    // row blockIdx.x of a token-major batch (one row: the reference's kernel)
+    out += (size_t)blockIdx.x * n;
+    x += (size_t)blockIdx.x * n;
     float s = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) s += x[i] * x[i];
     s = qg_block_sum(s, sm);
@@ -247,17 +250,30 @@ __global__ __launch_bounds__(256) void qg_attention_decode(float* out, const flo
 static __device__ __align__(256) float qa_part[QA_PART];
 static __device__ __align__(256) unsigned int qa_cnt[QA_MAXKV];
 
+template <int HD>  // head_dim capacity: 128 or QA_MAXHD (LDS, so occupancy, scales with it)
 __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float* q, const float* k, const float* v,
                                                          float* kc, float* vc, const float* sinks, int n_heads,
                                                          int n_kv, int hd, int kv_dim, int pos, float theta,
                                                          float yarn_scale, int orig_ctx, int neox, float scale,
-                                                         float* part, unsigned int* cnt) {
-    __shared__ __align__(16) float kl[QA_ROWS * (QA_MAXHD + 4)];
-    __shared__ __align__(16) float vl[QA_ROWS * QA_MAXHD];
-    __shared__ __align__(16) float qr[QA_MAXG * QA_MAXHD];
-    __shared__ __align__(16) float kr[QA_MAXHD];
+                                                         float* part, unsigned int* cnt, size_t cache_stride) {
+    __shared__ __align__(16) float kl[QA_ROWS * (HD + 4)];
+    __shared__ __align__(16) float vl[QA_ROWS * HD];
+    __shared__ __align__(16) float qr[QA_MAXG * HD];
+    __shared__ __align__(16) float kr[HD];
     __shared__ int last_flag;
     const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
+    {
+        const size_t z = blockIdx.z;
+        q += z * (size_t)n_heads * hd;
+        out += z * (size_t)n_heads * hd;
+        k += z * (size_t)kv_dim;
+        v += z * (size_t)kv_dim;
+        kc += z * cache_stride;
+        vc += z * cache_stride;
+        part += z * (size_t)n_heads * nch * (hd + 2);
+        cnt += z * (size_t)n_kv;
+    }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int h0 = (g * n_heads + n_kv - 1) / n_kv, h1 = ((g + 1) * n_heads + n_kv - 1) / n_kv, ng = h1 - h0;
     const int seq = pos + 1, half = hd >> 1, kp = hd + 4;
@@ -287,13 +303,13 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         }
     }
     // running state of this wavefront's heads j = w, w + 4, ... (< ng)
-    float m[QA_MAXG / 4], l[QA_MAXG / 4], o[QA_MAXG / 4][QA_MAXHD / 64];
+    float m[QA_MAXG / 4], l[QA_MAXG / 4], o[QA_MAXG / 4][HD / 64];
 #pragma unroll
     for (int a = 0; a < QA_MAXG / 4; a++) {
         m[a] = -1e30f;
         l[a] = 0.f;
 #pragma unroll
-        for (int d = 0; d < QA_MAXHD / 64; d++) o[a][d] = 0.f;
+        for (int d = 0; d < HD / 64; d++) o[a][d] = 0.f;
     }
     const int t_l = lane & 31, hsel = lane >> 5;
     for (int sl = c; sl * QA_ROWS < seq; sl += nch) {
@@ -341,11 +357,11 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             l[a] = l[a] * corr + ps;
             m[a] = mn;
 #pragma unroll
-            for (int d = 0; d < QA_MAXHD / 64; d++) o[a][d] *= corr;
+            for (int d = 0; d < HD / 64; d++) o[a][d] *= corr;
             for (int t = 0; t < nv; t++) {
                 const float pt = __shfl(p, t);
 #pragma unroll
-                for (int d = 0; d < QA_MAXHD / 64; d++) {
+                for (int d = 0; d < HD / 64; d++) {
                     const int dd = lane + 64 * d;
                     if (dd < hd) o[a][d] = fmaf(pt, vl[t * hd + dd], o[a][d]);
                 }
@@ -362,7 +378,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         const float L = ll * expf(mm - M) + (sink > -1e29f ? expf(sink - M) : 0.f);
         const float f = expf(mm - M) / L;
 #pragma unroll
-        for (int d = 0; d < QA_MAXHD / 64; d++) {
+        for (int d = 0; d < HD / 64; d++) {
             const int dd = lane + 64 * d;
             if (dd < hd) out[(size_t)h * hd + dd] = oo[d] * f;
         }
@@ -388,7 +404,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             __hip_atomic_store(pr + 1, l[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
-        for (int d = 0; d < QA_MAXHD / 64; d++) {
+        for (int d = 0; d < HD / 64; d++) {
             const int dd = lane + 64 * d;
             if (dd < hd) __hip_atomic_store(pr + 2 + dd, o[a][d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -417,16 +433,16 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         float L = lc * e;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-        float oo[QA_MAXHD / 64];
+        float oo[HD / 64];
 #pragma unroll
-        for (int d = 0; d < QA_MAXHD / 64; d++) oo[d] = 0.f;
+        for (int d = 0; d < HD / 64; d++) oo[d] = 0.f;
         for (int c0 = 0; c0 < nch; c0 += 8) {
             // eight slices' loads in flight before any of them is used
-            float ov[8][QA_MAXHD / 64];
+            float ov[8][HD / 64];
 #pragma unroll
             for (int u = 0; u < 8; u++)
 #pragma unroll
-                for (int d = 0; d < QA_MAXHD / 64; d++) {
+                for (int d = 0; d < HD / 64; d++) {
                     const int dd = lane + 64 * d, cc = c0 + u;
                     const uint32_t off = (cc < nch && dd < hd) ? base + 4u * (cc * rec + 2 + dd) : 0x80000000u;
                     ov[u][d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pb.rs, (int)off, 0, 16));
@@ -435,7 +451,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             for (int u = 0; u < 8; u++) {
                 const float ec = __shfl(e, (c0 + u) & 63);
 #pragma unroll
-                for (int d = 0; d < QA_MAXHD / 64; d++) oo[d] = fmaf(c0 + u < nch ? ov[u][d] : 0.f, ec, oo[d]);
+                for (int d = 0; d < HD / 64; d++) oo[d] = fmaf(c0 + u < nch ? ov[u][d] : 0.f, ec, oo[d]);
             }
         }
         finish(j, M, L, oo, true);
@@ -490,9 +506,10 @@ hipError_t qh_glue_vec(int op, float* dst, const float* src, float scale, int n,
     return hipGetLastError();
 }
 
-hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st) {
+hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st, int rows) {
     const int blk = n >= 4096 ? 1024 : n >= 1024 ? 256 : 64;
-    hipLaunchKernelGGL(qg_rms_norm, dim3(1), dim3(blk), 0, st, out, x, w, n);
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(qg_rms_norm, dim3((unsigned)rows), dim3(blk), 0, st, out, x, w, n);
     return hipGetLastError();
 }
 
@@ -555,9 +572,10 @@ static const QaScratch* qa_scratch_ptrs() {
 
 hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
                                   const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
-                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st) {
-    if (pos < 0 || hd <= 0 || (hd & 3) || hd > QA_MAXHD || n_kv > QA_MAXKV || (kv_dim & 3) ||
-        ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)k & 15))
+                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st, int n_seq,
+                                  size_t cache_stride) {
+    if (pos < 0 || hd <= 0 || (hd & 3) || hd > QA_MAXHD || n_seq < 1 || n_kv * n_seq > QA_MAXKV || (kv_dim & 3) ||
+        (cache_stride & 3) || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15))
         return hipErrorNotSupported;
     if (n_heads <= 0) return hipSuccess;
     // q heads per kv head (the largest group)
@@ -566,11 +584,17 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
     if (!sc) return hipErrorInvalidDevice;
     const int slices = (pos + QA_ROWS) / QA_ROWS;
     int nch = slices < QA_MAXCH ? slices : QA_MAXCH;
-    const int cap = QA_PART / (n_heads * (hd + 2));
+    const int cap = QA_PART / (n_seq * n_heads * (hd + 2));
     if (nch > cap) nch = cap;
-    if (nch < 1) nch = 1;
-    hipLaunchKernelGGL(qg_attention_step, dim3(n_kv, nch), dim3(256), 0, st, out, q, k, v, kc, vc, sinks, n_heads,
-                       n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale, sc->part, sc->cnt);
+    if (nch < 1) return hipErrorNotSupported;
+    if (hd <= 128)
+        hipLaunchKernelGGL(qg_attention_step<128>, dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc, vc,
+                           sinks, n_heads, n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale, sc->part,
+                           sc->cnt, cache_stride);
+    else
+        hipLaunchKernelGGL(qg_attention_step<QA_MAXHD>, dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc,
+                           vc, sinks, n_heads, n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale,
+                           sc->part, sc->cnt, cache_stride);
     return hipGetLastError();
 }
 

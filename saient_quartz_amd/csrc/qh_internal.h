@@ -66,7 +66,7 @@ hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float
 void qh_set_error(const char* msg);
 // Decode-step glue kernels (qh_glue.hip).
 hipError_t qh_glue_vec(int op, float* dst, const float* src, float scale, int n, hipStream_t st);
-hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st);
+hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st, int rows = 1);
 hipError_t qh_glue_rope(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale, int orig_ctx,
                         int neox, hipStream_t st);
 hipError_t qh_glue_kv_append(float* kc, float* vc, const float* k, const float* v, int pos, int kv_dim,
@@ -77,7 +77,8 @@ hipError_t qh_glue_attention_decode(float* out, const float* q, const float* kc,
                                     int n_heads, int n_kv, int seq, int hd, int kv_dim, float scale, hipStream_t st);
 hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
                                   const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
-                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st);
+                                  float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st, int n_seq = 1,
+                                  size_t cache_stride = 0);
 hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* up, int n, hipStream_t st);
 hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st);  // hip_last_error() text
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

@@ -287,3 +287,76 @@ class ForwardStep:
             self._fused(("down",), l, self.act, (self.hidden,), c.ffn, None, True, sp)
         if logits:
             self._fused(("head",), None, self.hidden, (self.logits,), c.hidden, self.w["out_norm"], False, sp)
+
+
+class BatchStep:
+    """forward_gpu_step for n sequences decoding in lockstep (token batch N of
+    BatchConfig configs[3]): every sequence has its own token, hidden state and
+    K/V cache, all at the same position.  The weight products are batched GEMMs
+    (hip_gemm_grouped: one weight pass per 16 tokens on the matrix cores; q/k
+    share one launch, v another, since they differ in type); the glue is one
+    launch per layer step for all sequences (hip_rms_norm_rows,
+    hip_attention_step_batched, hip_swiglu and hip_vec_add over n rows).
+    Weights: the dict ForwardStep takes."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict, n: int):
+        import math
+        self.cfg, self.L, self.w, self.n = cfg, lib(), weights, n
+        c = cfg
+        qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+        f32 = dict(device="cuda", dtype=torch.float32)
+        z = lambda d: torch.zeros(n, d, **f32)
+        self.hidden, self.xn, self.tmp = z(c.hidden), z(c.hidden), z(c.hidden)
+        self.q, self.k, self.v, self.att = z(qd), z(kvd), z(kvd), z(qd)
+        self.gate, self.up, self.act = z(c.ffn), z(c.ffn), z(c.ffn)
+        self.logits = z(c.vocab)
+        self.tokens = torch.zeros(n, dtype=torch.int32)
+        self.cache_stride = c.max_seq * kvd
+        self.kc = [torch.zeros(n * self.cache_stride, **f32) for _ in range(c.layers)]
+        self.vc = [torch.zeros(n * self.cache_stride, **f32) for _ in range(c.layers)]
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+
+    def _gemm(self, names, layer, x, ys, in_dim, sp):
+        """Batched GEMMs of the matrices `names` sharing x, one call per weight type."""
+        by_type = {}
+        for nm, y in zip(names, ys):
+            by_type.setdefault(self.cfg.type_of(nm), []).append((nm, y))
+        for t, group in by_type.items():
+            ws = [(self.w[nm][layer] if layer is not None else self.w[nm]).data_ptr() for nm, _ in group]
+            gemm_grouped_async(self.L, t, ws, [x.data_ptr()] * len(group), [y.data_ptr() for _, y in group],
+                               [self.n] * len(group), [y.shape[1] for _, y in group], in_dim, sp)
+
+    def issue(self, tokens, pos: int, stream=None, logits: bool = True):
+        """Enqueue one lockstep decode step: sequence i takes tokens[i] at `pos`."""
+        c, L, n = self.cfg, self.L, self.n
+        assert len(tokens) == n and 0 <= pos < c.max_seq
+        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        kvd = c.n_kv * c.head_dim
+        row = self.hidden.stride(0)
+        for i, t in enumerate(tokens):
+            check("hip_embed_lookup_async", L.hip_embed_lookup_async(
+                self.hidden.data_ptr() + 4 * i * row, self.w["embed"].data_ptr(), c.type_of("embed"), int(t),
+                c.hidden, sp))
+        for l in range(c.layers):
+            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
+                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["attn_norm"][l].data_ptr(), n, c.hidden, sp))
+            self._gemm(("q", "k", "v"), l, self.xn, (self.q, self.k, self.v), c.hidden, sp)
+            check("hip_attention_step_batched_async", L.hip_attention_step_batched_async(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
+                self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta,
+                1.0, 0, c.neox, self.scale, sp))
+            self._gemm(("o",), l, self.att, (self.tmp,), c.n_heads * c.head_dim, sp)
+            check("hip_vec_add_async", L.hip_vec_add_async(self.hidden.data_ptr(), self.tmp.data_ptr(),
+                                                           n * c.hidden, sp))
+            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
+                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["ffn_norm"][l].data_ptr(), n, c.hidden, sp))
+            self._gemm(("gate", "up"), l, self.xn, (self.gate, self.up), c.hidden, sp)
+            check("hip_swiglu_async", L.hip_swiglu_async(self.act.data_ptr(), self.gate.data_ptr(),
+                                                         self.up.data_ptr(), n * c.ffn, sp))
+            self._gemm(("down",), l, self.act, (self.tmp,), c.ffn, sp)
+            check("hip_vec_add_async", L.hip_vec_add_async(self.hidden.data_ptr(), self.tmp.data_ptr(),
+                                                           n * c.hidden, sp))
+        if logits:
+            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
+                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["out_norm"].data_ptr(), n, c.hidden, sp))
+            self._gemm(("head",), None, self.xn, (self.logits,), c.hidden, sp)

@@ -216,3 +216,43 @@ def test_attention_step_repeat(qh):
         sync(qh)
         outs.append(down(o, nh * hd))
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("n_seq, pos", [(1, 40), (4, 0), (4, 77), (16, 300)])
+def test_attention_step_batched(qh, n_seq, pos):
+    """hip_attention_step_batched: each sequence against its own single-sequence
+    oracle (own q/k/v rows and own cache), 1e-5 relative L2."""
+    nh, nkv, hd = 8, 2, 128
+    kvd = nkv * hd
+    max_seq = pos + 2
+    rng = np.random.default_rng(n_seq * 1000 + pos)
+    q = rng.standard_normal((n_seq, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((n_seq, kvd)).astype(np.float32)
+    v = rng.standard_normal((n_seq, kvd)).astype(np.float32)
+    kc = rng.standard_normal((n_seq, max_seq, kvd)).astype(np.float32)
+    vc = rng.standard_normal((n_seq, max_seq, kvd)).astype(np.float32)
+    dq, dk, dv, dkc, dvc = up(q), up(k), up(v), up(kc), up(vc)
+    do = GpuBuf.alloc_f32(n_seq * nh * hd)
+    check("batched", qh.hip_attention_step_batched_async(do.ptr, dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr, None,
+                                                         n_seq, max_seq * kvd, nh, nkv, hd, kvd, pos, 10000.0, 1.0,
+                                                         0, 0, 0.09, None))
+    sync(qh)
+    got = down(do, n_seq * nh * hd).reshape(n_seq, nh * hd)
+    for z in range(n_seq):
+        qr = g.rope_yarn(q[z], nh, hd, pos, 10000.0)
+        kr = g.rope_yarn(k[z], nkv, hd, pos, 10000.0)
+        kc64, vc64 = kc[z].astype(np.float64), vc[z].astype(np.float64)
+        kc64[pos], vc64[pos] = kr, v[z]
+        _, ref = g.attention(qr, kc64, vc64, nh, nkv, pos + 1, hd, kvd, 0.09)
+        assert cf.rel_l2(got[z], ref) < 1e-5, z
+
+
+def test_rms_norm_rows(qh):
+    rng = np.random.default_rng(5)
+    x, w = rng.standard_normal((7, 4096)) * 2, rng.standard_normal(4096)
+    dx, dw, do = up(x), up(w), GpuBuf.alloc_f32(7 * 4096)
+    check("rows", qh.hip_rms_norm_rows_async(do.ptr, dx.ptr, dw.ptr, 7, 4096, None))
+    sync(qh)
+    got = down(do, 7 * 4096).reshape(7, 4096)
+    for r in range(7):
+        assert cf.rel_l2(got[r], g.rms_norm(x[r].astype(np.float32), w.astype(np.float32))) < 1e-5
