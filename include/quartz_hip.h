@@ -105,6 +105,20 @@ int hip_gemm_grouped(uint32_t ggml_type, int count, const uint8_t* const* W, con
 int hip_gemm_grouped_async(uint32_t ggml_type, int count, const uint8_t* const* W, const float* const* x,
                            float* const* y, const int* n, const int* out_dims, int in_dim, void* stream);
 
+/* hip_gemm_grouped with the batched decode step's neighbours fused in:
+ * x_up != NULL: the GEMM's input is silu(x[k]) * x_up[k] (x[k] the gate rows,
+ *   x_up[k] the up rows, token-major [n[k]][in_dim]): cuda_swiglu before the down
+ *   projection, applied while x is digitised (src/cuda.rs:785-792);
+ * accumulate != 0: y[k] += product, the residual cuda_vec_add
+ *   (src/cuda.rs:647-662, :797-799).
+ * One prologue + one main launch on the matrix cores when every n[k] >= 2 and
+ * the type has the batched kernel; otherwise separate kernels on scratch
+ * (device, n*in_dim + n*max(out_dims) floats per matrix in turn; NULL is
+ * QH_ERR_NULL then).  x / x_up must not alias y. */
+int hip_gemm_grouped_ex_async(uint32_t ggml_type, int count, const uint8_t* const* W, const float* const* x,
+                              const float* const* x_up, float* const* y, const int* n, const int* out_dims,
+                              int in_dim, int accumulate, float* scratch, void* stream);
+
 /* Mixture-of-experts layer GEMMs over gathered tokens: for i < n_sel, expert
  * e = expert_ids[i] (its weights at d_experts + e * hip_type_size(type,
  * in_dim*out_dim), the expert slicing of src/cuda.rs:250-258 / :723-725)

@@ -319,6 +319,53 @@ int hip_gemm_grouped(uint32_t type, int count, const uint8_t* const* W, const fl
     return hip_gemm_grouped_async(type, count, W, x, y, n, out_dims, in_dim, nullptr);
 }
 
+int hip_gemm_grouped_ex_async(uint32_t type, int count, const uint8_t* const* W, const float* const* x,
+                              const float* const* x_up, float* const* y, const int* n, const int* out_dims,
+                              int in_dim, int accumulate, float* scratch, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (!x_up && !accumulate) return hip_gemm_grouped_async(type, count, W, x, y, n, out_dims, in_dim, stream);
+    if (count < 0) return QH_ERR_RANGE;
+    if (count == 0) return QH_OK;
+    if (!W || !x || !y || !n || !out_dims) return QH_ERR_NULL;
+    if (qh_block_elems(type) == 0) {
+        int rc = QH_ERR_TYPE;
+        for (int k = 0; k < count; k++) {
+            const size_t cnt = (out_dims[k] > 0 && n[k] > 0) ? (size_t)out_dims[k] * (size_t)n[k] : 0;
+            rc = qh_unknown_type("hip_gemm_grouped_ex", type, cnt ? y[k] : nullptr, cnt, st);
+        }
+        return rc;
+    }
+    bool batched = true;
+    for (int k = 0; k < count; k++) {
+        int rc = qh_check_dims(type, in_dim, out_dims[k]);
+        if (rc) return rc;
+        if (n[k] < 0) return QH_ERR_DIMS;
+        if (n[k] > 0 && out_dims[k] > 0 && (!W[k] || !x[k] || !y[k] || (x_up && !x_up[k]))) return QH_ERR_NULL;
+        batched = batched && n[k] > 1;
+    }
+    if (batched && !qh_force_valu()) {
+        hipError_t e = qh_launch_mmq_grouped(type, count, W, x, y, n, out_dims, in_dim, st, x_up, accumulate ? 1 : 0);
+        if (e == hipSuccess) return QH_OK;
+        if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_grouped_ex");
+    }
+    // separate kernels through scratch: [act (n in_dim)] [product (n out_dim)]
+    if (!scratch) return QH_ERR_NULL;
+    for (int k = 0; k < count; k++) {
+        if (n[k] == 0 || out_dims[k] == 0) continue;
+        const size_t nx = (size_t)n[k] * (size_t)in_dim;
+        const float* xk = x[k];
+        if (x_up) {
+            QH_CHECK(qh_glue_swiglu(0, scratch, x[k], x_up[k], (int)nx, st), "hip_gemm_grouped_ex");
+            xk = scratch;
+        }
+        float* yk = accumulate ? scratch + (x_up ? nx : 0) : y[k];
+        int rc = hip_gemm_async(type, W[k], xk, yk, in_dim, out_dims[k], n[k], stream);
+        if (rc) return rc;
+        if (accumulate) QH_CHECK(qh_glue_vec(0, y[k], yk, 0.f, n[k] * out_dims[k], st), "hip_gemm_grouped_ex");
+    }
+    return QH_OK;
+}
+
 int hip_gemm_moe_async(uint32_t type, const uint8_t* experts, int n_sel, const int* expert_ids, const int* tok_off,
                        const float* x, float* y, int in_dim, int out_dim, void* stream) {
     if (n_sel < 0) return QH_ERR_RANGE;

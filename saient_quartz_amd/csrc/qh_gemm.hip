@@ -235,6 +235,7 @@ static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES];
 #define QG_MAXG 16  // matrices (or row chunks) per grouped launch
 struct QgXs {        // the distinct token blocks of one grouped launch
     const float* x[QG_MAXG];
+    const float* x2[QG_MAXG];  // SwiGLU: x is silu(x) * x2 (gate, up) when non-null
     int n[QG_MAXG];  // tokens (<= 16)
 };
 struct QgGroups {    // the matrices of one grouped launch
@@ -246,6 +247,7 @@ struct QgGroups {    // the matrices of one grouped launch
     int ldy[QG_MAXG];          // y token stride
     int slot[QG_MAXG];         // x image slot
     int bstart[QG_MAXG + 1];   // first workgroup of each matrix; entries past the count are INT_MAX
+    int accum;                 // y += result (the residual add) instead of y = result
 };
 
 // One workgroup (256 threads) per group: thread T digitises elements 16 (T%16)
@@ -273,6 +275,17 @@ __global__ __launch_bounds__(256) void qh_mmq_ximg(const QgXs xs, unsigned char*
     for (int i = 0; i < 4; i++) {
         const qh_u32x4 u = qh_ld128(xb, off + 16u * i);
         v[i] = float4{__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
+    }
+    if (const float* x2 = xs.x2[blockIdx.y]) {
+        // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
+        const QhBuf ub = qh_buf(x2, 4u * (uint32_t)n * (uint32_t)in_dim);
+        auto sw = [](float gv, float uv) { return (gv / (1.f + expf(-gv))) * uv; };
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const qh_u32x4 u = qh_ld128(ub, off + 16u * i);
+            v[i] = float4{sw(v[i].x, __uint_as_float(u.x)), sw(v[i].y, __uint_as_float(u.y)),
+                          sw(v[i].z, __uint_as_float(u.z)), sw(v[i].w, __uint_as_float(u.w))};
+        }
     }
     float m = 0.f;
 #pragma unroll
@@ -591,7 +604,10 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const unsign
     }
     auto put = [&](int i, float a) {
         const int t = i >> 5, row = tile * 32 + (i & 31);
-        if (t < n && row < out_dim) y[(size_t)t * ldy + row] = a;
+        if (t < n && row < out_dim) {
+            float* yp = y + (size_t)t * ldy + row;
+            *yp = gs.accum ? *yp + a : a;
+        }
     };
     if (splits == 1) {
 #pragma unroll
@@ -706,6 +722,7 @@ static size_t qg_slot_bytes(uint32_t type, int ngroups) {
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
     const uint8_t* w;
     const float* x;
+    const float* x2;  // SwiGLU up (x is the gate), or null
     float* y;
     int n, rows, ldy;
 };
@@ -713,7 +730,7 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
 // One grouped launch pair: the prologue digitises every distinct token block
 // into its image slot, then the main kernel covers every entry's row tiles.
 static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, uint32_t row_bytes,
-                         const QgScratch& sc, hipStream_t st) {
+                         const QgScratch& sc, hipStream_t st, int accum) {
     const int ngroups = in_dim / 256;
     const int waves = qh_mmq_waves_env() ? qh_mmq_waves_env() : QG_WAVES;
     QgXs xs = {};
@@ -721,9 +738,10 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     int nslots = 0, ntmax = 0, tiles = 0;
     for (int i = 0; i < cnt; i++) {
         int j = 0;
-        while (j < nslots && !(xs.x[j] == en[i].x && xs.n[j] == en[i].n)) j++;
+        while (j < nslots && !(xs.x[j] == en[i].x && xs.x2[j] == en[i].x2 && xs.n[j] == en[i].n)) j++;
         if (j == nslots) {
             xs.x[j] = en[i].x;
+            xs.x2[j] = en[i].x2;
             xs.n[j] = en[i].n;
             nslots++;
         }
@@ -754,6 +772,7 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         if (i < cnt) wgs += (en[i].rows + 31) / 32 * splits;
     }
     gs.bstart[QG_MAXG] = INT_MAX;
+    gs.accum = accum;
 
     const dim3 pg((unsigned)ngroups, (unsigned)nslots);
     if (type == QT_Q6_K)
@@ -783,7 +802,8 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
 // one array per device, so calls that overlap on one device (different
 // streams) must be serialised by the caller.
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
-                                 float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st) {
+                                 float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
+                                 const float* const* X2, int accum) {
     if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || count < 1) return hipErrorNotSupported;
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;
@@ -806,24 +826,25 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
             if (n[i] <= t0 || out_dims[i] <= 0) continue;
             const int nt = n[i] - t0 < 16 ? n[i] - t0 : 16;
             const float* xs = X[i] + (size_t)t0 * in_dim;
+            const float* xs2 = X2 && X2[i] ? X2[i] + (size_t)t0 * in_dim : nullptr;
             for (int64_t r0 = 0; r0 < out_dims[i]; r0 += max_rows) {
                 // a new slot unless the previous entry's x is the same
-                const bool new_slot = !(cnt > 0 && xs == last_x && batch[cnt - 1].n == nt);
+                const bool new_slot = !(cnt > 0 && xs == last_x && batch[cnt - 1].x2 == xs2 && batch[cnt - 1].n == nt);
                 if (cnt == QG_MAXG || (new_slot && slots == max_slots)) {
-                    hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st);
+                    hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st, accum);
                     if (e != hipSuccess) return e;
                     cnt = 0;
                     slots = 0;
                 }
-                if (!(cnt > 0 && xs == last_x && batch[cnt - 1].n == nt)) slots++;
+                if (new_slot) slots++;
                 const int rows = (int)(out_dims[i] - r0 < max_rows ? out_dims[i] - r0 : max_rows);
-                batch[cnt++] = QgEntry{W[i] + (size_t)r0 * row_bytes, xs, Y[i] + (size_t)t0 * out_dims[i] + r0, nt,
-                                       rows, out_dims[i]};
+                batch[cnt++] = QgEntry{W[i] + (size_t)r0 * row_bytes, xs, xs2, Y[i] + (size_t)t0 * out_dims[i] + r0,
+                                       nt, rows, out_dims[i]};
                 last_x = xs;
             }
         }
         if (cnt) {
-            hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st);
+            hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st, accum);
             if (e != hipSuccess) return e;
         }
     }
@@ -833,5 +854,5 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                          hipStream_t st) {
     if (n < 2) return hipErrorNotSupported;
-    return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st);
+    return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st, nullptr, 0);
 }

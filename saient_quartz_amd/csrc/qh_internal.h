@@ -47,7 +47,8 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                          int n, hipStream_t st);
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
-                                 float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st);
+                                 float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
+                                 const float* const* X2 = nullptr, int accum = 0);
 hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
                                  const float* x, int in_dim, hipStream_t st, const float* norm_w, int accum,
                                  bool swiglu_pair = false);

@@ -18,7 +18,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import gemm_grouped_async, gemm_moe_async, gemv_group_async, gemv_multi_async
+from .host import gemm_grouped_async, gemm_grouped_ex_async, gemm_moe_async, gemv_group_async, gemv_multi_async
 
 Q4_K, Q6_K = 12, 14
 
@@ -294,9 +294,10 @@ class BatchStep:
     BatchConfig configs[3]): every sequence has its own token, hidden state and
     K/V cache, all at the same position.  The weight products are batched GEMMs
     (hip_gemm_grouped: one weight pass per 16 tokens on the matrix cores; q/k
-    share one launch, v another, since they differ in type); the glue is one
-    launch per layer step for all sequences (hip_rms_norm_rows,
-    hip_attention_step_batched, hip_swiglu and hip_vec_add over n rows).
+    share one launch, v another, since they differ in type); the residual adds
+    and the SwiGLU before the down projection are fused into the GEMMs
+    (hip_gemm_grouped_ex); the norms and the attention are one launch each for
+    all sequences (hip_rms_norm_rows, hip_attention_step_batched).
     Weights: the dict ForwardStep takes."""
 
     def __init__(self, cfg: ModelConfig, weights: dict, n: int):
@@ -315,6 +316,16 @@ class BatchStep:
         self.kc = [torch.zeros(n * self.cache_stride, **f32) for _ in range(c.layers)]
         self.vc = [torch.zeros(n * self.cache_stride, **f32) for _ in range(c.layers)]
         self.scale = 1.0 / math.sqrt(c.head_dim)
+        big = max(c.hidden, c.ffn, qd)
+        self.scratch = torch.zeros(2 * n * big, **f32)  # fallback of hip_gemm_grouped_ex
+
+    def _gemm_res(self, name, layer, x, in_dim, sp, up=None):
+        """hidden += W x (or W (silu(x) * up)) in one hip_gemm_grouped_ex call."""
+        c = self.cfg
+        gemm_grouped_ex_async(self.L, c.type_of(name), [self.w[name][layer].data_ptr()], [x.data_ptr()],
+                              [self.hidden.data_ptr()], [self.n], [c.hidden], in_dim, sp,
+                              up_ptrs=[up.data_ptr()] if up is not None else None, accumulate=True,
+                              scratch_ptr=self.scratch.data_ptr())
 
     def _gemm(self, names, layer, x, ys, in_dim, sp):
         """Batched GEMMs of the matrices `names` sharing x, one call per weight type."""
@@ -345,17 +356,11 @@ class BatchStep:
                 self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
                 self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta,
                 1.0, 0, c.neox, self.scale, sp))
-            self._gemm(("o",), l, self.att, (self.tmp,), c.n_heads * c.head_dim, sp)
-            check("hip_vec_add_async", L.hip_vec_add_async(self.hidden.data_ptr(), self.tmp.data_ptr(),
-                                                           n * c.hidden, sp))
+            self._gemm_res("o", l, self.att, c.n_heads * c.head_dim, sp)
             check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
                 self.xn.data_ptr(), self.hidden.data_ptr(), self.w["ffn_norm"][l].data_ptr(), n, c.hidden, sp))
             self._gemm(("gate", "up"), l, self.xn, (self.gate, self.up), c.hidden, sp)
-            check("hip_swiglu_async", L.hip_swiglu_async(self.act.data_ptr(), self.gate.data_ptr(),
-                                                         self.up.data_ptr(), n * c.ffn, sp))
-            self._gemm(("down",), l, self.act, (self.tmp,), c.ffn, sp)
-            check("hip_vec_add_async", L.hip_vec_add_async(self.hidden.data_ptr(), self.tmp.data_ptr(),
-                                                           n * c.hidden, sp))
+            self._gemm_res("down", l, self.gate, c.ffn, sp, up=self.up)
         if logits:
             check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
                 self.xn.data_ptr(), self.hidden.data_ptr(), self.w["out_norm"].data_ptr(), n, c.hidden, sp))

@@ -151,6 +151,19 @@ def gemm_grouped_async(L, ggml_type, w_ptrs, x_ptrs, y_ptrs, ns, out_dims, in_di
                                    in_dim, stream_ptr))
 
 
+def gemm_grouped_ex_async(L, ggml_type, w_ptrs, x_ptrs, y_ptrs, ns, out_dims, in_dim, stream_ptr, up_ptrs=None,
+                          accumulate=False, scratch_ptr=None):
+    """hip_gemm_grouped_ex_async: batched GEMMs with SwiGLU of (x, up) as input
+    and/or the residual add fused in."""
+    import ctypes as C
+    k = len(w_ptrs)
+    check("hip_gemm_grouped_ex_async",
+          L.hip_gemm_grouped_ex_async(ggml_type, k, (C.c_void_p * k)(*w_ptrs), (C.c_void_p * k)(*x_ptrs),
+                                      (C.c_void_p * k)(*up_ptrs) if up_ptrs else None, (C.c_void_p * k)(*y_ptrs),
+                                      (C.c_int * k)(*ns), (C.c_int * k)(*out_dims), in_dim, 1 if accumulate else 0,
+                                      scratch_ptr, stream_ptr))
+
+
 def gemm_moe_async(L, ggml_type, experts_ptr, expert_ids, tok_off, x_ptr, y_ptr, in_dim, out_dim, stream_ptr):
     """hip_gemm_moe_async: expert_ids[i] takes gathered tokens tok_off[i] .. tok_off[i+1]-1."""
     import ctypes as C
