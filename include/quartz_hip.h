@@ -119,6 +119,21 @@ int hip_gemm_grouped_ex_async(uint32_t ggml_type, int count, const uint8_t* cons
                               const float* const* x_up, float* const* y, const int* n, const int* out_dims,
                               int in_dim, int accumulate, float* scratch, void* stream);
 
+/* Y[t][j] for t < rows with ggml-cuda's int8 MMQ rounding (Q4_K, Q6_K): the
+ * GPU twin of the reference's CPU oracles gemm_q4k_q8_1_mmq / gemm_q6k_q8_1_mmq
+ * and their _stream_k forms (src/dequant.rs:202-645), bit-exact to them: x is
+ * quantised to Q8_1 per 32 values (f16 scale and sum for Q4_K, f32 scale for
+ * Q6_K), weight scale pairs are rounded to f16, dots are integer, and the f32
+ * accumulation runs in block order with fused multiply-adds.  reference_rows > 0
+ * and multiprocessors > 0 reproduce ggml-cuda's stream-K split for a launch of
+ * reference_rows rows on that many multiprocessors (cuda_stream_k_cut).  Token-
+ * major X [rows][in_dim] (16-byte aligned), Y [rows][out_dim]; in_dim % 256 == 0.
+ * A compatibility mode for ggml-identical results; hip_gemm is the fast path. */
+int hip_gemm_q8_1_mmq(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
+                      int out_dim, int rows, int reference_rows, int multiprocessors);
+int hip_gemm_q8_1_mmq_async(uint32_t ggml_type, const uint8_t* d_data, const float* d_x, float* d_y, int in_dim,
+                            int out_dim, int rows, int reference_rows, int multiprocessors, void* stream);
+
 /* Mixture-of-experts layer GEMMs over gathered tokens: for i < n_sel, expert
  * e = expert_ids[i] (its weights at d_experts + e * hip_type_size(type,
  * in_dim*out_dim), the expert slicing of src/cuda.rs:250-258 / :723-725)

@@ -645,3 +645,191 @@ const char* o_grid_sha256(int which) {
         default: return "";
     }
 }
+
+/* ------------------------------------------------ Q8_1 MMQ arithmetic mode -- */
+/* The reference's CPU oracles of ggml-cuda's int8 MMQ path (src/dequant.rs:
+ * 202-645): activations quantised to Q8_1 per 32 values, f16-rounded scales,
+ * integer dots, f32 accumulation with explicit mul_add (fmaf here) in block /
+ * group order, optional stream-K split of the accumulation. */
+
+/* f32_to_f16_round_to_even (src/dequant.rs:604-645), restated. */
+uint16_t o_f32_to_f16_rne(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const int exponent = (int)((bits >> 23) & 0xffu);
+    const uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent == 0xff) return (uint16_t)(sign | (mantissa == 0 ? 0x7c00u : 0x7e00u));
+    const int half_exponent = exponent - 127 + 15;
+    if (half_exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (half_exponent <= 0) {
+        if (half_exponent < -10) return sign;
+        const uint32_t significand = mantissa | 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - half_exponent);
+        uint32_t rounded = significand >> shift;
+        const uint32_t remainder = significand & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1u);
+        if (remainder > halfway || (remainder == halfway && (rounded & 1u))) rounded++;
+        return (uint16_t)(sign | rounded);
+    }
+    uint32_t rounded = mantissa >> 13;
+    const uint32_t remainder = mantissa & 0x1fffu;
+    if (remainder > 0x1000u || (remainder == 0x1000u && (rounded & 1u))) rounded++;
+    if (rounded == 0x400u) {
+        const int e = half_exponent + 1;
+        return (uint16_t)(sign | (e >= 31 ? 0x7c00u : (uint32_t)e << 10));
+    }
+    return (uint16_t)(sign | ((uint32_t)half_exponent << 10) | rounded);
+}
+
+static inline float round_to_f16(float v) { return o_f16_to_f32(o_f32_to_f16_rne(v)); } /* :600-602 */
+
+/* quantize_q8_1_mmq (src/dequant.rs:515-556) and _d4 (:558-598): per 32 values,
+ * partial max / sum over 8 lanes of 4, combined in XOR order 4, 2, 1; q =
+ * round(x * 127/max) (half away from zero); scale 1/(127/max), rounded to f16
+ * unless d4; sum f16-rounded (d4: 0). */
+void o_quantize_q8_1_mmq(const float* x, int in_dim, int rows, int d4, int8_t* values, float* scale, float* sum) {
+    const int nb = in_dim / 32;
+    for (int row = 0; row < rows; row++)
+        for (int b = 0; b < nb; b++) {
+            const float* grp = x + (size_t)row * in_dim + 32 * b;
+            float pm[8], ps[8];
+            for (int lane = 0; lane < 8; lane++) {
+                const float* v = grp + 4 * lane;
+                float m = 0.0f;
+                for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(v[i]));
+                pm[lane] = m;
+                ps[lane] = ((v[0] + v[1]) + v[2]) + v[3];
+            }
+            static const int offs[3] = {4, 2, 1};
+            for (int o = 0; o < 3; o++) {
+                float om[8], os[8];
+                memcpy(om, pm, sizeof om);
+                memcpy(os, ps, sizeof os);
+                for (int lane = 0; lane < 8; lane++) {
+                    pm[lane] = fmaxf(om[lane], om[lane ^ offs[o]]);
+                    ps[lane] = os[lane] + os[lane ^ offs[o]];
+                }
+            }
+            const float maximum = pm[0];
+            const float inv = maximum == 0.0f ? 0.0f : 127.0f / maximum;
+            int8_t* q = values + ((size_t)row * nb + b) * 32;
+            for (int i = 0; i < 32; i++) {
+                if (inv != 0.0f) {
+                    float r = roundf(grp[i] * inv);
+                    r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);  /* `as i8` saturates */
+                    q[i] = (int8_t)r;
+                } else {
+                    q[i] = 0;
+                }
+            }
+            const float sc = inv == 0.0f ? 0.0f : 1.0f / inv;
+            scale[(size_t)row * nb + b] = d4 ? sc : round_to_f16(sc);
+            sum[(size_t)row * nb + b] = d4 ? 0.0f : round_to_f16(ps[0]);
+        }
+}
+
+/* cuda_stream_k_cut (src/dequant.rs:338-374): the superblock at which ggml-cuda's
+ * stream-K partition splits output (row, column)'s accumulation, or -1. */
+int o_stream_k_cut(int row, int column, int in_dim, int out_dim, int reference_rows, int multiprocessors) {
+    const long MMQ_X = 128, MMQ_Y = 128, VPK = 256;
+    if (multiprocessors == 0 || in_dim % VPK != 0) return -1;
+    const long blocks_per_tile = in_dim / VPK;
+    const long tiles_x = (reference_rows + MMQ_X - 1) / MMQ_X;
+    const long tiles_y = (out_dim + MMQ_Y - 1) / MMQ_Y;
+    const long tile_count = tiles_x * tiles_y;
+    const long waves = (tile_count + multiprocessors - 1) / multiprocessors;
+    const long efficiency = 100 * tile_count / (multiprocessors * waves);
+    const long grid = efficiency >= 90 ? tile_count : multiprocessors;
+    if (grid == 0 || tile_count % grid == 0) return -1;
+    const long tile = (column / MMQ_Y) * tiles_x + row / MMQ_X;
+    const long tile_start = tile * blocks_per_tile, tile_end = tile_start + blocks_per_tile;
+    const long total = tile_count * blocks_per_tile;
+    for (long block = 1; block < grid; block++) {
+        const long boundary = block * total / grid;
+        if (boundary > tile_start && boundary < tile_end) return (int)(boundary - tile_start);
+    }
+    return -1;
+}
+
+/* gemm_q4k_q8_1_mmq[_stream_k] (src/dequant.rs:216-336) and
+ * gemm_q6k_q8_1_mmq[_stream_k] (:377-513).  x [rows][in_dim], y [rows][out_dim];
+ * reference_rows = 0: no stream-K split. */
+int o_gemm_q8_1_mmq(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, int out_dim, int rows,
+                    int reference_rows, int multiprocessors, float* y) {
+    if ((ggml_type != 12 && ggml_type != 14) || in_dim % 256 || rows < 0 || out_dim < 0) return -1;
+    const int q6 = ggml_type == 14;
+    const int nb8 = in_dim / 32, nsb = in_dim / 256;
+    const size_t bb = q6 ? 210 : 144;
+    int8_t* qv = malloc((size_t)rows * in_dim + 1);
+    float* qs = malloc(((size_t)rows * nb8 + 1) * sizeof(float));
+    float* qm = malloc(((size_t)rows * nb8 + 1) * sizeof(float));
+    if (!qv || !qs || !qm) { free(qv); free(qs); free(qm); return -2; }
+    o_quantize_q8_1_mmq(x, in_dim, rows, q6, qv, qs, qm);
+#pragma omp parallel for schedule(static)
+    for (int column = 0; column < out_dim; column++) {
+        const uint8_t* wrow = data + (size_t)column * nsb * bb;
+        for (int row = 0; row < rows; row++) {
+            float acc = 0.0f, prefix = 0.0f;
+            const int cut = reference_rows > 0
+                                ? o_stream_k_cut(row, column, in_dim, out_dim, reference_rows, multiprocessors)
+                                : -1;
+            for (int b = 0; b < nsb; b++) {
+                if (b == cut) { prefix = acc; acc = 0.0f; }
+                const uint8_t* blk = wrow + (size_t)b * bb;
+                const size_t a0 = (size_t)row * nb8 + (size_t)b * 8;
+                if (!q6) {
+                    const float d = o_f16_to_f32(rd16(blk)), dmin = o_f16_to_f32(rd16(blk + 2));
+                    for (int g = 0; g < 8; g++) {
+                        uint8_t sc, m;
+                        o_get_scale_min_k4(g, blk + 4, &sc, &m);
+                        const float cs = round_to_f16(d * (float)sc);
+                        const float cm = round_to_f16(-dmin * (float)m);
+                        const int8_t* av = qv + (a0 + g) * 32;
+                        const uint8_t* qq = blk + 16 + (g / 2) * 32;
+                        int dot = 0;
+                        for (int i = 0; i < 32; i++) {
+                            const int w = (g & 1) ? (qq[i] >> 4) : (qq[i] & 0x0f);
+                            dot += w * av[i];
+                        }
+                        const float ds = cs * qs[a0 + g];
+                        acc = fmaf(ds, (float)dot, acc);
+                        acc = fmaf(cm, qm[a0 + g], acc);
+                    }
+                } else {
+                    int8_t q[256];
+                    for (int half = 0; half < 2; half++)
+                        for (int i = 0; i < 32; i++) {
+                            const uint8_t l0 = blk[64 * half + i], l1 = blk[64 * half + i + 32];
+                            const uint8_t h = blk[128 + 32 * half + i];
+                            q[128 * half + i] = (int8_t)(((l0 & 0x0f) | ((h & 0x03) << 4)) - 32);
+                            q[128 * half + i + 32] = (int8_t)(((l1 & 0x0f) | (((h >> 2) & 0x03) << 4)) - 32);
+                            q[128 * half + i + 64] = (int8_t)(((l0 >> 4) | (((h >> 4) & 0x03) << 4)) - 32);
+                            q[128 * half + i + 96] = (int8_t)(((l1 >> 4) | (((h >> 6) & 0x03) << 4)) - 32);
+                        }
+                    const float d6 = o_f16_to_f32(rd16(blk + 208));
+                    for (int f = 0; f < 2; f++) {
+                        float fs = 0.0f;
+                        for (int g = 4 * f; g < 4 * f + 4; g++) {
+                            const int8_t* av = qv + (a0 + g) * 32;
+                            int d1 = 0, d2 = 0;
+                            for (int i = 0; i < 16; i++) {
+                                d1 += q[32 * g + i] * av[i];
+                                d2 += q[32 * g + i + 16] * av[i + 16];
+                            }
+                            const int s1 = (int8_t)blk[192 + 2 * g], s2 = (int8_t)blk[192 + 2 * g + 1];
+                            fs = fmaf(qs[a0 + g], (float)(s1 * d1 + s2 * d2), fs);
+                        }
+                        acc = fmaf(d6, fs, acc);
+                    }
+                }
+            }
+            if (cut >= 0) acc = acc + prefix;  /* tail + prefix, ggml's fixup order */
+            y[(size_t)row * out_dim + column] = acc;
+        }
+    }
+    free(qv);
+    free(qs);
+    free(qm);
+    return 0;
+}

@@ -18,6 +18,12 @@ int o_gemm(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, 
 void o_set_threads(int n);
 int o_get_threads(void);
 const char* o_grid_sha256(int which);
+/* Q8_1 MMQ arithmetic mode (src/dequant.rs:202-645) */
+uint16_t o_f32_to_f16_rne(float value);
+void o_quantize_q8_1_mmq(const float* x, int in_dim, int rows, int d4, int8_t* values, float* scale, float* sum);
+int o_stream_k_cut(int row, int column, int in_dim, int out_dim, int reference_rows, int multiprocessors);
+int o_gemm_q8_1_mmq(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, int out_dim, int rows,
+                    int reference_rows, int multiprocessors, float* y);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,9 @@ _SIGS = {
     "hip_gemm_grouped_async": (C.c_int, [C.c_uint32, C.c_int] + [C.c_void_p] * 5 + [C.c_int, C.c_void_p]),
     "hip_gemm_grouped_ex_async": (C.c_int, [C.c_uint32, C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_void_p,
                                                                                      C.c_void_p]),
+    "hip_gemm_q8_1_mmq": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p] + [C.c_int] * 5),
+    "hip_gemm_q8_1_mmq_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p] + [C.c_int] * 5 +
+                                [C.c_void_p]),
     "hip_gemm_moe": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int]),
     "hip_gemm_moe_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int,
                                                                                           C.c_void_p]),

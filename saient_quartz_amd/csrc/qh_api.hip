@@ -366,6 +366,24 @@ int hip_gemm_grouped_ex_async(uint32_t type, int count, const uint8_t* const* W,
     return QH_OK;
 }
 
+int hip_gemm_q8_1_mmq_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
+                            int rows, int reference_rows, int multiprocessors, void* stream) {
+    if (type != QT_Q4_K && type != QT_Q6_K) return QH_ERR_TYPE;
+    if (in_dim <= 0 || in_dim % 256 || out_dim < 0 || rows < 0 || reference_rows < 0 || multiprocessors < 0)
+        return QH_ERR_DIMS;
+    if (rows == 0 || out_dim == 0) return QH_OK;
+    if (!W || !x || !y) return QH_ERR_NULL;
+    if ((uintptr_t)x & 15u) return QH_ERR_RANGE;
+    QH_CHECK(qh_launch_mmq_q81(type, W, x, y, in_dim, out_dim, rows, reference_rows, multiprocessors,
+                               (hipStream_t)stream),
+             "hip_gemm_q8_1_mmq");
+    return QH_OK;
+}
+int hip_gemm_q8_1_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int rows,
+                      int reference_rows, int multiprocessors) {
+    return hip_gemm_q8_1_mmq_async(type, W, x, y, in_dim, out_dim, rows, reference_rows, multiprocessors, nullptr);
+}
+
 int hip_gemm_moe_async(uint32_t type, const uint8_t* experts, int n_sel, const int* expert_ids, const int* tok_off,
                        const float* x, float* y, int in_dim, int out_dim, void* stream) {
     if (n_sel < 0) return QH_ERR_RANGE;

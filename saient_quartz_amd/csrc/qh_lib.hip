@@ -6,6 +6,7 @@
 #include "qh_mmv.hip"
 #include "qh_mmv16.hip"
 #include "qh_gemm.hip"
+#include "qh_mmq81.hip"
 #include "qh_gemv.hip"
 #include "qh_glue.hip"
 #include "qh_api.hip"

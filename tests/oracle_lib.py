@@ -38,6 +38,13 @@ class Oracle:
         L.o_get_threads.restype = C.c_int
         L.o_grid_sha256.restype = C.c_char_p
         L.o_grid_sha256.argtypes = [C.c_int]
+        L.o_f32_to_f16_rne.restype = C.c_uint16
+        L.o_f32_to_f16_rne.argtypes = [C.c_float]
+        L.o_quantize_q8_1_mmq.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.o_stream_k_cut.restype = C.c_int
+        L.o_stream_k_cut.argtypes = [C.c_int] * 6
+        L.o_gemm_q8_1_mmq.restype = C.c_int
+        L.o_gemm_q8_1_mmq.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p] + [C.c_int] * 5 + [C.c_void_p]
 
     def f16(self, bits: int) -> float:
         return self.L.o_f16_to_f32(bits)
@@ -69,6 +76,31 @@ class Oracle:
         rc = self.L.o_gemm(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, n, y.ctypes.data)
         if rc:
             raise ValueError(f"o_gemm rc={rc}")
+        return y
+
+    def f32_to_f16_rne(self, v: float) -> int:
+        return self.L.o_f32_to_f16_rne(v)
+
+    def quantize_q8_1(self, x: np.ndarray, in_dim: int, rows: int, d4: bool):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        q = np.empty(rows * in_dim, dtype=np.int8)
+        sc = np.empty(rows * in_dim // 32, dtype=np.float32)
+        sm = np.empty(rows * in_dim // 32, dtype=np.float32)
+        self.L.o_quantize_q8_1_mmq(x.ctypes.data, in_dim, rows, 1 if d4 else 0, q.ctypes.data, sc.ctypes.data,
+                                   sm.ctypes.data)
+        return q.reshape(rows, in_dim), sc.reshape(rows, -1), sm.reshape(rows, -1)
+
+    def stream_k_cut(self, row, column, in_dim, out_dim, reference_rows, mps) -> int:
+        return self.L.o_stream_k_cut(row, column, in_dim, out_dim, reference_rows, mps)
+
+    def gemm_q8_1_mmq(self, t, x, data, in_dim, out_dim, rows, reference_rows=0, mps=0) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        y = np.empty((rows, out_dim), dtype=np.float32)
+        rc = self.L.o_gemm_q8_1_mmq(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, rows, reference_rows, mps,
+                                    y.ctypes.data)
+        if rc:
+            raise ValueError(f"o_gemm_q8_1_mmq rc={rc}")
         return y
 
     def set_threads(self, n):
