@@ -286,9 +286,42 @@ def moe_leg(torch, reps):
                      "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
                      "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
                      "tokens_per_s": round(64 / (ms * 1e-3), 1)}
+        if grouped:
+            out[name + "_routed"] = routed_moe(torch, layer, t, reps)
         del g, layer
         torch.cuda.empty_cache()
     return out
+
+
+def routed_moe(torch, layer, t, reps):
+    """The whole MoE FFN for 64 tokens with top-2 routing on the device
+    (MoeStep: F32 router GEMM, hip_moe_route / plan, one 36-byte tok_off copy to
+    the host, gather, expert GEMMs, SwiGLU, hip_gemm_moe, weighted combine), on
+    the same expert weights.  Not graph-captured (the host reads tok_off), so
+    the time includes that round trip; events around `reps` layer calls."""
+    from saient_quartz_amd.decode import MoeStep
+
+    E, k, n, d, f = layer.E, 2, 64, layer.h, layer.f
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20261207)
+    rw = torch.randn(E, d, device="cuda", generator=gen) / d ** 0.5
+    x = torch.randn(n, d, device="cuda", generator=gen)
+    y = torch.empty(n, d, device="cuda")
+    step = MoeStep((t, t, t), layer.wg, layer.wu, layer.wd, rw, E, k, d, f, n_max=n)
+    step.issue(x, y, n)
+    torch.cuda.synchronize()
+    counts = [b - a for a, b in zip(step.tok_off_host.tolist()[:-1], step.tok_off_host.tolist()[1:])]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        step.issue(x, y, n)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    wbytes = sum(3 * layer.slice for c in counts if c)
+    return {"ms_per_layer": round(ms, 4), "tokens_per_s": round(n / (ms * 1e-3), 1), "tokens_per_expert": counts,
+            "weight_bytes_touched": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1)}
 
 
 def measured_traffic(path):

@@ -240,6 +240,40 @@ int hip_swiglu(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* stream);
 int hip_swiglu_oai(float* out, const float* gate, const float* up, int n);
 int hip_swiglu_oai_async(float* out, const float* gate, const float* up, int n, void* stream);
+
+/* Mixture-of-experts routing and gather/scatter on the device, for a batch of
+ * n_tok tokens (all arrays device memory, token-major).  The reference routes
+ * on the host after copying the router logits back (src/cuda.rs:670-700,
+ * src/main.rs:964-993) and scale-adds each chosen expert's output
+ * (src/cuda.rs:703-798, src/main.rs:995-1040).  The layer is:
+ *   hip_gemm(F32 router) -> hip_moe_route -> hip_moe_plan -> hip_moe_gather ->
+ *   gate/up GEMMs per expert over its slot range -> hip_moe_swiglu ->
+ *   hip_gemm_moe (down) -> hip_moe_combine.
+ * route: logits[n_tok][n_exp] (+ router_bias[n_exp] if non-null) -> the top k
+ *   experts per token in total_cmp descending order (equal keys: lower index
+ *   first) in ids[n_tok][k], and weights[n_tok][k]: softmax over the chosen k
+ *   (renorm != 0: Mixtral, Qwen-MoE, gpt-oss) or the chosen entries of a softmax
+ *   over all n_exp logits (renorm == 0: OLMoE).  n_exp <= 256, k <= 16.
+ * plan: ids -> tok_off[n_exp + 1] (expert e's slots are tok_off[e] ..
+ *   tok_off[e+1]-1, in token then choice order), slot_of[n_tok][k] (the slot of
+ *   each choice; -1 for an id outside [0, n_exp)), slot_tok[] and slot_exp[]
+ *   (token and expert of each slot).  Copy tok_off to the host to size the
+ *   expert GEMMs (the reference copies the logits at the same point).
+ * gather: xg[q] = x[slot_tok[q]] for q < n_slots, rows of dim floats.
+ * swiglu: act[q] = swiglu(gate[q] + gate_bias[e], up[q] + up_bias[e]),
+ *   e = slot_exp[q]; biases may be null; oai != 0 is the clamped gpt-oss form.
+ * combine: out[t] = (accumulate ? out[t] : 0) + sum over j = 0..k-1, in order,
+ *   of weights[t][j] * (y_slots[slot_of[t][j]] + down_bias[ids[t][j]]), each
+ *   product and sum rounded separately as the reference's `*a += rw * b`. */
+int hip_moe_route_async(const float* logits, const float* router_bias, int n_tok, int n_exp, int k, int renorm,
+                        int* ids, float* weights, void* stream);
+int hip_moe_plan_async(const int* ids, int n_tok, int k, int n_exp, int* tok_off, int* slot_of, int* slot_tok,
+                       int* slot_exp, void* stream);
+int hip_moe_gather_async(float* xg, const float* x, const int* slot_tok, int n_slots, int dim, void* stream);
+int hip_moe_swiglu_async(float* act, const float* gate, const float* up, const float* gate_bias, const float* up_bias,
+                         const int* slot_exp, int n_slots, int ffn_dim, int oai, void* stream);
+int hip_moe_combine_async(float* out, const float* y_slots, const int* slot_of, const float* weights, const int* ids,
+                          const float* down_bias, int n_tok, int k, int dim, int accumulate, void* stream);
 /* hip_gemv_fused over count (1..8) matrices of any types sharing x (per-matrix
  * types[k]): the projections of one input, e.g. a Q4_K_M layer's q and k
  * (Q4_K) with v (Q6_K).  Two matrix-core types (Q4_K, Q5_K, Q6_K; <= 4

@@ -15,14 +15,27 @@ the step built on it; only tests/ import it.
   forward_step    src/cuda.rs:556-837 (dense FFN, no biases / QK-norm / sliding
                                        window): the sequence of the above around
                                        the seven GEMVs and the head.
+  moe_route       src/main.rs:964-993 (= src/cuda.rs:684-701): router logits
+                                       (+ bias), sort by total_cmp descending,
+                                       top k, softmax over the k (renorm) or over
+                                       all experts (OLMoE); weights in f32 as
+                                       the reference computes them.
+  moe_ffn         src/main.rs:995-1040: per chosen expert gate/up (+ biases),
+                                       SwiGLU (plain or OAI), down (+ bias),
+                                       output += w * down, in float64.
 
 Pinned by tests/test_glue_ref.py with closed forms: rope at pos 0 is the
 identity and preserves each pair's norm at any pos; rms_norm of a constant
 vector is sign(x) * w (up to the eps term); softmax rows sum to 1 without a sink
 and to 1 - p_sink with one; attention over one cached token returns that
 token's value; swiglu(0, .) = 0 and swiglu(g, 1) = silu(g); the OAI form
-clamps at 7.
+clamps at 7; moe_route's order against numpy's stable argsort on distinct
+values, -0 < +0 and NaN placement by sign, k = n_exp weights summing to 1, and
+the OLMoE weights against a float64 softmax; moe_ffn with one expert of weight
+1 against the dense FFN.
 """
+import struct
+
 import numpy as np
 
 
@@ -112,3 +125,56 @@ def forward_step(hidden, pos, layers, head_w, out_norm, kv, cfg):
         xn = rms_norm(x, L["ffn_norm"])
         x = x + L["down"] @ swiglu(L["gate"] @ xn, L["up"] @ xn)
     return head_w @ rms_norm(x, out_norm), x
+
+
+def total_order_key(v):
+    """f32::total_cmp as an integer key (Rust's core::f32::total_cmp: flip the
+    magnitude bits of negative values, then compare as signed 32-bit)."""
+    b = struct.unpack("<i", struct.pack("<f", float(np.float32(v))))[0]
+    return b ^ ((b >> 31) & 0x7FFFFFFF)
+
+
+def moe_route(logits, k, renorm=True, bias=None):
+    """Top-k experts and weights of one token (src/main.rs:964-993), f32
+    arithmetic as the reference.  Ties keep the lower index first (the
+    reference's sort_unstable_by leaves them unspecified).  Returns (ids, w)."""
+    v = np.asarray(logits, np.float32).copy()
+    if bias is not None:
+        v = (v + np.asarray(bias, np.float32)).astype(np.float32)
+    order = sorted(range(len(v)), key=lambda i: (-total_order_key(v[i]), i))
+    top = order[:k]
+    tv = v[top]
+    with np.errstate(over="ignore", invalid="ignore"):
+        if renorm:
+            mx = np.float32(-np.inf)
+            for t in tv:
+                mx = t if np.isnan(mx) else (mx if np.isnan(t) else max(mx, t))
+            e = np.exp((tv - mx).astype(np.float32)).astype(np.float32)
+            s = np.float32(0)
+            for x in e:
+                s = np.float32(s + x)
+        else:
+            mx = np.float32(-np.inf)
+            for t in v:
+                mx = t if np.isnan(mx) else (mx if np.isnan(t) else max(mx, t))
+            s = np.float32(0)
+            for x in v:
+                s = np.float32(s + np.float32(np.exp(np.float32(x - mx))))
+            e = np.exp((tv - mx).astype(np.float32)).astype(np.float32)
+        w = (e / s).astype(np.float32)
+    return np.array(top, np.int64), w
+
+
+def moe_ffn(x, ids, w, gate, up, down, gate_b=None, up_b=None, down_b=None, oai=False):
+    """One token's MoE output in float64 (src/main.rs:995-1040): gate/up/down are
+    per-expert dequantized f64 matrices ([E] lists of [f, d] / [d, f]); biases
+    [E][f] / [E][d] or None."""
+    x = np.asarray(x, np.float64)
+    out = np.zeros(down[0].shape[0])
+    for e, rw in zip(ids, w):
+        g = gate[e] @ x + (gate_b[e] if gate_b is not None else 0.0)
+        u = up[e] @ x + (up_b[e] if up_b is not None else 0.0)
+        h = swiglu_oai(g, u) if oai else swiglu(g, u)
+        o = down[e] @ h + (down_b[e] if down_b is not None else 0.0)
+        out += float(rw) * o
+    return out

@@ -603,6 +603,42 @@ int hip_attention_step_async(float* out, const float* q, const float* k, const f
                                             head_dim, kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, s);
 }
 
+int hip_moe_route_async(const float* logits, const float* router_bias, int n_tok, int n_exp, int k, int renorm,
+                        int* ids, float* weights, void* s) {
+    if (n_tok < 0 || n_exp < 1 || n_exp > 256 || k < 1 || k > 16 || k > n_exp) return QH_ERR_DIMS;
+    if (n_tok > 0 && (!logits || !ids || !weights)) return QH_ERR_NULL;
+    QH_GLUE(qh_moe_route(logits, router_bias, n_tok, n_exp, k, renorm, ids, weights, (hipStream_t)s),
+            "hip_moe_route");
+}
+int hip_moe_plan_async(const int* ids, int n_tok, int k, int n_exp, int* tok_off, int* slot_of, int* slot_tok,
+                       int* slot_exp, void* s) {
+    if (n_tok < 0 || n_exp < 1 || n_exp > 256 || k < 1 || k > 16 || (int64_t)n_tok * k > (1 << 24))
+        return QH_ERR_DIMS;
+    if (!tok_off || (n_tok > 0 && (!ids || !slot_of || !slot_tok || !slot_exp))) return QH_ERR_NULL;
+    QH_GLUE(qh_moe_plan(ids, n_tok, k, n_exp, tok_off, slot_of, slot_tok, slot_exp, (hipStream_t)s),
+            "hip_moe_plan");
+}
+int hip_moe_gather_async(float* xg, const float* x, const int* slot_tok, int n_slots, int dim, void* s) {
+    if (n_slots < 0 || dim < 0) return QH_ERR_DIMS;
+    if (n_slots > 0 && dim > 0 && (!xg || !x || !slot_tok)) return QH_ERR_NULL;
+    QH_GLUE(qh_moe_gather(xg, x, slot_tok, n_slots, dim, (hipStream_t)s), "hip_moe_gather");
+}
+int hip_moe_swiglu_async(float* act, const float* gate, const float* up, const float* gate_bias, const float* up_bias,
+                         const int* slot_exp, int n_slots, int ffn_dim, int oai, void* s) {
+    if (n_slots < 0 || ffn_dim < 0) return QH_ERR_DIMS;
+    if (n_slots > 0 && ffn_dim > 0 && (!act || !gate || !up || ((gate_bias || up_bias) && !slot_exp)))
+        return QH_ERR_NULL;
+    QH_GLUE(qh_moe_swiglu(act, gate, up, gate_bias, up_bias, slot_exp, n_slots, ffn_dim, oai, (hipStream_t)s),
+            "hip_moe_swiglu");
+}
+int hip_moe_combine_async(float* out, const float* y_slots, const int* slot_of, const float* weights, const int* ids,
+                          const float* down_bias, int n_tok, int k, int dim, int accumulate, void* s) {
+    if (n_tok < 0 || k < 1 || dim < 0) return QH_ERR_DIMS;
+    if (n_tok > 0 && dim > 0 && (!out || !y_slots || !slot_of || !weights || (down_bias && !ids))) return QH_ERR_NULL;
+    QH_GLUE(qh_moe_combine(out, y_slots, slot_of, weights, ids, down_bias, n_tok, k, dim, accumulate, (hipStream_t)s),
+            "hip_moe_combine");
+}
+
 int hip_swiglu_async(float* out, const float* gate, const float* up, int n, void* s) {
     if (n > 0 && (!out || !gate || !up)) return QH_ERR_NULL;
     QH_GLUE(qh_glue_swiglu(0, out, gate, up, n, (hipStream_t)s), "hip_swiglu");

@@ -134,6 +134,51 @@ QH_DEV uint32_t qh_signmask4(uint32_t s4) {
     return (s << 8) - s;  // s * 0xFF, bytes 0 or 0xFF
 }
 
+// IQ pieces for the int8 matrix-core kernels: 16 consecutive weights of one
+// row (half hh of 32-weight sub-block K) as signed codebook bytes b[0..3], and
+// the sub-block's integer scale sc, read from a superblock staged in LDS at r
+// with 16-byte slices at 16c and the last slice loaded from block byte LAST
+// (so block bytes past the previous slice sit 16 (CH-1) - LAST further on).
+// The B operand times sc times the format's float d is the dequantized value.
+//
+// IQ3_S (src/dequant.rs:1184-1237): d, qs[64], qh[8], signs[32], scales[4];
+// 8-weight group l of sub-block K takes grid indices qs[8K + 2l], qs[8K + 2l +
+// 1] with bits 2l, 2l+1 of qh[K] as bit 8 and signs[4K + l]; scale
+// 1 + 2 * nibble K % 2 of scales[K / 2].  Last slice from byte 94: byte o >= 96
+// at LDS o + 2.
+QH_DEV int qh_iq3s_at(int o) { return o >= 96 ? o + 2 : o; }
+QH_DEV uint32_t qh_rd16(const unsigned char* p, int o) { return *reinterpret_cast<const uint16_t*>(p + o); }
+QH_DEV void qh_iq3s_piece(const unsigned char* r, int K, int hh, const uint32_t* g32, uint32_t* b, int& sc) {
+    const int oq = 2 + 8 * K + 4 * hh;  // the 4 index bytes of groups 2hh, 2hh+1
+    const uint32_t q = qh_rd16(r, oq) | (qh_rd16(r, oq + 2) << 16);
+    const uint32_t qh = (uint32_t)r[66 + K] >> (4 * hh);
+    const uint32_t sg = qh_rd16(r, qh_iq3s_at(74 + 4 * K + 2 * hh));
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const uint32_t idx = ((q >> (8 * m)) & 0xFFu) | (((qh >> m) & 1u) << 8);
+        b[m] = qh_negbytes(g32[idx], qh_signmask4(sg >> (4 * m)));
+    }
+    sc = 1 + 2 * (int)((r[qh_iq3s_at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
+}
+
+// IQ2_XXS (src/dequant.rs:1011-1041): d, then per sub-block K 4 grid indices
+// (bytes 2 + 8K ..) and a u32 (bytes 6 + 8K ..) with four 7-bit sign fields
+// and the scale in bits 28-31: weight = d/8 (2 scale + 1) grid * sign.  Last
+// slice from byte 50: byte o >= 64 at LDS o + 14.
+QH_DEV int qh_iq2xxs_at(int o) { return o >= 64 ? o + 14 : o; }
+QH_DEV void qh_iq2xxs_piece(const unsigned char* r, int K, int hh, const uint64_t* g64, uint32_t* b, int& sc) {
+    const uint32_t a0 = qh_rd16(r, 2 + 8 * K + 2 * hh);  // indices of groups 2hh, 2hh+1
+    const uint32_t a1 = qh_rd16(r, qh_iq2xxs_at(6 + 8 * K)) | (qh_rd16(r, qh_iq2xxs_at(8 + 8 * K)) << 16);
+#pragma unroll
+    for (int l = 0; l < 2; l++) {
+        const uint64_t g = g64[(a0 >> (8 * l)) & 0xFFu];
+        const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * hh + l))) & 127u);
+        b[2 * l] = qh_negbytes((uint32_t)g, qh_signmask4(s8));
+        b[2 * l + 1] = qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
+    }
+    sc = 2 * (int)(a1 >> 28) + 1;
+}
+
 // ---------------------------------------------------------------- reductions
 
 // Full 64-lane sum; the result is valid in lane 63.

@@ -135,17 +135,11 @@ struct GQ6K {
 };
 
 
-// IQ3_S (src/dequant.rs:1184-1237), 110-byte blocks: d, qs[64], qh[8],
-// signs[32], scales[4].  Sub-block k (32 weights, scale d (1 + 2 nibble)):
-// 8-weight group l has grid indices qs[8k + 2l], qs[8k + 2l + 1] with bits 2l,
-// 2l+1 of qh[k] as bit 8, and sign byte signs[4k + l].  Weights are signed grid
-// bytes, so the B operand holds the dequantized value / (d scale) exactly.
-// The 7th 16-byte slice is loaded from block bytes 94-109: block byte b >= 96
-// sits at LDS b + 2.
+// IQ3_S and IQ2_XXS: the B operand of sub-block K, lane half hh, is the
+// qh_iq3s_piece / qh_iq2xxs_piece of the staged block (signed codebook bytes,
+// the dequantized value / (d scale) exactly), with the codebooks in LDS.
 extern __device__ uint32_t qh_g_iq3s[512];
 extern __device__ uint64_t qh_g_iq2xxs[256];
-
-QH_DEV uint32_t qh_rd16(const unsigned char* p, int o) { return *reinterpret_cast<const uint16_t*>(p + o); }
 
 struct GIQ3S {
     static constexpr int BYTES = 110, CH = 7, RS = 112, LAST = 94;
@@ -154,28 +148,15 @@ struct GIQ3S {
     static constexpr int KIND = 1, GRID = 1;  // one scale per 32 weights; IQ3S codebook in LDS
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{qh_h2f(qh_rd16(r, 0)), 0.f}; }
-    static QH_DEV int at(int o) { return o >= 96 ? o + 2 : o; }
     template <int K>
     static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
-        const int oq = 2 + 8 * K + 4 * hh;  // 4 index bytes of groups 2hh, 2hh+1
-        const uint32_t q = qh_rd16(r, oq) | (qh_rd16(r, oq + 2) << 16);
-        const uint32_t qh = (uint32_t)r[66 + K] >> (4 * hh);
-        const uint32_t sg = qh_rd16(r, at(74 + 4 * K + 2 * hh));
-        const uint32_t* g32 = reinterpret_cast<const uint32_t*>(grid);
+        uint32_t v[4];
+        qh_iq3s_piece(r, K, hh, reinterpret_cast<const uint32_t*>(grid), v, sc);
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const uint32_t idx = ((q >> (8 * m)) & 0xFFu) | (((qh >> m) & 1u) << 8);
-            b[m] = (int)qh_negbytes(g32[idx], qh_signmask4(sg >> (4 * m)));
-        }
-        sc = 1 + 2 * (int)((r[at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
+        for (int m = 0; m < 4; m++) b[m] = (int)v[m];
     }
 };
 
-// IQ2_XXS (src/dequant.rs:1011-1041), 66-byte blocks: d, then per sub-block k 4
-// grid indices (bytes 2+8k..) and a u32 (bytes 6+8k..) holding four 7-bit sign
-// fields and the scale in bits 28-31: weight = d/8 (2 scale + 1) grid * sign.
-// The 5th slice is loaded from block bytes 50-65: block byte b >= 64 sits at LDS
-// b + 14.
 struct GIQ2XXS {
     static constexpr int BYTES = 66, CH = 5, RS = 80, LAST = 50;
     static constexpr int SUMK = 32, SUMSH = 5;
@@ -183,20 +164,12 @@ struct GIQ2XXS {
     static constexpr int KIND = 1, GRID = 2;  // IQ2XXS codebook in LDS
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{0.125f * qh_h2f(qh_rd16(r, 0)), 0.f}; }
-    static QH_DEV int at(int o) { return o >= 64 ? o + 14 : o; }
     template <int K>
     static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
-        const uint32_t a0 = qh_rd16(r, 2 + 8 * K + 2 * hh);  // indices of groups 2hh, 2hh+1
-        const uint32_t a1 = qh_rd16(r, at(6 + 8 * K)) | (qh_rd16(r, at(8 + 8 * K)) << 16);
-        const uint64_t* g64 = reinterpret_cast<const uint64_t*>(grid);
+        uint32_t v[4];
+        qh_iq2xxs_piece(r, K, hh, reinterpret_cast<const uint64_t*>(grid), v, sc);
 #pragma unroll
-        for (int l = 0; l < 2; l++) {
-            const uint64_t g = g64[(a0 >> (8 * l)) & 0xFFu];
-            const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * hh + l))) & 127u);
-            b[2 * l] = (int)qh_negbytes((uint32_t)g, qh_signmask4(s8));
-            b[2 * l + 1] = (int)qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
-        }
-        sc = 2 * (int)(a1 >> 28) + 1;
+        for (int m = 0; m < 4; m++) b[m] = (int)v[m];
     }
 };
 
@@ -816,14 +789,15 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
     if (max_slots < 1) return hipErrorNotSupported;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
     if (max_rows < 32) return hipErrorNotSupported;
-    int nmax = 0;
-    for (int i = 0; i < count; i++) nmax = n[i] > nmax ? n[i] : nmax;
+    // Entries go matrix-major: a matrix's token chunks follow each other, so
+    // its weights are read from HBM once and from the MALL (256 MB) for the
+    // chunks after the first, instead of once per chunk pass over all matrices.
     QgEntry batch[QG_MAXG];
-    for (int t0 = 0; t0 < nmax; t0 += 16) {
-        int cnt = 0, slots = 0;
-        const float* last_x = nullptr;
-        for (int i = 0; i < count; i++) {
-            if (n[i] <= t0 || out_dims[i] <= 0) continue;
+    int cnt = 0, slots = 0;
+    const float* last_x = nullptr;
+    for (int i = 0; i < count; i++) {
+        if (out_dims[i] <= 0) continue;
+        for (int t0 = 0; t0 < n[i]; t0 += 16) {
             const int nt = n[i] - t0 < 16 ? n[i] - t0 : 16;
             const float* xs = X[i] + (size_t)t0 * in_dim;
             const float* xs2 = X2 && X2[i] ? X2[i] + (size_t)t0 * in_dim : nullptr;
@@ -843,10 +817,10 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
                 last_x = xs;
             }
         }
-        if (cnt) {
-            hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st, accum);
-            if (e != hipSuccess) return e;
-        }
+    }
+    if (cnt) {
+        hipError_t e = qg_run(type, batch, cnt, in_dim, row_bytes, *sc, st, accum);
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }

@@ -170,6 +170,8 @@ hipError_t qh_launch_gemv(uint32_t type, const uint8_t* W, const float* x, float
 hipError_t qh_launch_gemm(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                           int n, hipStream_t st) {
     if (n == 1) return qh_launch_gemv(type, W, x, y, in_dim, out_dim, st);
+    // f32 weights (routers): one launch for all tokens
+    if (type == QT_F32) return qh_launch_gemm_f32(reinterpret_cast<const float*>(W), x, y, in_dim, out_dim, n, st);
     if (!qh_force_valu()) {
         hipError_t e = qh_launch_mmq(type, W, x, y, in_dim, out_dim, n, st);
         if (e != hipErrorNotSupported) return e;

@@ -82,6 +82,17 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
                                   const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
                                   float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st, int n_seq = 1,
                                   size_t cache_stride = 0);
+hipError_t qh_launch_gemm_f32(const float* W, const float* x, float* y, int in_dim, int out_dim, int n,
+                              hipStream_t st);
+hipError_t qh_moe_route(const float* logits, const float* bias, int n_tok, int ne, int k, int renorm, int* ids,
+                        float* wts, hipStream_t st);
+hipError_t qh_moe_plan(const int* ids, int n_tok, int k, int ne, int* tok_off, int* slot_of, int* slot_tok,
+                       int* slot_exp, hipStream_t st);
+hipError_t qh_moe_gather(float* xg, const float* x, const int* slot_tok, int n_slots, int d, hipStream_t st);
+hipError_t qh_moe_swiglu(float* act, const float* g, const float* u, const float* gb, const float* ub,
+                         const int* slot_exp, int n_slots, int f, int oai, hipStream_t st);
+hipError_t qh_moe_combine(float* out, const float* yg, const int* slot_of, const float* wts, const int* ids,
+                          const float* db, int n_tok, int k, int d, int accumulate, hipStream_t st);
 hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* up, int n, hipStream_t st);
 hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st);  // hip_last_error() text
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

@@ -9,5 +9,6 @@
 #include "qh_mmq81.hip"
 #include "qh_gemv.hip"
 #include "qh_glue.hip"
+#include "qh_moe.hip"
 #include "qh_api.hip"
 #include "qh_gguf.hip"

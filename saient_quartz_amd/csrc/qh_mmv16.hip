@@ -56,7 +56,8 @@ QH_DEV uint32_t qh_hi4(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
 // positions 16(c%2) .. +15.
 struct M16Q4K {
     static constexpr int BYTES = 144, CH = 9, ROWS = 14, LAST = 128, RS = QH_RS;
-    static constexpr bool FLOAT_D = false;
+    static constexpr bool FLOAT_D = false, MINS = true;
+    static constexpr int GRID = 0;
     struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r, int) {
         const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
@@ -69,7 +70,7 @@ struct M16Q4K {
         o.dm = qh_f16_hi(h.x);
         return o;
     }
-    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char*) {
         const qh_u32x4 q0 = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * kg);
         const qh_u32x4 q1 = *reinterpret_cast<const qh_u32x4*>(r + 80 + 16 * kg);
 #pragma unroll
@@ -98,10 +99,11 @@ struct M16Q4K {
 // Chunks as Q4_K (qs at byte 48); both of lane kg's chunks use qh[16(kg%2) ..].
 struct M16Q5K {
     static constexpr int BYTES = 176, CH = 11, ROWS = 11, LAST = 160, RS = QH_RS;
-    static constexpr bool FLOAT_D = false;
+    static constexpr bool FLOAT_D = false, MINS = true;
+    static constexpr int GRID = 0;
     using H = M16Q4K::H;
     static QH_DEV H hdr(const unsigned char* r, int kg) { return M16Q4K::hdr(r, kg); }
-    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char*) {
         const qh_u32x4 q0 = *reinterpret_cast<const qh_u32x4*>(r + 48 + 16 * kg);
         const qh_u32x4 q1 = *reinterpret_cast<const qh_u32x4*>(r + 112 + 16 * kg);
         const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * (kg & 1));
@@ -134,7 +136,8 @@ struct M16Q6K {
     // The 14th slice is loaded from block bytes 194-209 (not 208-223), so no load
     // leaves the block: the LDS line then holds bytes 0-207 at 0-207 and d at 222.
     static constexpr int LAST = 194, RS = QH_RS;
-    static constexpr bool FLOAT_D = false;
+    static constexpr bool FLOAT_D = false, MINS = true;
+    static constexpr int GRID = 0;
     struct H { qh_u32x4 s; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r, int) {
         H o;
@@ -143,7 +146,7 @@ struct M16Q6K {
         o.dm = 32.0f * o.d;
         return o;
     }
-    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char*) {
         const qh_u32x4 l0 = *reinterpret_cast<const qh_u32x4*>(r + 16 * kg);
         const qh_u32x4 l1 = *reinterpret_cast<const qh_u32x4*>(r + 64 + 16 * kg);
         const qh_u32x4 u0 = *reinterpret_cast<const qh_u32x4*>(r + 128 + 16 * (kg & 1));
@@ -174,7 +177,8 @@ struct M16Q6K {
 // puts the 16 rows of a column 4 banks apart.
 struct M16Q80 {
     static constexpr int BYTES = 272, CH = 17, ROWS = 15, LAST = 256, RS = 272;
-    static constexpr bool FLOAT_D = true;
+    static constexpr bool FLOAT_D = true, MINS = false;
+    static constexpr int GRID = 0;
     struct H { float d[4]; float dm; };
     template <int S>
     static QH_DEV int piece(int kg) { return 4 * S + kg; }
@@ -185,7 +189,7 @@ struct M16Q80 {
         o.dm = 0.f;
         return o;
     }
-    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B) {
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char*) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const int p = 4 * s + kg;
@@ -198,6 +202,75 @@ struct M16Q80 {
     static QH_DEV int mn(const H&, int) { return 0; }
     template <int S>
     static QH_DEV float dsc(const H& h) { return h.d[S]; }
+};
+
+// IQ3_S / IQ2_XXS: signed codebook bytes as the B operand (qh_iq3s_piece /
+// qh_iq2xxs_piece), the codebook in the workgroup's LDS (GRID 1 / 2).  Lane kg,
+// MFMA s: half kg % 2 of sub-block 2s + kg / 2, i.e. piece 4s + kg; its scale is
+// the sub-block's odd integer, no mins.
+struct M16IQ3S {
+    static constexpr int BYTES = 110, CH = 7, ROWS = 16, LAST = 94, RS = QH_RS;
+    static constexpr bool FLOAT_D = false, MINS = false;
+    static constexpr int GRID = 1;
+    struct H { int sc[4]; float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r, int kg) {
+        H o;
+        // scales[0..3] sit at LDS 108..111 (block bytes 106..109)
+        const uint32_t s4 = *reinterpret_cast<const uint32_t*>(r + qh_iq3s_at(106));
+        const int nib = 4 * ((kg >> 1) & 1);
+#pragma unroll
+        for (int s = 0; s < 4; s++) o.sc[s] = 1 + 2 * (int)((s4 >> (8 * s + nib)) & 0xFu);
+        o.d = qh_h2f(qh_rd16(r, 0));
+        o.dm = 0.f;
+        return o;
+    }
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char* grid) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            uint32_t v[4];
+            int sc;
+            qh_iq3s_piece(r, 2 * s + (kg >> 1), kg & 1, reinterpret_cast<const uint32_t*>(grid), v, sc);
+#pragma unroll
+            for (int m = 0; m < 4; m++) B[s][m] = (int)v[m];
+        }
+    }
+    template <int S>
+    static QH_DEV int piece(int kg) { return 4 * S + kg; }
+    template <int S>
+    static QH_DEV int scl(const H& h, int) { return h.sc[S]; }
+    template <int S>
+    static QH_DEV int mn(const H&, int) { return 0; }
+};
+
+struct M16IQ2XXS {
+    static constexpr int BYTES = 66, CH = 5, ROWS = 16, LAST = 50, RS = QH_RS;
+    static constexpr bool FLOAT_D = false, MINS = false;
+    static constexpr int GRID = 2;
+    struct H { int sc[4]; float d, dm; };
+    static QH_DEV H hdr(const unsigned char* r, int kg) {
+        H o;
+#pragma unroll
+        for (int s = 0; s < 4; s++) o.sc[s] = 2 * (int)(r[qh_iq2xxs_at(9 + 8 * (2 * s + (kg >> 1)))] >> 4) + 1;
+        o.d = 0.125f * qh_h2f(qh_rd16(r, 0));
+        o.dm = 0.f;
+        return o;
+    }
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char* grid) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            uint32_t v[4];
+            int sc;
+            qh_iq2xxs_piece(r, 2 * s + (kg >> 1), kg & 1, reinterpret_cast<const uint64_t*>(grid), v, sc);
+#pragma unroll
+            for (int m = 0; m < 4; m++) B[s][m] = (int)v[m];
+        }
+    }
+    template <int S>
+    static QH_DEV int piece(int kg) { return 4 * S + kg; }
+    template <int S>
+    static QH_DEV int scl(const H& h, int) { return h.sc[S]; }
+    template <int S>
+    static QH_DEV int mn(const H&, int) { return 0; }
 };
 
 // 16-row tiles of the same formats (3 loads per lane and group instead of 2):
@@ -247,7 +320,8 @@ struct QhMats {
 // ring of wavefront partials, finished rows and the per-wavefront sums of x^2.
 template <class F, int W, int GPW>
 constexpr int qh_mmv16_lds() {
-    return W * GPW * (F::ROWS * F::RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4;
+    return W * GPW * (F::ROWS * F::RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4 +
+           (F::GRID ? 2048 : 0);
 }
 
 // The kernel body for workgroup `bid` of `nblk` working on mm's tiles (a
@@ -269,6 +343,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
     float* res = red + 2 * QH_RING * W * 16;  // finished rows of this workgroup's tiles
     float* sqw = res + QH_MAXT * 16;           // per-wavefront sums of x^2 (fused RMS norm)
+    unsigned char* gridl = reinterpret_cast<unsigned char*>(sqw + W);  // IQ codebook (GRID formats)
     const int ntiles = mm.tstart[QH_MULTI];
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
@@ -447,7 +522,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
             const unsigned char* wrow = wl + t * TILE + (n < ROWS ? n : 0) * RS;
             const typename F::H hd = F::hdr(wrow, kg);
             qh_i32x4 B[4];
-            F::bops(wrow, kg, hd, B);
+            F::bops(wrow, kg, hd, B, gridl);
             int i0 = 0, i1 = 0, i2 = 0;
             float fm = 0.f;
             const unsigned char* xt = xl + t * QH_XG;
@@ -464,8 +539,10 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                     i0 += __mul24(sc, D[0]);
                     i1 += __mul24(sc, D[1]);
                     i2 += __mul24(sc, D[2]);
-                    const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
-                    fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+                    if constexpr (F::MINS) {
+                        const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
+                        fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             };
@@ -476,7 +553,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
             if constexpr (!F::FLOAT_D) {
                 const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
                 acc = fmaf(hd.d, P, acc);
-                accm = fmaf(hd.dm, fm, accm);
+                if constexpr (F::MINS) accm = fmaf(hd.dm, fm, accm);
             }
         }
         return fmaf(acc, rs, -accm);
@@ -531,6 +608,11 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     load_x(0, xva);
     load_nw(nv);
     load_w(tile, 0, wra);
+    if constexpr (F::GRID != 0) {
+        const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
+        for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
+        __syncthreads();
+    }
     int it = 0;
     auto body = [&](qh_u32x4* wr, float4* xv) -> bool {
         const int ch = item_ch(it);
@@ -749,6 +831,8 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
                        ? dispatch_mmv16<M16Q5K16>(W, x, y, in_dim, out_dim, row_bytes, st)
                        : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_IQ3_S: return dispatch_mmv16<M16IQ3S>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_IQ2_XXS: return dispatch_mmv16<M16IQ2XXS>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q8_0:
             return qh_rows16_better(M16Q80::ROWS, out_dim)
                        ? dispatch_mmv16<M16Q8016>(W, x, y, in_dim, out_dim, row_bytes, st)

@@ -1,16 +1,21 @@
-"""Llama-3-8B-shaped Q4_K_M decode step: the weight GEMVs of one token.
+"""Decode-step drivers over the C ABI, with random-init weights generated on the
+device (seeded).
 
-Per layer, in the order of forward_gpu_step (src/cuda.rs:556-562, :647, :773-788):
+  DecodeStep   the weight GEMVs/GEMMs of a Llama-3-8B Q4_K_M step alone
+               (activations fixed): weight streaming, >99% of a step's bytes.
+  MoeLayer     a Mixtral-shaped expert layer's GEMMs over fixed gathered tokens.
+  MoeStep      a full MoE FFN for a batch of tokens: router GEMM, device-side
+               top-k routing, gather, expert GEMMs, SwiGLU, weighted combine
+               (moe_ffn, src/main.rs:952-1043; src/cuda.rs:667-798).
+  ForwardStep  forward_gpu_step (src/cuda.rs:507-851, dense path) end to end for
+               one token: embedding, 32 layers of fused GEMVs, attention and
+               glue, the head.
+  BatchStep    the same for N sequences in lockstep on batched GEMMs.
+
+Layer shapes (forward_gpu_step's order, src/cuda.rs:556-562, :647, :773-788):
   q 4096x4096 Q4_K, k 1024x4096 Q4_K, v 1024x4096 Q6_K, o 4096x4096 Q4_K,
   gate 14336x4096 Q4_K, up 14336x4096 Q4_K, down 4096x14336 Q6_K;
 then the output head 128256x4096 Q6_K.  32 layers: 4,875,853,824 weight bytes.
-
-`DecodeStep` holds random-init weights (seeded, generated on the device) and
-issues the step's GEMVs (n tokens: hip_gemm, n = 1: hip_gemv) through the C ABI
-on a caller stream.  The glue between GEMVs (rms_norm, rope, attention, swiglu,
-residual adds) is not part of this library yet: activations are fixed buffers,
-so a step measures weight streaming, which is >99% of the bytes of a decode step
-at short context.
 """
 from dataclasses import dataclass
 
@@ -160,6 +165,96 @@ class MoeLayer:
                                                           self.up[e].data_ptr(), h, f, n, sp))
             check("hip_gemm_async", self.L.hip_gemm_async(t, self.expert(self.wd, e), self.hbuf[e].data_ptr(),
                                                           self.down[e].data_ptr(), f, h, n, sp))
+
+
+class MoeStep:
+    """One MoE FFN for n tokens, all on the device: moe_ffn (src/main.rs:952-1043)
+    and its GPU twin (src/cuda.rs:667-798) for any expert count, top-k and types.
+
+      logits = router_w x (+ router_b)       hip_gemm (F32)
+      ids, w = top-k + softmax               hip_moe_route (renorm or OLMoE form)
+      slots  = expert-ordered (token, j)     hip_moe_plan; tok_off copied back
+      xg     = x[slot_tok]                   hip_moe_gather
+      g, u   = gate/up of each slot's expert hip_gemm_grouped / hip_gemm_moe
+      act    = swiglu(g + bg, u + bu)        hip_moe_swiglu (plain or OAI clamp)
+      yg     = down act                      hip_gemm_moe
+      out    = (out +) sum_j w * (yg + bd)   hip_moe_combine
+
+    Weights: wg, wu [E][f][d] and wd [E][d][f] stacked GGUF bytes (expert e at
+    e * slice, src/cuda.rs:250-258); router_w [E][d] f32; biases optional
+    [E][f] / [E][d] / [E].  The one host round trip is tok_off (E + 1 ints), at
+    the point where the reference copies the router logits back."""
+
+    def __init__(self, types, wg, wu, wd, router_w, E, k, d, f, n_max, renorm=True, oai=False, router_b=None,
+                 gate_b=None, up_b=None, down_b=None):
+        from . import type_size
+        self.L = lib()
+        self.tg, self.tu, self.td = types
+        self.wg, self.wu, self.wd, self.rw = wg, wu, wd, router_w
+        self.E, self.k, self.d, self.f, self.n_max = E, k, d, f, n_max
+        self.renorm, self.oai = int(renorm), int(oai)
+        self.rb, self.gb, self.ub, self.db = router_b, gate_b, up_b, down_b
+        self.sg, self.su = type_size(self.tg, f * d), type_size(self.tu, f * d)
+        dev, S = "cuda", n_max * k
+        self.logits = torch.empty(n_max, E, device=dev)
+        self.ids = torch.empty(n_max, k, dtype=torch.int32, device=dev)
+        self.wts = torch.empty(n_max, k, device=dev)
+        self.tok_off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        self.slot_of = torch.empty(n_max, k, dtype=torch.int32, device=dev)
+        self.slot_tok = torch.empty(S, dtype=torch.int32, device=dev)
+        self.slot_exp = torch.empty(S, dtype=torch.int32, device=dev)
+        self.xg = torch.empty(S, d, device=dev)
+        self.g = torch.empty(S, f, device=dev)
+        self.u = torch.empty(S, f, device=dev)
+        self.act = torch.empty(S, f, device=dev)
+        self.yg = torch.empty(S, d, device=dev)
+        self.tok_off_host = torch.empty(E + 1, dtype=torch.int32, pin_memory=True)
+
+    @staticmethod
+    def _p(t):
+        return t.data_ptr() if t is not None else None
+
+    def issue(self, x, out, n, accumulate=False, stream=None):
+        """x: device f32 [n][d] (normed activations), out: device f32 [n][d]."""
+        assert 0 < n <= self.n_max
+        st = stream or torch.cuda.current_stream()
+        sp = st.cuda_stream
+        L, E, k, d, f = self.L, self.E, self.k, self.d, self.f
+        xp = x.data_ptr()
+        check("hip_gemm_async", L.hip_gemm_async(0, self.rw.data_ptr(), xp, self.logits.data_ptr(), d, E, n, sp))
+        check("hip_moe_route_async",
+              L.hip_moe_route_async(self.logits.data_ptr(), self._p(self.rb), n, E, k, self.renorm,
+                                    self.ids.data_ptr(), self.wts.data_ptr(), sp))
+        check("hip_moe_plan_async",
+              L.hip_moe_plan_async(self.ids.data_ptr(), n, k, E, self.tok_off.data_ptr(), self.slot_of.data_ptr(),
+                                   self.slot_tok.data_ptr(), self.slot_exp.data_ptr(), sp))
+        self.tok_off_host.copy_(self.tok_off, non_blocking=True)
+        st.synchronize()
+        off = self.tok_off_host.tolist()
+        sel = [e for e in range(E) if off[e + 1] > off[e]]
+        s_off = [off[e] for e in sel] + [off[E]]
+        S = off[E]
+        check("hip_moe_gather_async", L.hip_moe_gather_async(self.xg.data_ptr(), xp, self.slot_tok.data_ptr(), S, d,
+                                                             sp))
+        if self.tg == self.tu and 2 * len(sel) <= 16:
+            # gate and up of every selected expert in one grouped launch (x digitised once per expert)
+            xs = [self.xg.data_ptr() + 4 * d * off[e] for e in sel]
+            gemm_grouped_async(L, self.tg, [self.wg.data_ptr() + e * self.sg for e in sel] +
+                               [self.wu.data_ptr() + e * self.su for e in sel], xs + xs,
+                               [self.g.data_ptr() + 4 * f * off[e] for e in sel] +
+                               [self.u.data_ptr() + 4 * f * off[e] for e in sel],
+                               [off[e + 1] - off[e] for e in sel] * 2, [f] * (2 * len(sel)), d, sp)
+        else:
+            gemm_moe_async(L, self.tg, self.wg.data_ptr(), sel, s_off, self.xg.data_ptr(), self.g.data_ptr(), d, f, sp)
+            gemm_moe_async(L, self.tu, self.wu.data_ptr(), sel, s_off, self.xg.data_ptr(), self.u.data_ptr(), d, f, sp)
+        check("hip_moe_swiglu_async",
+              L.hip_moe_swiglu_async(self.act.data_ptr(), self.g.data_ptr(), self.u.data_ptr(), self._p(self.gb),
+                                     self._p(self.ub), self.slot_exp.data_ptr(), S, f, self.oai, sp))
+        gemm_moe_async(L, self.td, self.wd.data_ptr(), sel, s_off, self.act.data_ptr(), self.yg.data_ptr(), f, d, sp)
+        check("hip_moe_combine_async",
+              L.hip_moe_combine_async(out.data_ptr(), self.yg.data_ptr(), self.slot_of.data_ptr(),
+                                      self.wts.data_ptr(), self.ids.data_ptr(), self._p(self.db), n, k, d,
+                                      int(accumulate), sp))
 
 
 @dataclass(frozen=True)

@@ -89,3 +89,54 @@ def test_swiglu_forms():
     o = g.swiglu_oai(gg, np.array([0.0, 1.0, 8.0, -9.0]))
     assert np.isclose(o[3], 7 / (1 + np.exp(-1.702 * 7)) * (-7 + 1))
     assert np.isclose(o[2], 2 / (1 + np.exp(-3.404)) * 8.0)
+
+
+def test_moe_route_order():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(37).astype(np.float32)
+    for k in (1, 4, 37):
+        ids, _ = g.moe_route(v, k)
+        assert list(ids) == list(np.argsort(-v.astype(np.float64), kind="stable")[:k])
+    # total order: +0 above -0; +NaN above +inf, -NaN below -inf; ties: lower index first
+    nan, neg_nan = np.float32(np.nan), -np.float32(np.nan)
+    v = np.array([-0.0, 0.0, 1.0, 1.0, -np.inf, np.inf, neg_nan, nan, -5.0], np.float32)
+    ids, _ = g.moe_route(v, 9)
+    assert list(ids) == [7, 5, 2, 3, 1, 0, 8, 4, 6]
+    # the router bias is added before the sort
+    ids, _ = g.moe_route([0.0, 1.0, 2.0], 1, bias=[5.0, 0.0, 0.0])
+    assert list(ids) == [0]
+
+
+def test_moe_route_weights():
+    rng = np.random.default_rng(4)
+    v = (rng.standard_normal(16) * 3).astype(np.float32)
+    # renorm: softmax over the chosen k; with k = all, they sum to 1
+    _, w = g.moe_route(v, 16, renorm=True)
+    assert abs(float(np.sum(w.astype(np.float64))) - 1.0) < 1e-6
+    ids, w = g.moe_route(v, 3, renorm=True)
+    top = v[ids].astype(np.float64)
+    ref = np.exp(top - top.max()) / np.exp(top - top.max()).sum()
+    assert np.allclose(w, ref, rtol=1e-6)
+    # OLMoE: the chosen entries of a softmax over all experts (not renormalised)
+    ids, w = g.moe_route(v, 3, renorm=False)
+    full = np.exp(v.astype(np.float64) - v.max()) / np.exp(v.astype(np.float64) - v.max()).sum()
+    assert np.allclose(w, full[ids], rtol=1e-6)
+    assert float(np.sum(w)) < 1.0
+
+
+def test_moe_ffn_single_expert_is_dense_ffn():
+    rng = np.random.default_rng(5)
+    d, f, E = 8, 12, 3
+    gate = [rng.standard_normal((f, d)) for _ in range(E)]
+    up = [rng.standard_normal((f, d)) for _ in range(E)]
+    down = [rng.standard_normal((d, f)) for _ in range(E)]
+    x = rng.standard_normal(d)
+    dense = down[1] @ (gate[1] @ x / (1 + np.exp(-(gate[1] @ x))) * (up[1] @ x))
+    assert np.allclose(g.moe_ffn(x, [1], [1.0], gate, up, down), dense)
+    # linear in the weights, biases added where the reference adds them
+    bd = rng.standard_normal((E, d))
+    two = g.moe_ffn(x, [1, 2], [0.25, 0.5], gate, up, down, down_b=bd)
+    one1 = g.moe_ffn(x, [1], [1.0], gate, up, down, down_b=bd)
+    one2 = g.moe_ffn(x, [2], [1.0], gate, up, down, down_b=bd)
+    assert np.allclose(two, 0.25 * one1 + 0.5 * one2)
+    assert np.allclose(one1, dense + bd[1])

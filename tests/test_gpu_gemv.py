@@ -308,3 +308,21 @@ def test_gemm_grouped_ex(qh, oracle, t, n, swiglu, acc):
             ratio = np.max(np.abs(gx).max(axis=1) / np.sqrt((gx * gx).mean(axis=1)))
             tol = min(max(2e-4, 2.0 ** -15 * ratio * 2), 1e-3)
             assert cf.rel_l2(got[i], ref) < tol, (k, i, ratio, cf.rel_l2(got[i], ref))
+
+
+@pytest.mark.parametrize("in_dim, out_dim, n, off", [(4096, 8, 64, 0), (1001, 257, 3, 0), (2880, 32, 5, 1),
+                                                     (64, 128, 300, 0)])
+def test_gemm_f32_router(qh, oracle, in_dim, out_dim, n, off):
+    """F32 weights over a batch (MoE routers) take one launch; off = 1 shifts x
+    by one float so the float4 path is not used."""
+    import torch
+    rng = np.random.default_rng(in_dim + n)
+    w = rng.standard_normal((out_dim, in_dim)).astype(np.float32)
+    x = rng.standard_normal((n, in_dim)).astype(np.float32)
+    W = torch.from_numpy(w).cuda()
+    X = torch.from_numpy(np.concatenate([np.zeros(off, np.float32), x.reshape(-1)])).cuda()
+    Y = torch.empty(n, out_dim, device="cuda")
+    check("hip_gemm", qh.hip_gemm(0, W.data_ptr(), X.data_ptr() + 4 * off, Y.data_ptr(), in_dim, out_dim, n))
+    torch.cuda.synchronize()
+    ref = oracle.gemm(0, x, w.view(np.uint8).reshape(-1), in_dim, out_dim, n)
+    assert cf.rel_l2(Y.cpu().numpy(), ref) < 1e-5  # two f32 summation orders over up to 4096 terms
