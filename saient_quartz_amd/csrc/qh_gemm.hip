@@ -780,6 +780,21 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
     if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || count < 1) return hipErrorNotSupported;
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;
+    if (!X2 && count <= 4) {
+        // 2-4 tokens of one x shared by up to 4 matrices: the GEMV kernel carries
+        // the tokens (no x-image prologue, the weights read once)
+        bool same = n[0] >= 2 && n[0] <= 4;
+        for (int i = 1; i < count; i++) same = same && X[i] == X[0] && n[i] == n[0];
+        // 3-4 tokens: the four MFMAs per token and group make big matrices
+        // compute-bound in the GEMV kernel (measured slower above ~16 MB)
+        int64_t wbytes = 0;
+        for (int i = 0; i < count; i++) wbytes += (int64_t)qh_type_size(type, (size_t)in_dim) * (out_dims[i] > 0 ? out_dims[i] : 0);
+        if (same && (n[0] == 2 || wbytes <= ((int64_t)16 << 20))) {
+            hipError_t e = qh_launch_mmv16_tokens(type, count, W, Y, out_dims, out_dims, X[0], in_dim, n[0], in_dim,
+                                                  accum, st);
+            if (e != hipErrorNotSupported) return e;
+        }
+    }
     const QgScratch* sc = qh_mmq_scratch_ptrs();
     if (!sc) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);

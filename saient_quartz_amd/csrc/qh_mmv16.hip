@@ -314,36 +314,52 @@ struct QhMats {
     //   accum: y += result instead of y = result (the residual add).
     const float* nw;
     int accum;
+    // Launches with NT > 1 tokens: ntok (<= NT) tokens of x, token t at x + t * ldx,
+    // its results at y[m] + t * ldy[m].  Unused when NT = 1.
+    int ntok, ldx;
+    int ldy[QH_MULTI];
 };
+
+// Tokens per launch (NT) share every weight load and B operand; the x digit
+// planes, the ring of wavefront partials and the finished rows grow with NT, so
+// NT > 1 keeps a shorter ring and fewer tiles per workgroup to fit 160 KB of LDS.
+template <int NT>
+constexpr int qh_ring() { return NT > 1 ? 2 : QH_RING; }
+template <int NT>
+constexpr int qh_maxt() { return NT > 2 ? 8 : (NT > 1 ? 16 : QH_MAXT); }
 
 // LDS of one workgroup: GPW staging tiles and x digit planes per wavefront, the
 // ring of wavefront partials, finished rows and the per-wavefront sums of x^2.
-template <class F, int W, int GPW>
+template <class F, int W, int GPW, int NT = 1>
 constexpr int qh_mmv16_lds() {
-    return W * GPW * (F::ROWS * F::RS + 16) + W * GPW * QH_XG + 2 * QH_RING * W * 16 * 4 + QH_MAXT * 16 * 4 + W * 4 +
-           (F::GRID ? 2048 : 0);
+    return W * GPW * (F::ROWS * F::RS + 16) + W * GPW * NT * QH_XG + 2 * qh_ring<NT>() * W * 16 * 4 * NT +
+           qh_maxt<NT>() * 16 * 4 * NT + W * 4 * NT + (F::GRID ? 2048 : 0);
 }
 
 // The kernel body for workgroup `bid` of `nblk` working on mm's tiles (a
 // launch may run two bodies of different formats side by side, see qh_mmv16_mix).
-template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR>
+template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR, int NT = 1>
 __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __restrict__ x, uint32_t row_bytes,
                                               int ngroups, unsigned char* lds, const int bid, const int nblk) {
+    static_assert(!PAIR || NT == 1, "SwiGLU pairs run one token");
+    constexpr int RING = qh_ring<NT>();
     constexpr int ROWS = F::ROWS, CH = F::CH;
     constexpr int NH = (ROWS * CH + 63) / 64;  // 16-byte loads per lane and group
     constexpr int RS = F::RS;                // LDS line per row
     static_assert(ROWS <= 16 && 16 * CH <= RS, "tile shape");
     constexpr int TILE = ROWS * RS + 16;  // staging tile of one group + 16 spare bytes
-    // Wavefront partials of finished tiles wait in a ring of two sets of QH_RING
+    // Wavefront partials of finished tiles wait in a ring of two sets of RING
     // tiles; the workgroup meets at a barrier only when a set is full.
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const QhBuf xb = qh_buf(x, 4u * 256u * (uint32_t)ngroups);
+    const int ntok = NT == 1 ? 1 : mm.ntok;
+    const QhBuf xb = qh_buf(x, 4u * (256u * (uint32_t)ngroups + (NT > 1 ? (uint32_t)(mm.ldx * (ntok - 1)) : 0u)));
     unsigned char* wl = lds + w * (GPW * TILE);  // GPW staging tiles of this wavefront
-    unsigned char* xl = lds + W * GPW * TILE + w * (GPW * QH_XG);
-    float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * QH_XG);
-    float* res = red + 2 * QH_RING * W * 16;  // finished rows of this workgroup's tiles
-    float* sqw = res + QH_MAXT * 16;           // per-wavefront sums of x^2 (fused RMS norm)
-    unsigned char* gridl = reinterpret_cast<unsigned char*>(sqw + W);  // IQ codebook (GRID formats)
+    // x digit planes of group t, token k at xl + (t NT + k) QH_XG
+    unsigned char* xl = lds + W * GPW * TILE + w * (GPW * NT * QH_XG);
+    float* red = reinterpret_cast<float*>(lds + W * GPW * TILE + W * GPW * NT * QH_XG);
+    float* res = red + 2 * RING * W * 16 * NT;  // finished rows of this workgroup's tiles
+    float* sqw = res + qh_maxt<NT>() * 16 * NT;  // per-wavefront sums of x^2 (fused RMS norm)
+    unsigned char* gridl = reinterpret_cast<unsigned char*>(sqw + W * NT);  // IQ codebook (GRID formats)
     const int ntiles = mm.tstart[QH_MULTI];
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
@@ -411,13 +427,19 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                 wo[t * NH + h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)(g0 + t));
             }
     };
+    // x of group t, token k -> xo[t NT + k]; tokens past ntok read as zeros.
     auto load_x = [&](int ch, float4* xo) {
         const int g0 = ch * (W * GPW) + w * GPW;
 #pragma unroll
-        for (int t = 0; t < GPW; t++) {
-            const qh_u32x4 v = qh_ld128(xb, 1024u * (uint32_t)(g0 + t) + 16u * lane);
-            xo[t] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        }
+        for (int t = 0; t < GPW; t++)
+#pragma unroll
+            for (int k = 0; k < NT; k++) {
+                const uint32_t o = k < ntok ? 1024u * (uint32_t)(g0 + t) + 16u * lane + (NT > 1 ? 4u * (uint32_t)(k * mm.ldx) : 0u)
+                                            : 0x80000000u;
+                const qh_u32x4 v = qh_ld128(xb, o);
+                xo[t * NT + k] =
+                    float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+            }
     };
     // Fused RMS norm (X1 only): this wavefront's sum of x^2 goes to sqw[w] and x
     // becomes x * nw.  The row scale rsqrt(mean + eps) is applied at the end.
@@ -433,30 +455,33 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     auto norm_x = [&](float4* xo, const qh_u32x4* nv) {
         if constexpr (X1) {
             if (mm.nw) {
-                float sq = 0.f;
 #pragma unroll
-                for (int t = 0; t < GPW; t++) {
-                    const qh_u32x4 v = nv[t];
-                    float4& a = xo[t];
-                    sq += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
-                    a.x *= __uint_as_float(v.x);
-                    a.y *= __uint_as_float(v.y);
-                    a.z *= __uint_as_float(v.z);
-                    a.w *= __uint_as_float(v.w);
+                for (int k = 0; k < NT; k++) {
+                    float sq = 0.f;
+#pragma unroll
+                    for (int t = 0; t < GPW; t++) {
+                        const qh_u32x4 v = nv[t];
+                        float4& a = xo[t * NT + k];
+                        sq += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+                        a.x *= __uint_as_float(v.x);
+                        a.y *= __uint_as_float(v.y);
+                        a.z *= __uint_as_float(v.z);
+                        a.w *= __uint_as_float(v.w);
+                    }
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+                    if (lane == 0) sqw[k * W + w] = sq;
                 }
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-                if (lane == 0) sqw[w] = sq;
             }
         }
     };
     // Row scale of the fused RMS norm (1 without it); valid after a barrier.
-    auto norm_scale = [&]() -> float {
+    auto norm_scale = [&](int k) -> float {
         if constexpr (X1) {
             if (mm.nw) {
                 float t = 0.f;
 #pragma unroll
-                for (int i = 0; i < W; i++) t += sqw[i];
+                for (int i = 0; i < W; i++) t += sqw[k * W + i];
                 return rsqrtf(t / (float)(256 * ngroups) + 1e-5f);
             }
         }
@@ -464,13 +489,16 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     };
     // x -> digit planes in LDS.  One exponent per wavefront and chunk:
     // max|x| * 2^s < 2^22.  Returns 2^-s; `bad` turns NaN when x is not finite.
-    float bad = 0.f;
-    auto prep_x = [&](const float4* xv) -> float {
+    float bad[NT];
+#pragma unroll
+    for (int k = 0; k < NT; k++) bad[k] = 0.f;
+    auto prep_x = [&](const float4* xall, int k) -> float {
         float m = 0.f;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[t].x), fabsf(xv[t].y)), fmaxf(fabsf(xv[t].z), fabsf(xv[t].w))));
-            bad += ((xv[t].x * 0.f + xv[t].y * 0.f) + (xv[t].z * 0.f + xv[t].w * 0.f));
+            const float4 xv = xall[t * NT + k];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w))));
+            bad[k] += ((xv.x * 0.f + xv.y * 0.f) + (xv.z * 0.f + xv.w * 0.f));
         }
         m = qh_dpp_max(m);
         int e = 0;
@@ -481,7 +509,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         const uint32_t bias = 0x4B400000u - 0x808080u;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
-            const float4 v = xv[t];
+            const float4 v = xall[t * NT + k];
+            unsigned char* xp = xl + (t * NT + k) * QH_XG;
             const uint32_t a0 = (__float_as_uint(fmaf(v.x, scx, 12582912.0f)) - bias) ^ 0x808080u;
             const uint32_t a1 = (__float_as_uint(fmaf(v.y, scx, 12582912.0f)) - bias) ^ 0x808080u;
             const uint32_t a2 = (__float_as_uint(fmaf(v.z, scx, 12582912.0f)) - bias) ^ 0x808080u;
@@ -491,15 +520,15 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
             const uint32_t u01 = __builtin_amdgcn_perm(a1, a0, 0x06020602u);
             const uint32_t u23 = __builtin_amdgcn_perm(a3, a2, 0x06020602u);
             // lane holds x[256t + 4 lane .. +3] = positions 4(lane%4).. of piece lane/4.
-            unsigned char* ub = xl + t * QH_XG + 4 * lane;
+            unsigned char* ub = xp + 4 * lane;
             *reinterpret_cast<uint32_t*>(ub) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
             *reinterpret_cast<uint32_t*>(ub + 256) = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
             *reinterpret_cast<uint32_t*>(ub + 512) = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
             float hs = (v.x + v.y) + (v.z + v.w);
             hs += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hs), 0xB1, 0xF, 0xF, false));
             hs += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hs), 0x4E, 0xF, 0xF, false));
-            if ((lane & 3) == 0) *reinterpret_cast<float*>(xl + t * QH_XG + QH_XG_SUM + lane) = hs;
-            if (lane == 0) *reinterpret_cast<qh_u32x4*>(xl + t * QH_XG + QH_XG_ZERO) = qh_u32x4{0, 0, 0, 0};
+            if ((lane & 3) == 0) *reinterpret_cast<float*>(xp + QH_XG_SUM + lane) = hs;
+            if (lane == 0) *reinterpret_cast<qh_u32x4*>(xp + QH_XG_ZERO) = qh_u32x4{0, 0, 0, 0};
         }
         return ldexpf(1.0f, -s);
     };
@@ -514,84 +543,94 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    // One staged item: four MFMAs per group.
-    auto compute = [&](float rs) -> float {
-        float acc = 0.f, accm = 0.f;
+    // One staged item: four MFMAs per group and token, the B operands shared by
+    // the tokens; out[k] = token k's partial of the lane's row.
+    auto compute = [&](const float* rs, float* out) {
+        float acc[NT], accm[NT];
+#pragma unroll
+        for (int k = 0; k < NT; k++) acc[k] = accm[k] = 0.f;
 #pragma unroll
         for (int t = 0; t < GPW; t++) {
             const unsigned char* wrow = wl + t * TILE + (n < ROWS ? n : 0) * RS;
             const typename F::H hd = F::hdr(wrow, kg);
             qh_i32x4 B[4];
             F::bops(wrow, kg, hd, B, gridl);
-            int i0 = 0, i1 = 0, i2 = 0;
-            float fm = 0.f;
-            const unsigned char* xt = xl + t * QH_XG;
-            auto mfma = [&](auto SC) {
-                constexpr int S = decltype(SC)::value;
-                const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xt + aoff[S]);
-                const qh_i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[S], qh_i32x4{0, 0, 0, 0}, 0, 0, 0);
-                if constexpr (F::FLOAT_D) {
-                    // each piece has its own f32 scale (the digit dots are exact in f32)
-                    const float P = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
-                    acc = fmaf(F::template dsc<S>(hd), P, acc);
-                } else {
-                    const int sc = F::template scl<S>(hd, kg);
-                    i0 += __mul24(sc, D[0]);
-                    i1 += __mul24(sc, D[1]);
-                    i2 += __mul24(sc, D[2]);
-                    if constexpr (F::MINS) {
-                        const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
-                        fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+#pragma unroll
+            for (int k = 0; k < NT; k++) {
+                int i0 = 0, i1 = 0, i2 = 0;
+                float fm = 0.f;
+                const unsigned char* xt = xl + (t * NT + k) * QH_XG;
+                auto mfma = [&](auto SC) {
+                    constexpr int S = decltype(SC)::value;
+                    const qh_i32x4 a = *reinterpret_cast<const qh_i32x4*>(xt + aoff[S]);
+                    const qh_i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[S], qh_i32x4{0, 0, 0, 0}, 0, 0, 0);
+                    if constexpr (F::FLOAT_D) {
+                        // each piece has its own f32 scale (the digit dots are exact in f32)
+                        const float P = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
+                        acc[k] = fmaf(F::template dsc<S>(hd), P, acc[k]);
+                    } else {
+                        const int sc = F::template scl<S>(hd, kg);
+                        i0 += __mul24(sc, D[0]);
+                        i1 += __mul24(sc, D[1]);
+                        i2 += __mul24(sc, D[2]);
+                        if constexpr (F::MINS) {
+                            const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
+                            fm = fmaf((float)F::template mn<S>(hd, kg), xs, fm);
+                        }
                     }
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                mfma(std::integral_constant<int, 0>{});
+                mfma(std::integral_constant<int, 1>{});
+                mfma(std::integral_constant<int, 2>{});
+                mfma(std::integral_constant<int, 3>{});
+                if constexpr (!F::FLOAT_D) {
+                    const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
+                    acc[k] = fmaf(hd.d, P, acc[k]);
+                    if constexpr (F::MINS) accm[k] = fmaf(hd.dm, fm, accm[k]);
                 }
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            mfma(std::integral_constant<int, 0>{});
-            mfma(std::integral_constant<int, 1>{});
-            mfma(std::integral_constant<int, 2>{});
-            mfma(std::integral_constant<int, 3>{});
-            if constexpr (!F::FLOAT_D) {
-                const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
-                acc = fmaf(hd.d, P, acc);
-                if constexpr (F::MINS) accm = fmaf(hd.dm, fm, accm);
             }
         }
-        return fmaf(acc, rs, -accm);
+#pragma unroll
+        for (int k = 0; k < NT; k++) out[k] = fmaf(acc[k], rs[k], -accm[k]);
     };
 
-    auto put = [&](int d, int c, float r) {  // y of row c of this workgroup's tile d
+    auto put = [&](int d, int c, float r, int k) {  // y of row c of this workgroup's tile d, token k
         const int tile = wg_tile(d), m = mat_of(tile);
         const int row = local_tile(tile, m) * ROWS + c;
-        if (c < ROWS && row < mm.rows[m]) {
-            float* yp = mm.y[m] + row;
+        if (c < ROWS && row < mm.rows[m] && k < ntok) {
+            float* yp = mm.y[m] + (NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row;
             *yp = mm.accum ? *yp + r : r;
         }
     };
     // Sum the wavefront partials of tiles d0 .. d0+cnt-1 (one set of the ring)
     // into res, or into y once the loop is over: a store inside the loop would
     // make the compiler drain all loads in flight (stores and loads share vmcnt).
-    float nsc = 1.f;  // fused RMS-norm row scale, set after the first barrier
+    float nsc[NT];  // fused RMS-norm row scale per token, set after the first barrier
+#pragma unroll
+    for (int k = 0; k < NT; k++) nsc[k] = 1.f;
     auto flush = [&](int d0, int cnt, bool direct) {
-        if ((int)threadIdx.x < 16 * cnt) {
-            const int d = d0 + ((int)threadIdx.x >> 4), c = threadIdx.x & 15;
-            const float* rb = red + (d % (2 * QH_RING)) * (W * 16) + c;
+        if ((int)threadIdx.x < 16 * cnt * NT) {
+            const int q = (int)threadIdx.x >> 4, c = threadIdx.x & 15;
+            const int k = NT > 1 ? q / cnt : 0, d = d0 + q - k * cnt;
+            const float* rb = red + ((d % (2 * RING)) * NT + k) * (W * 16) + c;
             float r = 0.f;
 #pragma unroll
             for (int i = 0; i < W; i++) r += rb[i * 16];
-            r *= nsc;
-            if (direct) put(d, c, r);
-            else res[d * 16 + c] = r;
+            r *= nsc[k];
+            if (direct) put(d, c, r, k);
+            else res[(d * NT + k) * 16 + c] = r;
         }
     };
     int tile = wg_tile(0), done = 0;
     if (tile >= ntiles) return;  // uniform over the workgroup
-    // Few tiles per workgroup: meet every QH_RING tiles (the end-of-kernel wait
+    // Few tiles per workgroup: meet every RING tiles (the end-of-kernel wait
     // for the slowest wavefront is what short launches pay).  Many tiles: meet
     // at every tile (PAIR: every pair), which keeps the wavefronts on one tile's
     // rows at a time.
     const int my_tiles = PAIR ? 2 * ((ntiles / 2 - bid + nblk - 1) / nblk)
                               : (ntiles - bid + nblk - 1) / nblk;
-    const int ring = my_tiles <= 2 * QH_RING ? QH_RING : (PAIR ? 2 : 1);
+    const int ring = my_tiles <= 2 * RING ? RING : (PAIR ? 2 : 1);
     // Pipeline: the registers of an item are staged into LDS as soon as they
     // arrive and then receive the loads of the next item, which stay in flight
     // while the staged item is computed.  No loaded value is copied between
@@ -602,8 +641,10 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     auto item_tile = [&](int it) { return wg_tile(it / cpt); };
     auto item_ch = [&](int it) { return it - (it / cpt) * cpt; };
     qh_u32x4 wra[GPW * NH];
-    float4 xva[GPW];
-    float rs = 0.f, tot = 0.f;
+    float4 xva[GPW * NT];
+    float rs[NT], tot[NT];
+#pragma unroll
+    for (int k = 0; k < NT; k++) rs[k] = tot[k] = 0.f;
     qh_u32x4 nv[GPW];
     load_x(0, xva);
     load_nw(nv);
@@ -613,29 +654,47 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
         __syncthreads();
     }
+    if constexpr (X1) {
+        // x fits one chunk: digitised once, before the loop, so its registers
+        // are free for the rest of the kernel
+        norm_x(xva, nv);
+#pragma unroll
+        for (int k = 0; k < NT; k++) rs[k] = prep_x(xva, k);
+    }
     int it = 0;
     auto body = [&](qh_u32x4* wr, float4* xv) -> bool {
         const int ch = item_ch(it);
-        if (X1 && it == 0) norm_x(xv, nv);
-        if (!X1 || it == 0) rs = prep_x(xv);
+        if constexpr (!X1) {
+#pragma unroll
+            for (int k = 0; k < NT; k++) rs[k] = prep_x(xv, k);
+        }
         stage(wr);
         const int ld = it + 1;  // the item these registers load next
         if (!X1) load_x(item_ch(ld), xv);
         load_w(item_tile(ld), item_ch(ld), wr);
-        tot += compute(rs);
+        {
+            float part[NT];
+            compute(rs, part);
+#pragma unroll
+            for (int k = 0; k < NT; k++) tot[k] += part[k];
+        }
         const int nt = item_tile(it + 1);
         if (ch == cpt - 1) {
             // Tile finished: sum the four lanes of each column into this
             // wavefront's slot; the sum over wavefronts waits for a full set.
-            float v = tot + bad;
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            if (lane < 16) red[((done % (2 * QH_RING)) * W + w) * 16 + lane] = v;
-            tot = 0.f;
+#pragma unroll
+            for (int k = 0; k < NT; k++) {
+                float v = tot[k] + bad[k];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                if (lane < 16) red[(((done % (2 * RING)) * NT + k) * W + w) * 16 + lane] = v;
+                tot[k] = 0.f;
+            }
             done++;
             if (done % ring == 0 && nt < ntiles) {
                 __syncthreads();
-                nsc = norm_scale();
+#pragma unroll
+                for (int k = 0; k < NT; k++) nsc[k] = norm_scale(k);
                 flush(done - ring, ring, false);
             }
         }
@@ -645,7 +704,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     while (body(wra, xva)) {
     }
     __syncthreads();
-    nsc = norm_scale();
+#pragma unroll
+    for (int k = 0; k < NT; k++) nsc[k] = norm_scale(k);
     const int last = done % ring ? done % ring : ring;
     if constexpr (PAIR) {
         // act = silu(gate) * up (qg_swiglu's expression) for every pair
@@ -662,14 +722,15 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     }
     // The last set goes straight to y; earlier sets wait in res.
     flush(done - last, last, true);
-    for (int i = threadIdx.x; i < (done - last) * 16; i += 64 * W) put(i >> 4, i & 15, res[i]);
+    for (int i = threadIdx.x; i < (done - last) * 16 * NT; i += 64 * W) put(i / (16 * NT), i & 15, res[i], (i >> 4) % NT);
 }
 
-template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false>
+template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false, int NT = 1>
 __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float* __restrict__ x, uint32_t row_bytes,
                                                    int ngroups) {
-    __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW>()];
-    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR>(mm, x, row_bytes, ngroups, lds, (int)blockIdx.x, (int)gridDim.x);
+    static_assert(qh_mmv16_lds<F, W, GPW, NT>() <= 163840, "LDS");
+    __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW, NT>()];
+    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, x, row_bytes, ngroups, lds, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
@@ -891,6 +952,99 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
             return qh_rows16_better(M16Q80::ROWS, total)
                        ? multi_mmv16<M16Q8016>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
                        : multi_mmv16<M16Q80>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        default: return hipErrorNotSupported;
+    }
+}
+
+// 2-4 tokens through the GEMV kernel: the tokens share every weight load, LDS
+// stage and B operand, and each token's arithmetic is the one-token kernel's,
+// so token t's result equals the GEMV of its x bit for bit.  NT = 2 or 4 (a
+// third token runs in a 4-token launch with the fourth masked).
+static bool qh_tokens_enabled() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_TOKENS");
+        return e ? atoi(e) : 1;
+    }();
+    return v != 0;
+}
+
+template <class F, int W, bool X1, int NT>
+static hipError_t launch_mmv16_tok(const QhMats& mm, const float* x, int in_dim, uint32_t row_bytes, hipStream_t st) {
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16<F, W, 1, X1, true, false, NT>, 64 * W, 0) !=
+                hipSuccess ||
+            per_cu < 1)
+            return hipErrorNotSupported;
+        resident = per_cu * prop.multiProcessorCount;
+    }
+    const int tiles = mm.tstart[QH_MULTI];
+    int grid = tiles < resident ? tiles : resident;
+    if ((tiles + grid - 1) / grid > qh_maxt<NT>()) grid = (tiles + qh_maxt<NT>() - 1) / qh_maxt<NT>();
+    hipLaunchKernelGGL((qh_mmv16<F, W, 1, X1, true, false, NT>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
+                       row_bytes, in_dim / 256);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, const int* outs, const int* ldys,
+                            const float* x, int ldx, int ntok, int in_dim, uint32_t row_bytes, int accum,
+                            hipStream_t st) {
+    QhMats mm;
+    int tiles = 0;
+    for (int k = 0; k < QH_MULTI; k++) {
+        const bool on = k < nm;
+        mm.w[k] = on ? Ws[k] : nullptr;
+        mm.y[k] = on ? ys[k] : nullptr;
+        mm.rows[k] = on ? outs[k] : 0;
+        mm.ldy[k] = on ? ldys[k] : 0;
+        mm.wbytes[k] = on ? (uint32_t)(((uint64_t)outs[k] * row_bytes + 3) & ~(uint64_t)3) : 0;
+        mm.tstart[k] = on ? tiles : INT_MAX;
+        if (on) tiles += (outs[k] + F::ROWS - 1) / F::ROWS;
+    }
+    mm.tstart[QH_MULTI] = tiles;
+    mm.nw = nullptr;
+    mm.accum = accum;
+    mm.ntok = ntok;
+    mm.ldx = ldx;
+    if (tiles == 0) return hipSuccess;
+    const bool x1 = in_dim <= 256 * 16;
+    if (ntok <= 2)
+        return x1 ? launch_mmv16_tok<F, 16, true, 2>(mm, x, in_dim, row_bytes, st)
+                  : launch_mmv16_tok<F, 8, false, 2>(mm, x, in_dim, row_bytes, st);
+    return x1 ? launch_mmv16_tok<F, 16, true, 4>(mm, x, in_dim, row_bytes, st)
+              : launch_mmv16_tok<F, 8, false, 4>(mm, x, in_dim, row_bytes, st);
+}
+
+// Y[m][t][:] (+)= W[m] x[t] for t < ntok (x token t at x + t ldx, y token t at
+// ys[m] + t ldys[m]), nm <= QH_MULTI matrices of one type sharing x.
+// hipErrorNotSupported when the shape or type has no such kernel.
+hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* Ws, float* const* ys, const int* outs,
+                                  const int* ldys, const float* x, int ldx, int ntok, int in_dim, int accum,
+                                  hipStream_t st) {
+    if (!qh_tokens_enabled() || ntok < 2 || ntok > 4 || nm < 1 || nm > QH_MULTI || in_dim % 256 ||
+        ((uintptr_t)x & 15u) || ldx % 4 || ldx < in_dim || (int64_t)ldx * (ntok - 1) + in_dim > ((int64_t)1 << 29))
+        return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    int total = 0;
+    for (int k = 0; k < nm; k++) {
+        if ((int64_t)outs[k] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+        total += outs[k];
+    }
+    switch (type) {
+        case QT_Q4_K:
+            return qh_rows16_better(M16Q4K::ROWS, total)
+                       ? tok_mmv16<M16Q4K16>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st)
+                       : tok_mmv16<M16Q4K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+        case QT_Q5_K: return tok_mmv16<M16Q5K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+        case QT_Q6_K: return tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+        case QT_Q8_0: return tok_mmv16<M16Q80>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+        case QT_IQ3_S: return tok_mmv16<M16IQ3S>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+        case QT_IQ2_XXS:
+            return tok_mmv16<M16IQ2XXS>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
         default: return hipErrorNotSupported;
     }
 }

@@ -22,6 +22,15 @@ def oracle():
 
 @pytest.fixture(scope="session")
 def qh():
-    """The HIP library; GPU tests fail (not skip) when it is missing."""
+    """The HIP library; GPU tests fail (not skip) when it is missing.  torch's
+    wheel bundles its own HIP runtime (a second copy beside /opt/rocm's, which
+    the library links): when a process uses both, torch must bring the GPU up
+    first, so tests that mix them work whatever order they run in."""
+    try:
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.init()
+    except ImportError:
+        pass
     from saient_quartz_amd import lib
     return lib()

@@ -326,3 +326,27 @@ def test_gemm_f32_router(qh, oracle, in_dim, out_dim, n, off):
     torch.cuda.synchronize()
     ref = oracle.gemm(0, x, w.view(np.uint8).reshape(-1), in_dim, out_dim, n)
     assert cf.rel_l2(Y.cpu().numpy(), ref) < 1e-5  # two f32 summation orders over up to 4096 terms
+
+
+@pytest.mark.parametrize("t", [12, 13, 14, 8, 21, 16])
+@pytest.mark.parametrize("n", [2, 3, 4])
+@pytest.mark.parametrize("out_dim, in_dim", [(300, 4096), (77, 14336), (4100, 512)])
+def test_gemm_few_tokens_equal_gemv(qh, oracle, t, n, out_dim, in_dim):
+    """2-4 tokens run through the GEMV kernel with shared weight loads: each
+    token's row is the one-token GEMV of that token, bit for bit, and within
+    the GEMV bar of the oracle (x 16-byte aligned, so both take the matrix-core
+    kernels)."""
+    data = synth.weights(t, out_dim, in_dim, seed=40 + t + n)
+    x = synth.activations(n, in_dim, seed=41 + n)
+    x[n - 1] *= 1e-4  # tokens of very different magnitudes keep their own exponents
+    got = gpu_gemm(qh, t, x, data, in_dim, out_dim, n)
+    w = GpuBuf.upload(data)
+    for k in range(n):
+        dx = GpuBuf.upload_f32(np.ascontiguousarray(x[k]))
+        dy = GpuBuf.alloc_f32(out_dim)
+        check("hip_gemv", qh.hip_gemv(t, w.ptr, dx.ptr, dy.ptr, in_dim, out_dim))
+        one = dy.download(np.float32)[:out_dim]
+        assert np.array_equal(got[k].view(np.uint32), one.view(np.uint32)), (k, np.argwhere(got[k] != one)[:4])
+    ref = oracle.gemm(t, x, data, in_dim, out_dim, n)
+    for k in range(n):
+        assert cf.rel_l2(got[k], ref[k]) < TOL
