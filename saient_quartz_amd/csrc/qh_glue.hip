@@ -276,7 +276,8 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int h0 = (g * n_heads + n_kv - 1) / n_kv, h1 = ((g + 1) * n_heads + n_kv - 1) / n_kv, ng = h1 - h0;
-    const int seq = pos + 1, half = hd >> 1, kp = hd + 4;
+    const int seq = pos + 1, half = hd >> 1;
+    constexpr int kp = HD + 4;  // LDS row strides of K (padded) and V: the template capacity
     const bool owner = ((pos / QA_ROWS) % nch) == c;
     const float* kh = k + (size_t)g * hd;
     const float* vh = v + (size_t)g * hd;
@@ -312,24 +313,38 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         for (int d = 0; d < HD / 64; d++) o[a][d] = 0.f;
     }
     const int t_l = lane & 31, hsel = lane >> 5;
+    // K and V rows of a slice: every thread's loads are issued before any is
+    // stored, and the next slice's are in flight while this one is computed.
+    constexpr int IT = QA_ROWS * (HD / 4) / 256;  // float4 per thread and slice
+    const int q4 = hd >> 2;
+    typedef float f4 __attribute__((ext_vector_type(4)));  // a native vector: promoted to registers
+    f4 kk[IT], vv[IT];
+    // Thread i of the slice covers row i / (HD/4), column chunk i % (HD/4).
+    // Rows past the slice (or the sequence) read row pos again and columns past
+    // hd a valid column; the compute reads neither, so loads and stores carry
+    // no branches and stay in registers.
+    auto fetch = [&](int sl) {
+#pragma unroll
+        for (int u = 0; u < IT; u++) {
+            const int i = threadIdx.x + 256 * u, r = i / (HD / 4), c4 = min(i % (HD / 4), q4 - 1);
+            const int t = min(sl * QA_ROWS + r, pos);
+            kk[u] = *reinterpret_cast<const f4*>(kc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
+            vv[u] = *reinterpret_cast<const f4*>(vc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
+        }
+    };
+    // the owner's row pos is in the cache before anyone of its workgroup reads it
+    __syncthreads();
+    fetch(c);
     for (int sl = c; sl * QA_ROWS < seq; sl += nch) {
         const int t0 = sl * QA_ROWS, nv = min(QA_ROWS, seq - t0);
-        // K and V rows t0 .. t0 + nv - 1 into LDS (row pos from kr / v)
-        const int q4 = hd >> 2;
-        for (int i = threadIdx.x; i < nv * q4; i += 256) {
-            const int r = i / q4, c4 = i - r * q4, t = t0 + r;
-            float4 kk, vv;
-            if (t < pos) {
-                kk = *reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
-                vv = *reinterpret_cast<const float4*>(vc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
-            } else {
-                kk = *reinterpret_cast<const float4*>(kr + 4 * c4);
-                vv = float4{vh[4 * c4], vh[4 * c4 + 1], vh[4 * c4 + 2], vh[4 * c4 + 3]};
-            }
-            *reinterpret_cast<float4*>(kl + r * kp + 4 * c4) = kk;
-            *reinterpret_cast<float4*>(vl + r * hd + 4 * c4) = vv;
+#pragma unroll
+        for (int u = 0; u < IT; u++) {
+            const int i = threadIdx.x + 256 * u, r = i / (HD / 4), c4 = i % (HD / 4);
+            *reinterpret_cast<f4*>(kl + r * kp + 4 * c4) = kk[u];
+            *reinterpret_cast<f4*>(vl + r * HD + 4 * c4) = vv[u];
         }
         __syncthreads();
+        fetch(sl + nch);
 #pragma unroll
         for (int a = 0; a < QA_MAXG / 4; a++) {
             const int j = w + 4 * a;
@@ -358,12 +373,15 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             m[a] = mn;
 #pragma unroll
             for (int d = 0; d < HD / 64; d++) o[a][d] *= corr;
+            // p of row t sits in lane t: a scalar read of a uniform lane, not a
+            // cross-lane LDS permute per row
+#pragma unroll 8
             for (int t = 0; t < nv; t++) {
-                const float pt = __shfl(p, t);
+                const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), t));
 #pragma unroll
                 for (int d = 0; d < HD / 64; d++) {
                     const int dd = lane + 64 * d;
-                    if (dd < hd) o[a][d] = fmaf(pt, vl[t * hd + dd], o[a][d]);
+                    if (dd < hd) o[a][d] = fmaf(pt, vl[t * HD + dd], o[a][d]);
                 }
             }
         }
@@ -583,7 +601,12 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
     const QaScratch* sc = qa_scratch_ptrs();
     if (!sc) return hipErrorInvalidDevice;
     const int slices = (pos + QA_ROWS) / QA_ROWS;
-    int nch = slices < QA_MAXCH ? slices : QA_MAXCH;
+    static const int per = [] {
+        const char* e = getenv("QUARTZ_HIP_ATTN_SLICES");
+        return e && atoi(e) > 0 ? atoi(e) : 1;
+    }();
+    int nch = (slices + per - 1) / per;
+    nch = nch < QA_MAXCH ? nch : QA_MAXCH;
     const int cap = QA_PART / (n_seq * n_heads * (hd + 2));
     if (nch > cap) nch = cap;
     if (nch < 1) return hipErrorNotSupported;
