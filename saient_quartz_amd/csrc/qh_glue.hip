@@ -250,7 +250,9 @@ __global__ __launch_bounds__(256) void qg_attention_decode(float* out, const flo
 static __device__ __align__(256) float qa_part[QA_PART];
 static __device__ __align__(256) unsigned int qa_cnt[QA_MAXKV];
 
-template <int HD>  // head_dim capacity: 128 or QA_MAXHD (LDS, so occupancy, scales with it)
+// HD: head_dim capacity, 128 or QA_MAXHD (LDS, so occupancy, scales with it);
+// GW: q heads per wavefront (1, 2 or 4: groups of up to 4, 8 or QA_MAXG heads).
+template <int HD, int GW>
 __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float* q, const float* k, const float* v,
                                                          float* kc, float* vc, const float* sinks, int n_heads,
                                                          int n_kv, int hd, int kv_dim, int pos, float theta,
@@ -281,13 +283,17 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     const bool owner = ((pos / QA_ROWS) % nch) == c;
     const float* kh = k + (size_t)g * hd;
     const float* vh = v + (size_t)g * hd;
+    // q rows at stride HD, zero past hd: the score dot runs over HD (a constant)
+    if (hd < HD)
+        for (int p = threadIdx.x; p < ng * HD; p += 256)
+            if (p % HD >= hd) qr[p] = 0.f;
     for (int p = threadIdx.x; p < ng * half; p += 256) {
         const int j = p / half, i = p - j * half;
         const QgRot r = qg_rope_rot(i, hd, pos, theta, yarn_scale, orig_ctx, neox);
         const float* qh = q + (size_t)(h0 + j) * hd;
         const float q0 = qh[r.i0], q1 = qh[r.i1];
-        qr[j * hd + r.i0] = q0 * r.c - q1 * r.s;
-        qr[j * hd + r.i1] = q0 * r.s + q1 * r.c;
+        qr[j * HD + r.i0] = q0 * r.c - q1 * r.s;
+        qr[j * HD + r.i1] = q0 * r.s + q1 * r.c;
         if (owner && j == 0) {
             const float k0 = kh[r.i0], k1 = kh[r.i1];
             kr[r.i0] = k0 * r.c - k1 * r.s;
@@ -304,9 +310,9 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         }
     }
     // running state of this wavefront's heads j = w, w + 4, ... (< ng)
-    float m[QA_MAXG / 4], l[QA_MAXG / 4], o[QA_MAXG / 4][HD / 64];
+    float m[GW], l[GW], o[GW][HD / 64];
 #pragma unroll
-    for (int a = 0; a < QA_MAXG / 4; a++) {
+    for (int a = 0; a < GW; a++) {
         m[a] = -1e30f;
         l[a] = 0.f;
 #pragma unroll
@@ -346,14 +352,16 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         __syncthreads();
         fetch(sl + nch);
 #pragma unroll
-        for (int a = 0; a < QA_MAXG / 4; a++) {
+        for (int a = 0; a < GW; a++) {
             const int j = w + 4 * a;
             if (j >= ng) break;  // uniform per wavefront
-            // score of row t_l: half hsel of the dot, then the two halves summed
-            const float* qj = qr + j * hd + hsel * half;
-            const float* kt = kl + t_l * kp + hsel * half;
+            // score of row t_l: half hsel of the dot (HD / 2 terms, the ones past hd
+            // zero), then the two halves summed
+            const float* qj = qr + j * HD + hsel * (HD / 2);
+            const float* kt = kl + t_l * kp + hsel * (HD / 2);
             float sdot = 0.f;
-            for (int i = 0; i < half; i += 4) {
+#pragma unroll
+            for (int i = 0; i < HD / 2; i += 4) {
                 const float4 kk = *reinterpret_cast<const float4*>(kt + i);
                 const float4 qq = *reinterpret_cast<const float4*>(qj + i);
                 sdot += (qq.x * kk.x + qq.y * kk.y) + (qq.z * kk.z + qq.w * kk.w);
@@ -373,15 +381,21 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             m[a] = mn;
 #pragma unroll
             for (int d = 0; d < HD / 64; d++) o[a][d] *= corr;
-            // p of row t sits in lane t: a scalar read of a uniform lane, not a
-            // cross-lane LDS permute per row
-#pragma unroll 8
-            for (int t = 0; t < nv; t++) {
-                const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), t));
+            // o += p_t v_t over the slice's rows in order (p is 0 past nv), eight
+            // rows' V loads in flight at a time; p of row t sits in lane t and is
+            // read as a scalar
 #pragma unroll
-                for (int d = 0; d < HD / 64; d++) {
-                    const int dd = lane + 64 * d;
-                    if (dd < hd) o[a][d] = fmaf(pt, vl[t * HD + dd], o[a][d]);
+            for (int t0 = 0; t0 < QA_ROWS; t0 += 8) {
+                float vb[8][HD / 64];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int d = 0; d < HD / 64; d++) vb[u][d] = vl[(t0 + u) * HD + lane + 64 * d];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), t0 + u));
+#pragma unroll
+                    for (int d = 0; d < HD / 64; d++) o[a][d] = fmaf(pt, vb[u][d], o[a][d]);
                 }
             }
         }
@@ -403,7 +417,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     };
     if (nch == 1) {
 #pragma unroll
-        for (int a = 0; a < QA_MAXG / 4; a++) {
+        for (int a = 0; a < GW; a++) {
             const int j = w + 4 * a;
             if (j >= ng) break;
             finish(j, m[a], l[a], o[a], false);
@@ -413,7 +427,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     // partial record of (head h, slice c): [m, l, o[0 .. hd)]
     const int rec = hd + 2;
 #pragma unroll
-    for (int a = 0; a < QA_MAXG / 4; a++) {
+    for (int a = 0; a < GW; a++) {
         const int j = w + 4 * a;
         if (j >= ng) break;
         float* pr = part + ((size_t)(h0 + j) * nch + c) * rec;
@@ -601,23 +615,40 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
     const QaScratch* sc = qa_scratch_ptrs();
     if (!sc) return hipErrorInvalidDevice;
     const int slices = (pos + QA_ROWS) / QA_ROWS;
-    static const int per = [] {
+    // 32-row slices per workgroup: more workgroups until the merge of their
+    // partials costs more than the slices they take over (measured on MI355X:
+    // 1 up to 16 slices, 2 up to 64, then 4).  QUARTZ_HIP_ATTN_SLICES=k forces k.
+    static const int env_per = [] {
         const char* e = getenv("QUARTZ_HIP_ATTN_SLICES");
-        return e && atoi(e) > 0 ? atoi(e) : 1;
+        return e && atoi(e) > 0 ? atoi(e) : 0;
     }();
+    const int per = env_per ? env_per : (slices <= 16 ? 1 : (slices <= 64 ? 2 : 4));
     int nch = (slices + per - 1) / per;
     nch = nch < QA_MAXCH ? nch : QA_MAXCH;
     const int cap = QA_PART / (n_seq * n_heads * (hd + 2));
     if (nch > cap) nch = cap;
     if (nch < 1) return hipErrorNotSupported;
-    if (hd <= 128)
-        hipLaunchKernelGGL(qg_attention_step<128>, dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc, vc,
+    const int gmax = (n_heads + n_kv - 1) / n_kv;
+    auto launch = [&](auto HDC, auto GWC) {
+        constexpr int H = decltype(HDC)::value, G = decltype(GWC)::value;
+        hipLaunchKernelGGL((qg_attention_step<H, G>), dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc, vc,
                            sinks, n_heads, n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale, sc->part,
                            sc->cnt, cache_stride);
-    else
-        hipLaunchKernelGGL(qg_attention_step<QA_MAXHD>, dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc,
-                           vc, sinks, n_heads, n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale,
-                           sc->part, sc->cnt, cache_stride);
+    };
+    using I128 = std::integral_constant<int, 128>;
+    using IMAX = std::integral_constant<int, QA_MAXHD>;
+    using G1 = std::integral_constant<int, 1>;
+    using G2 = std::integral_constant<int, 2>;
+    using G4 = std::integral_constant<int, QA_MAXG / 4>;
+    if (hd <= 128) {
+        if (gmax <= 4) launch(I128{}, G1{});
+        else if (gmax <= 8) launch(I128{}, G2{});
+        else launch(I128{}, G4{});
+    } else {
+        if (gmax <= 4) launch(IMAX{}, G1{});
+        else if (gmax <= 8) launch(IMAX{}, G2{});
+        else launch(IMAX{}, G4{});
+    }
     return hipGetLastError();
 }
 
