@@ -119,6 +119,18 @@ int hip_gemm_grouped_ex_async(uint32_t ggml_type, int count, const uint8_t* cons
                               const float* const* x_up, float* const* y, const int* n, const int* out_dims,
                               int in_dim, int accumulate, float* scratch, void* stream);
 
+/* y[k][t][:] = W[k] (rms_norm(x[t]) * norm_w) for count matrices of one type
+ * sharing the n token rows of x (token-major, in_dim each): the RMS norm
+ * (eps 1e-5, cuda_rms_norm's formula, src/cuda_kernels.cu:563-575) fused into
+ * the GEMMs that read it, as forward_gpu_step's norm + q/k/v and norm +
+ * gate/up pairs (src/cuda.rs:549-562, :662-665, :773-788) for a batch.  The norm
+ * fuses into the GEMV kernel for n <= 4 tokens (n = 3, 4 on matrices up to
+ * 16 MB); otherwise the rows are normalised into scratch (n * in_dim floats)
+ * and then multiplied, and a null scratch returns QH_ERR_NULL. */
+int hip_gemm_grouped_norm_async(uint32_t ggml_type, int count, const uint8_t* const* d_data, const float* d_x,
+                                const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
+                                float* d_scratch, void* stream);
+
 /* Y[t][j] for t < rows with ggml-cuda's int8 MMQ rounding (Q4_K, Q6_K): the
  * GPU twin of the reference's CPU oracles gemm_q4k_q8_1_mmq / gemm_q6k_q8_1_mmq
  * and their _stream_k forms (src/dequant.rs:202-645), bit-exact to them: x is

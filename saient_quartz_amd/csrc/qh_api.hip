@@ -366,6 +366,55 @@ int hip_gemm_grouped_ex_async(uint32_t type, int count, const uint8_t* const* W,
     return QH_OK;
 }
 
+int hip_gemm_grouped_norm_async(uint32_t type, int count, const uint8_t* const* W, const float* x,
+                                const float* norm_w, float* const* y, int n, const int* out_dims, int in_dim,
+                                float* scratch, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 0 || n < 0) return QH_ERR_RANGE;
+    if (count == 0 || n == 0) return QH_OK;
+    if (!W || !x || !norm_w || !y || !out_dims) return QH_ERR_NULL;
+    if (in_dim <= 0) return QH_ERR_DIMS;
+    if (qh_block_elems(type) != 0) {
+        for (int k = 0; k < count; k++) {
+            int rc = qh_check_dims(type, in_dim, out_dims[k]);
+            if (rc) return rc;
+            if (out_dims[k] > 0 && (!W[k] || !y[k])) return QH_ERR_NULL;
+        }
+        if (!qh_force_valu() && count <= 16) {
+            hipError_t e = hipErrorNotSupported;
+            if (n == 1 && count <= 4)
+                e = qh_launch_mmv16_multi(type, W, y, out_dims, count, x, in_dim, st, norm_w, 0, false);
+            else if (n >= 2) {
+                const float* xs[16];
+                int ns[16];
+                for (int k = 0; k < count; k++) {
+                    xs[k] = x;
+                    ns[k] = n;
+                }
+                e = qh_launch_mmq_grouped(type, count, W, xs, y, ns, out_dims, in_dim, st, nullptr, 0, norm_w);
+            }
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_grouped_norm");
+        }
+    }
+    // the normalised rows into scratch (n in_dim floats), then one grouped call
+    // (matrices sharing x share its digitisation)
+    if (!scratch) return QH_ERR_NULL;
+    QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st, n), "hip_gemm_grouped_norm");
+    for (int k0 = 0; k0 < count; k0 += 16) {
+        const int cnt = count - k0 < 16 ? count - k0 : 16;
+        const float* xs[16];
+        int ns[16];
+        for (int k = 0; k < cnt; k++) {
+            xs[k] = scratch;
+            ns[k] = n;
+        }
+        int rc = hip_gemm_grouped_async(type, cnt, W + k0, xs, y + k0, ns, out_dims + k0, in_dim, stream);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
 int hip_gemm_q8_1_mmq_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                             int rows, int reference_rows, int multiprocessors, void* stream) {
     if (type != QT_Q4_K && type != QT_Q6_K) return QH_ERR_TYPE;

@@ -241,6 +241,7 @@ __global__ __launch_bounds__(256) void qh_mmq_ximg(const QgXs xs, unsigned char*
     img += (size_t)blockIdx.y * gridDim.x * XI::BYTES;
     const int t = T >> 4, p = T & 15;
     for (int i = 16 * T; i < XI::BYTES; i += 16 * 256) *reinterpret_cast<qh_u32x4*>(im + i) = qh_u32x4{0, 0, 0, 0};
+    __syncthreads();  // the zero fill lands before any thread's image writes
     float4 v[4];
     const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
     const uint32_t off = t < n ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)g + 16u * p) : 0x80000000u;
@@ -776,10 +777,11 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
 // streams) must be serialised by the caller.
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
                                  float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
-                                 const float* const* X2, int accum) {
+                                 const float* const* X2, int accum, const float* nw) {
     if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || count < 1) return hipErrorNotSupported;
-    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
-        return hipErrorNotSupported;
+    // an RMS norm fuses only into the 2-4 token GEMV path (the batched kernel's
+    // 15-bit x image measured less accurate with x * w digitised before the scale)
+    if (nw && X2) return hipErrorNotSupported;
     if (!X2 && count <= 4) {
         // 2-4 tokens of one x shared by up to 4 matrices: the GEMV kernel carries
         // the tokens (no x-image prologue, the weights read once)
@@ -791,10 +793,13 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
         for (int i = 0; i < count; i++) wbytes += (int64_t)qh_type_size(type, (size_t)in_dim) * (out_dims[i] > 0 ? out_dims[i] : 0);
         if (same && (n[0] == 2 || wbytes <= ((int64_t)16 << 20))) {
             hipError_t e = qh_launch_mmv16_tokens(type, count, W, Y, out_dims, out_dims, X[0], in_dim, n[0], in_dim,
-                                                  accum, st);
+                                                  accum, st, nw);
             if (e != hipErrorNotSupported) return e;
         }
     }
+    if (nw) return hipErrorNotSupported;  // the caller normalises first
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
+        return hipErrorNotSupported;
     const QgScratch* sc = qh_mmq_scratch_ptrs();
     if (!sc) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
@@ -843,5 +848,5 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
 hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim, int n,
                          hipStream_t st) {
     if (n < 2) return hipErrorNotSupported;
-    return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st, nullptr, 0);
+    return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st, nullptr, 0, nullptr);
 }

@@ -48,7 +48,7 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
                          int n, hipStream_t st);
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
                                  float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
-                                 const float* const* X2 = nullptr, int accum = 0);
+                                 const float* const* X2 = nullptr, int accum = 0, const float* nw = nullptr);
 hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm,
                                  const float* x, int in_dim, hipStream_t st, const float* norm_w, int accum,
                                  bool swiglu_pair = false);
@@ -57,7 +57,7 @@ hipError_t qh_launch_mmv16_mix(uint32_t t1, const uint8_t* const* Ws1, float* co
                                const float* x, int in_dim, const float* nw, int accum, hipStream_t st);
 hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* Ws, float* const* ys, const int* outs,
                                   const int* ldys, const float* x, int ldx, int ntok, int in_dim, int accum,
-                                  hipStream_t st);
+                                  hipStream_t st, const float* nw = nullptr);
 hipError_t qh_launch_mmq_q81(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                              int rows, int ref_rows, int mps, hipStream_t st);
 hipError_t qh_launch_mmv(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,

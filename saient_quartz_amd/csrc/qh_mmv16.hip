@@ -434,8 +434,11 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         for (int t = 0; t < GPW; t++)
 #pragma unroll
             for (int k = 0; k < NT; k++) {
-                const uint32_t o = k < ntok ? 1024u * (uint32_t)(g0 + t) + 16u * lane + (NT > 1 ? 4u * (uint32_t)(k * mm.ldx) : 0u)
-                                            : 0x80000000u;
+                // groups past in_dim read zeros too (with NT > 1 the buffer range
+                // runs on into the next token's row)
+                const uint32_t o = k < ntok && g0 + t < ngroups
+                                       ? 1024u * (uint32_t)(g0 + t) + 16u * lane + (NT > 1 ? 4u * (uint32_t)(k * mm.ldx) : 0u)
+                                       : 0x80000000u;
                 const qh_u32x4 v = qh_ld128(xb, o);
                 xo[t * NT + k] =
                     float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
@@ -948,6 +951,8 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
                        ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
                        : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_IQ3_S: return multi_mmv16<M16IQ3S>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_IQ2_XXS: return multi_mmv16<M16IQ2XXS>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q8_0:
             return qh_rows16_better(M16Q80::ROWS, total)
                        ? multi_mmv16<M16Q8016>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
@@ -992,7 +997,7 @@ static hipError_t launch_mmv16_tok(const QhMats& mm, const float* x, int in_dim,
 template <class F>
 static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, const int* outs, const int* ldys,
                             const float* x, int ldx, int ntok, int in_dim, uint32_t row_bytes, int accum,
-                            hipStream_t st) {
+                            const float* nw, hipStream_t st) {
     QhMats mm;
     int tiles = 0;
     for (int k = 0; k < QH_MULTI; k++) {
@@ -1006,7 +1011,7 @@ static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, 
         if (on) tiles += (outs[k] + F::ROWS - 1) / F::ROWS;
     }
     mm.tstart[QH_MULTI] = tiles;
-    mm.nw = nullptr;
+    mm.nw = nw;
     mm.accum = accum;
     mm.ntok = ntok;
     mm.ldx = ldx;
@@ -1024,7 +1029,9 @@ static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, 
 // hipErrorNotSupported when the shape or type has no such kernel.
 hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* Ws, float* const* ys, const int* outs,
                                   const int* ldys, const float* x, int ldx, int ntok, int in_dim, int accum,
-                                  hipStream_t st) {
+                                  hipStream_t st, const float* nw) {
+    // the fused RMS norm needs a token's whole x in one workgroup (one K chunk)
+    if (nw && in_dim > 256 * 16) return hipErrorNotSupported;
     if (!qh_tokens_enabled() || ntok < 2 || ntok > 4 || nm < 1 || nm > QH_MULTI || in_dim % 256 ||
         ((uintptr_t)x & 15u) || ldx % 4 || ldx < in_dim || (int64_t)ldx * (ntok - 1) + in_dim > ((int64_t)1 << 29))
         return hipErrorNotSupported;
@@ -1037,14 +1044,14 @@ hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* W
     switch (type) {
         case QT_Q4_K:
             return qh_rows16_better(M16Q4K::ROWS, total)
-                       ? tok_mmv16<M16Q4K16>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st)
-                       : tok_mmv16<M16Q4K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
-        case QT_Q5_K: return tok_mmv16<M16Q5K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
-        case QT_Q6_K: return tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
-        case QT_Q8_0: return tok_mmv16<M16Q80>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
-        case QT_IQ3_S: return tok_mmv16<M16IQ3S>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+                       ? tok_mmv16<M16Q4K16>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st)
+                       : tok_mmv16<M16Q4K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q5_K: return tok_mmv16<M16Q5K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q6_K: return tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q8_0: return tok_mmv16<M16Q80>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_IQ3_S: return tok_mmv16<M16IQ3S>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_IQ2_XXS:
-            return tok_mmv16<M16IQ2XXS>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, st);
+            return tok_mmv16<M16IQ2XXS>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         default: return hipErrorNotSupported;
     }
 }

@@ -23,7 +23,8 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import gemm_grouped_async, gemm_grouped_ex_async, gemm_moe_async, gemv_group_async, gemv_multi_async
+from .host import (gemm_grouped_async, gemm_grouped_ex_async, gemm_grouped_norm_async, gemm_moe_async,
+                   gemv_group_async, gemv_multi_async)
 
 Q4_K, Q6_K = 12, 14
 
@@ -402,7 +403,7 @@ class BatchStep:
         qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
         f32 = dict(device="cuda", dtype=torch.float32)
         z = lambda d: torch.zeros(n, d, **f32)
-        self.hidden, self.xn, self.tmp = z(c.hidden), z(c.hidden), z(c.hidden)
+        self.hidden, self.xn = z(c.hidden), z(c.hidden)
         self.q, self.k, self.v, self.att = z(qd), z(kvd), z(kvd), z(qd)
         self.gate, self.up, self.act = z(c.ffn), z(c.ffn), z(c.ffn)
         self.logits = z(c.vocab)
@@ -432,6 +433,24 @@ class BatchStep:
             gemm_grouped_async(self.L, t, ws, [x.data_ptr()] * len(group), [y.data_ptr() for _, y in group],
                                [self.n] * len(group), [y.shape[1] for _, y in group], in_dim, sp)
 
+    def _gemm_norm(self, names, layer, norm, ys, sp):
+        """y = W rms_norm(hidden) * norm for the matrices `names`.  Up to 4 tokens:
+        the norm fused into the GEMMs (one hip_gemm_grouped_norm call per weight
+        type); more: one hip_rms_norm_rows shared by every type's GEMMs."""
+        if self.n > 4:
+            check("hip_rms_norm_rows_async", self.L.hip_rms_norm_rows_async(
+                self.xn.data_ptr(), self.hidden.data_ptr(), norm.data_ptr(), self.n, self.cfg.hidden, sp))
+            self._gemm(names, layer, self.xn, ys, self.cfg.hidden, sp)
+            return
+        by_type = {}
+        for nm, y in zip(names, ys):
+            by_type.setdefault(self.cfg.type_of(nm), []).append((nm, y))
+        for t, group in by_type.items():
+            ws = [(self.w[nm][layer] if layer is not None else self.w[nm]).data_ptr() for nm, _ in group]
+            gemm_grouped_norm_async(self.L, t, ws, self.hidden.data_ptr(), norm.data_ptr(),
+                                    [y.data_ptr() for _, y in group], self.n, [y.shape[1] for _, y in group],
+                                    self.cfg.hidden, sp, self.scratch.data_ptr())
+
     def issue(self, tokens, pos: int, stream=None, logits: bool = True):
         """Enqueue one lockstep decode step: sequence i takes tokens[i] at `pos`."""
         c, L, n = self.cfg, self.L, self.n
@@ -444,19 +463,13 @@ class BatchStep:
                 self.hidden.data_ptr() + 4 * i * row, self.w["embed"].data_ptr(), c.type_of("embed"), int(t),
                 c.hidden, sp))
         for l in range(c.layers):
-            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
-                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["attn_norm"][l].data_ptr(), n, c.hidden, sp))
-            self._gemm(("q", "k", "v"), l, self.xn, (self.q, self.k, self.v), c.hidden, sp)
+            self._gemm_norm(("q", "k", "v"), l, self.w["attn_norm"][l], (self.q, self.k, self.v), sp)
             check("hip_attention_step_batched_async", L.hip_attention_step_batched_async(
                 self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
                 self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta,
                 1.0, 0, c.neox, self.scale, sp))
             self._gemm_res("o", l, self.att, c.n_heads * c.head_dim, sp)
-            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
-                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["ffn_norm"][l].data_ptr(), n, c.hidden, sp))
-            self._gemm(("gate", "up"), l, self.xn, (self.gate, self.up), c.hidden, sp)
+            self._gemm_norm(("gate", "up"), l, self.w["ffn_norm"][l], (self.gate, self.up), sp)
             self._gemm_res("down", l, self.gate, c.ffn, sp, up=self.up)
         if logits:
-            check("hip_rms_norm_rows_async", L.hip_rms_norm_rows_async(
-                self.xn.data_ptr(), self.hidden.data_ptr(), self.w["out_norm"].data_ptr(), n, c.hidden, sp))
-            self._gemm(("head",), None, self.xn, (self.logits,), c.hidden, sp)
+            self._gemm_norm(("head",), None, self.w["out_norm"], (self.logits,), sp)

@@ -350,3 +350,34 @@ def test_gemm_few_tokens_equal_gemv(qh, oracle, t, n, out_dim, in_dim):
     ref = oracle.gemm(t, x, data, in_dim, out_dim, n)
     for k in range(n):
         assert cf.rel_l2(got[k], ref[k]) < TOL
+
+
+@pytest.mark.parametrize("t", [12, 14, 13, 21])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16, 20])
+@pytest.mark.parametrize("in_dim", [2048, 768])
+def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
+    """y[k] = W[k] (rms_norm(x) * w) with the norm fused into the GEMMs (the
+    one-token GEMV, the 2-4 token GEMV, the batched kernel's x prologue) against
+    the oracle on the normalised rows, computed in float64."""
+    import ctypes as C
+    outs = [300, 77]
+    rng = np.random.default_rng(n + t)
+    x = (rng.standard_normal((n, in_dim)) * rng.uniform(0.1, 10, (n, 1))).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    datas = [synth.weights(t, o, in_dim, seed=o + n) for o in outs]
+    dw = [GpuBuf.upload(d) for d in datas]
+    dx, dn = GpuBuf.upload_f32(x.reshape(-1)), GpuBuf.upload_f32(w)
+    dy = [GpuBuf.alloc_f32(n * o) for o in outs]
+    scratch = GpuBuf.alloc_f32(n * in_dim)
+    k = len(outs)
+    check("hip_gemm_grouped_norm_async", qh.hip_gemm_grouped_norm_async(
+        t, k, (C.c_void_p * k)(*[b.ptr for b in dw]), dx.ptr, dn.ptr, (C.c_void_p * k)(*[b.ptr for b in dy]), n,
+        (C.c_int * k)(*outs), in_dim, scratch.ptr, None))
+    check("hip_sync", qh.hip_sync())
+    xd = x.astype(np.float64)
+    xn = (xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5) * w).astype(np.float32)
+    for b, d, o in zip(dy, datas, outs):
+        got = b.download(np.float32)[:n * o].reshape(n, o)
+        ref = oracle.gemm(t, xn, d, in_dim, o, n)
+        for r in range(n):
+            assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
