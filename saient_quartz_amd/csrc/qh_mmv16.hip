@@ -273,6 +273,70 @@ struct M16IQ2XXS {
     static QH_DEV int mn(const H&, int) { return 0; }
 };
 
+// The 32-element block formats (src/dequant.rs:1381-1443 Q5_0/Q5_1, :1527-1574
+// IQ4_NL; Q4_0/Q4_1 by the public GGUF layout): a group is 8 blocks (16-byte
+// aligned in a row when in_dim % 256 == 0).  Piece p = half p % 2 of block
+// p / 2, 16 quants as the int8 B operand with the block's own f32 scale d
+// (FLOAT_D); the offset of Q4_0 / Q5_0 (-8 / -16) and IQ4_NL's codebook go into
+// the bytes, the minimum m of Q4_1 / Q5_1 through the piece's x sum.
+// Dispatched for Q4_1 and Q5_1 only: their quants sit 4- and 8-byte aligned in
+// the staged line; the 18- and 22-byte blocks of Q4_0, IQ4_NL and Q5_0 leave
+// them 2-byte aligned, and those measured no faster (Q5_0: 23.4 against 15.1 us
+// at 14336x4096) than the VALU kernel, which keeps them.
+template <int KIND>  // 0 Q4_0, 1 Q4_1, 2 Q5_0, 3 Q5_1, 4 IQ4_NL
+struct M16Blk {
+    static constexpr int BB = (KIND == 0 || KIND == 4) ? 18 : (KIND == 1 ? 20 : (KIND == 2 ? 22 : 24));
+    static constexpr int QS = (KIND == 0 || KIND == 4) ? 2 : (KIND == 1 ? 4 : (KIND == 2 ? 6 : 8));  // quants
+    static constexpr int BYTES = 8 * BB, CH = BYTES / 16, ROWS = 128 / CH, LAST = BYTES - 16, RS = QH_RS;
+    static constexpr bool FLOAT_D = true, MINS = KIND == 1 || KIND == 3;
+    static constexpr int GRID = 0;
+    struct H { float d[4], m[4]; float dm; };
+    template <int S>
+    static QH_DEV int piece(int kg) { return 4 * S + kg; }
+    static QH_DEV H hdr(const unsigned char* r, int kg) {
+        H o;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int blk = (4 * s + kg) >> 1;
+            o.d[s] = qh_h2f(*reinterpret_cast<const uint16_t*>(r + BB * blk));
+            o.m[s] = MINS ? qh_h2f(*reinterpret_cast<const uint16_t*>(r + BB * blk + 2)) : 0.f;
+        }
+        o.dm = 0.f;
+        return o;
+    }
+    static QH_DEV void bops(const unsigned char* r, int kg, const H&, qh_i32x4* B, const unsigned char*) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int p = 4 * s + kg, blk = p >> 1, half = p & 1;
+            uint32_t w[4];
+            __builtin_memcpy(w, r + BB * blk + QS, 16);
+            uint32_t hb = 0;
+            if constexpr (KIND == 2 || KIND == 3) {
+                uint32_t qh;
+                __builtin_memcpy(&qh, r + BB * blk + QS - 4, 4);
+                hb = half ? qh >> 16 : qh & 0xFFFFu;  // bit j: weight j of the piece
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t q = half ? (w[i] >> 4) & 0x0F0F0F0Fu : w[i] & 0x0F0F0F0Fu;
+                if constexpr (KIND == 2 || KIND == 3) q |= qh_spread4((hb >> (4 * i)) & 0xFu) << 4;
+                if constexpr (KIND == 0) q = (q + 0x78787878u) ^ 0x80808080u;  // q - 8 as int8 (no carries)
+                if constexpr (KIND == 2) q = (q + 0x70707070u) ^ 0x80808080u;  // q - 16
+                if constexpr (KIND == 4) q = qh_iq4nl_lut(q) ^ 0x80808080u;    // T[q] (T + 128 flipped)
+                B[s][i] = (int)q;
+            }
+        }
+    }
+    template <int S>
+    static QH_DEV int scl(const H&, int) { return 1; }
+    template <int S>
+    static QH_DEV int mn(const H&, int) { return 0; }
+    template <int S>
+    static QH_DEV float dsc(const H& h) { return h.d[S]; }
+    template <int S>
+    static QH_DEV float mnf(const H& h) { return -h.m[S]; }  // enters as -(-m) * sum(x)
+};
+
 // 16-row tiles of the same formats (3 loads per lane and group instead of 2):
 // chosen when they spread the tiles more evenly over the CUs (4096 rows = 256
 // tiles = one per CU).
@@ -571,6 +635,10 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                         // each piece has its own f32 scale (the digit dots are exact in f32)
                         const float P = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
                         acc[k] = fmaf(F::template dsc<S>(hd), P, acc[k]);
+                        if constexpr (F::MINS) {
+                            const float xs = *reinterpret_cast<const float*>(xt + xsoff[S]);
+                            fm = fmaf(F::template mnf<S>(hd), xs, fm);
+                        }
                     } else {
                         const int sc = F::template scl<S>(hd, kg);
                         i0 += __mul24(sc, D[0]);
@@ -591,6 +659,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
                     const float P = fmaf((float)i2, 65536.0f, fmaf((float)i1, 256.0f, (float)i0));
                     acc[k] = fmaf(hd.d, P, acc[k]);
                     if constexpr (F::MINS) accm[k] = fmaf(hd.dm, fm, accm[k]);
+                } else if constexpr (F::MINS) {
+                    accm[k] += fm;
                 }
             }
         }
@@ -896,6 +966,8 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
                        : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_IQ3_S: return dispatch_mmv16<M16IQ3S>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q4_1: return dispatch_mmv16<M16Blk<1>>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q5_1: return dispatch_mmv16<M16Blk<3>>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_IQ2_XXS: return dispatch_mmv16<M16IQ2XXS>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q8_0:
             return qh_rows16_better(M16Q80::ROWS, out_dim)
@@ -952,6 +1024,8 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
                        : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_IQ3_S: return multi_mmv16<M16IQ3S>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_Q4_1: return multi_mmv16<M16Blk<1>>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_Q5_1: return multi_mmv16<M16Blk<3>>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_IQ2_XXS: return multi_mmv16<M16IQ2XXS>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q8_0:
             return qh_rows16_better(M16Q80::ROWS, total)
@@ -1050,6 +1124,8 @@ hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* W
         case QT_Q6_K: return tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_Q8_0: return tok_mmv16<M16Q80>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_IQ3_S: return tok_mmv16<M16IQ3S>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q4_1: return tok_mmv16<M16Blk<1>>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q5_1: return tok_mmv16<M16Blk<3>>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_IQ2_XXS:
             return tok_mmv16<M16IQ2XXS>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         default: return hipErrorNotSupported;

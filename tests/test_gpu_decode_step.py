@@ -28,9 +28,11 @@ Q4_K, Q6_K, Q8_0, Q5_K = 12, 14, 8, 13
 LLAMA_TYPES = (("q", Q4_K), ("k", Q4_K), ("v", Q6_K), ("o", Q4_K), ("gate", Q4_K), ("up", Q4_K),
                ("down", Q6_K), ("head", Q6_K), ("embed", Q4_K))
 Q8_TYPES = tuple((n, Q8_0) for n, _ in LLAMA_TYPES)
-# no fused kernel for Q5_0: every GEMV takes the separate-kernel fallback through the scratch buffer
 Q5_0 = 6
 Q50_TYPES = tuple((n, Q5_0) for n, _ in LLAMA_TYPES)
+# no fused kernel for Q2_K: every GEMV takes the separate-kernel fallback through the scratch buffer
+Q2_K = 10
+Q2K_TYPES = tuple((n, Q2_K) for n, _ in LLAMA_TYPES)
 MIXED_TYPES = (("q", Q5_K), ("k", Q4_K), ("v", Q8_0), ("o", Q6_K), ("gate", Q4_K), ("up", Q5_K),
                ("down", Q4_K), ("head", Q4_K), ("embed", Q6_K))
 
@@ -67,7 +69,8 @@ def host_model(cfg, seed, realistic=False):
 # follow BASELINE.json's distributions, whose weights are O(1), so a model built
 # from them grows its residual stream ~100x per layer; dividing every scale by 64
 # gives weights of a real checkpoint's size (~0.02) and O(1) activations.
-_D_FIELDS = {12: (144, (0, 2)), 13: (176, (0, 2)), 14: (210, (208,)), 8: (34, (0,)), 6: (22, (0,))}
+_D_FIELDS = {12: (144, (0, 2)), 13: (176, (0, 2)), 14: (210, (208,)), 8: (34, (0,)), 6: (22, (0,)),
+             10: (84, (80, 82))}
 
 
 def realistic_scale(data, t):
@@ -101,7 +104,8 @@ def oracle_model(oracle, cfg, raw, norms):
 CASES = {
     "llama_q4km": dict(types=LLAMA_TYPES),
     "q8_0": dict(types=Q8_TYPES),
-    "q5_0_fallback": dict(types=Q50_TYPES),
+    "q5_0": dict(types=Q50_TYPES),
+    "q2_k_fallback": dict(types=Q2K_TYPES),
     "mixed": dict(types=MIXED_TYPES),
     # norm x past one workgroup's chunk (hidden > 4096): the unfused norm path for q/k/v/gate/up/head
     "wide": dict(types=LLAMA_TYPES, hidden=4352, n_heads=2, n_kv=1, ffn=512, vocab=64, layers=1),
@@ -161,12 +165,14 @@ SYM_TYPES = (("q", Q6_K), ("k", Q8_0), ("v", Q6_K), ("o", Q8_0), ("gate", Q6_K),
 BATCH_CASES = {
     "llama_q4km_1layer": dict(types=LLAMA_TYPES, layers=1),
     "sym_2layers": dict(types=SYM_TYPES, layers=2),
-    "q5_0_fallback": dict(types=Q50_TYPES, layers=1),
+    "q5_0": dict(types=Q50_TYPES, layers=1),
+    "q2_k_fallback": dict(types=Q2K_TYPES, layers=1),
 }
 
 
 @pytest.mark.parametrize("n, case", [(3, "llama_q4km_1layer"), (16, "llama_q4km_1layer"), (4, "sym_2layers"),
-                                     (16, "sym_2layers"), (2, "q5_0_fallback")])
+                                     (16, "sym_2layers"), (2, "q5_0"),
+                                     (2, "q2_k_fallback")])
 def test_batch_step_matches_oracle(qh, oracle, n, case):
     """BatchStep (n sequences in lockstep: batched GEMMs, batched norm and
     attention) against oracle/glue_ref.forward_step run per sequence, each

@@ -45,13 +45,14 @@ def test_gemv_fused(qh, oracle, t, dims, in_dim, norm, acc):
 
 
 def test_gemv_fused_needs_scratch_only_on_fallback(qh):
-    """Q5_0 has no fused kernel: without scratch the call reports QH_ERR_NULL (-3)
-    instead of writing anywhere; Q4_K and Q8_0 at in_dim 4096 need none."""
+    """Q2_K and Q5_0 have no fused kernel: without scratch the call reports
+    QH_ERR_NULL (-3) instead of writing anywhere; Q4_K, Q8_0 and Q5_1 at in_dim
+    4096 need none."""
     x = GpuBuf.upload_f32(np.ones(4096, np.float32))
     n = GpuBuf.upload_f32(np.ones(4096, np.float32))
     y = GpuBuf.alloc_f32(64)
     import ctypes as C
-    for t, want in ((6, -3), (12, 0), (8, 0)):
+    for t, want in ((10, -3), (6, -3), (12, 0), (8, 0), (7, 0)):
         w = GpuBuf.upload(synth.weights(t, 64, 4096, seed=1))
         rc = qh.hip_gemv_fused_async(t, 1, (C.c_void_p * 1)(w.ptr), (C.c_void_p * 1)(y.ptr), (C.c_int * 1)(64),
                                      x.ptr, n.ptr, 0, 4096, None, None)
