@@ -153,7 +153,7 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qh_mmv16<M16Q4K, 16, 1, true, false, false>", "kernel_us": round(kern_ms * 1e3, 3)},
+                     "kernel": "qh_mmv16<M16Q4K, 16, 1, true, false, false, 1>", "kernel_us": round(kern_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "decode": decode,
         "moe": moe,
