@@ -1172,9 +1172,23 @@ static hipError_t launch_mmv16_mix(const uint8_t* const* Ws1, float* const* ys1,
     QhMats mm1, mm2;
     const int t1 = fill(mm1, Ws1, ys1, outs1, n1, rb1, F1::ROWS), t2 = fill(mm2, Ws2, ys2, outs2, n2, rb2, F2::ROWS);
     if (t1 == 0 || t2 == 0) return hipErrorNotSupported;  // one format: the plain launch
-    const double b1 = (double)t1 * F1::ROWS * rb1, b2 = (double)t2 * F2::ROWS * rb2;
-    int g1 = (int)(resident * b1 / (b1 + b2) + 0.5);
-    g1 = g1 < 1 ? 1 : (g1 > t1 ? t1 : g1);
+    // Split the resident workgroups so that the side with the longer chain of
+    // tiles per workgroup (tiles x tile bytes) is as short as possible.  Small
+    // launches are latency-bound: a second Q6_K tile on a few workgroups costs a
+    // full round, which a byte-proportional split does not see (q, k, v of an 8B
+    // model: 9.0 us split by bytes, 7.1 us with v at one tile per workgroup).
+    const double c1 = (double)F1::ROWS * rb1, c2 = (double)F2::ROWS * rb2;
+    int g1 = 1;
+    double best = 1e300;
+    for (int a = 1; a < resident; a++) {
+        const double cost = fmax(c1 * ((t1 + a - 1) / a), c2 * ((t2 + (resident - a) - 1) / (resident - a)));
+        if (cost < best) {
+            best = cost;
+            g1 = a;
+        }
+    }
+    if (resident - g1 > t2) g1 = resident - t2;  // workgroups the second side cannot use
+    g1 = g1 > t1 ? t1 : g1;
     int g2 = resident - g1;
     g2 = g2 < 1 ? 1 : (g2 > t2 ? t2 : g2);
     if ((t1 + g1 - 1) / g1 > QH_MAXT) g1 = (t1 + QH_MAXT - 1) / QH_MAXT;
