@@ -23,6 +23,7 @@
 // Reference counterpart: the warp-per-row cuda_gemv kernels of
 // src/cuda_kernels.cu:1046-1077 (one f32 FMA per weight).
 #include <climits>
+#include <type_traits>
 
 #include "qh_formats.h"
 #include "qh_internal.h"
@@ -907,8 +908,10 @@ static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int 
 }
 
 // Launch shape: waves per workgroup W and groups per wave and chunk GPW.
-// Measured on MI355X: 16 x 1 is fastest when K fits one chunk (in_dim <= 4096),
-// 8 x 1 above that.  QUARTZ_HIP_MMV16=4|10|2 forces 16x1 | 8x1 | 8x2 (tuning).
+// Measured on MI355X: 16 x 1 is fastest when K fits one chunk (in_dim <= 4096);
+// above that 8 x 1, except Q4_K, which stays at 16 x 1 (4096 x 11008 / 14336,
+// 8192 x 28672: 2-15% faster, while Q6_K and the IQ formats lose at 16 x 1).
+// QUARTZ_HIP_MMV16=4|10|2 forces 16x1 | 8x1 | 8x2 (tuning).
 static int qh_mmv16_variant_env() {
     static const int v = [] {
         const char* e = getenv("QUARTZ_HIP_MMV16");
@@ -916,12 +919,21 @@ static int qh_mmv16_variant_env() {
     }();
     return v;
 }
+template <class F>
+constexpr bool qh_mmv16_wide() {  // 16 x 1 also when K spans several chunks
+    return std::is_same<F, M16Q4K>::value || std::is_same<F, M16Q4K16>::value;
+}
+template <class F>
+static int qh_mmv16_variant(int in_dim) {
+    const int v = qh_mmv16_variant_env();
+    if (v >= 0) return v;
+    return in_dim <= 4096 || qh_mmv16_wide<F>() ? 4 : 10;
+}
 
 template <class F>
 static hipError_t dispatch_mmv16(const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                                  uint32_t row_bytes, hipStream_t st) {
-    int v = qh_mmv16_variant_env();
-    if (v < 0) v = in_dim <= 4096 ? 4 : 10;
+    const int v = qh_mmv16_variant<F>(in_dim);
     switch (v) {
         case 2: return launch_mmv16<F, 8, 2>(W, x, y, in_dim, out_dim, row_bytes, st);
         case 4: return launch_mmv16<F, 16, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
@@ -988,8 +1000,7 @@ static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const 
         if ((int64_t)outs[k] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
         total += outs[k];
     }
-    int v = qh_mmv16_variant_env();
-    if (v < 0) v = in_dim <= 4096 ? 4 : 10;
+    const int v = qh_mmv16_variant<F>(in_dim);
     const bool x1w16 = in_dim <= 256 * 16, x1w8 = in_dim <= 256 * 8;
     (void)total;
     switch (v) {
@@ -1091,6 +1102,11 @@ static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, 
     mm.ldx = ldx;
     if (tiles == 0) return hipSuccess;
     const bool x1 = in_dim <= 256 * 16;
+    // the GEMV's launch shape, so that each token's result is bit-identical to it
+    if constexpr (qh_mmv16_wide<F>())
+        if (!x1)
+            return ntok <= 2 ? launch_mmv16_tok<F, 16, false, 2>(mm, x, in_dim, row_bytes, st)
+                             : launch_mmv16_tok<F, 16, false, 4>(mm, x, in_dim, row_bytes, st);
     if (ntok <= 2)
         return x1 ? launch_mmv16_tok<F, 16, true, 2>(mm, x, in_dim, row_bytes, st)
                   : launch_mmv16_tok<F, 8, false, 2>(mm, x, in_dim, row_bytes, st);
