@@ -229,8 +229,9 @@ __global__ __launch_bounds__(256) void qg_attention_decode(float* out, const flo
 // 32-row slices c, c + nch, ... of the pos + 1 cached rows:
 //   * RoPE of its q heads (qg_rope_rot, as qg_rope_yarn) into LDS;
 //   * the workgroup owning row pos rotates k, appends k and v to the cache at
-//     row pos and uses them from LDS / v for that row (the others read rows
-//     < pos only, so nobody waits for the append);
+//     row pos and takes that row from LDS (the others read rows < pos only, so
+//     nobody waits for the append, and the first slice's K/V loads are issued
+//     before the RoPE, sharing its round trip to memory);
 //   * per slice: K and V rows into LDS once for all the group's heads, scores
 //     (wavefront = q head, lane = row x half of head_dim), an online softmax
 //     (running max m, sum l, output o; lane owns dims lane + 64 j);
@@ -262,6 +263,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     __shared__ __align__(16) float vl[QA_ROWS * HD];
     __shared__ __align__(16) float qr[QA_MAXG * HD];
     __shared__ __align__(16) float kr[HD];
+    __shared__ __align__(16) float vr[HD];
     __shared__ int last_flag;
     const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
     // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
@@ -283,41 +285,6 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     const bool owner = ((pos / QA_ROWS) % nch) == c;
     const float* kh = k + (size_t)g * hd;
     const float* vh = v + (size_t)g * hd;
-    // q rows at stride HD, zero past hd: the score dot runs over HD (a constant)
-    if (hd < HD)
-        for (int p = threadIdx.x; p < ng * HD; p += 256)
-            if (p % HD >= hd) qr[p] = 0.f;
-    for (int p = threadIdx.x; p < ng * half; p += 256) {
-        const int j = p / half, i = p - j * half;
-        const QgRot r = qg_rope_rot(i, hd, pos, theta, yarn_scale, orig_ctx, neox);
-        const float* qh = q + (size_t)(h0 + j) * hd;
-        const float q0 = qh[r.i0], q1 = qh[r.i1];
-        qr[j * HD + r.i0] = q0 * r.c - q1 * r.s;
-        qr[j * HD + r.i1] = q0 * r.s + q1 * r.c;
-        if (owner && j == 0) {
-            const float k0 = kh[r.i0], k1 = kh[r.i1];
-            kr[r.i0] = k0 * r.c - k1 * r.s;
-            kr[r.i1] = k0 * r.s + k1 * r.c;
-        }
-    }
-    __syncthreads();
-    if (owner) {
-        float* kd = kc + (size_t)pos * kv_dim + (size_t)g * hd;
-        float* vd = vc + (size_t)pos * kv_dim + (size_t)g * hd;
-        for (int i = threadIdx.x; i < hd; i += 256) {
-            kd[i] = kr[i];
-            vd[i] = vh[i];
-        }
-    }
-    // running state of this wavefront's heads j = w, w + 4, ... (< ng)
-    float m[GW], l[GW], o[GW][HD / 64];
-#pragma unroll
-    for (int a = 0; a < GW; a++) {
-        m[a] = -1e30f;
-        l[a] = 0.f;
-#pragma unroll
-        for (int d = 0; d < HD / 64; d++) o[a][d] = 0.f;
-    }
     const int t_l = lane & 31, hsel = lane >> 5;
     // K and V rows of a slice: every thread's loads are issued before any is
     // stored, and the next slice's are in flight while this one is computed.
@@ -338,16 +305,57 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             vv[u] = *reinterpret_cast<const f4*>(vc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
         }
     };
-    // the owner's row pos is in the cache before anyone of its workgroup reads it
-    __syncthreads();
     fetch(c);
+    // q rows at stride HD, zero past hd: the score dot runs over HD (a constant)
+    if (hd < HD)
+        for (int p = threadIdx.x; p < ng * HD; p += 256)
+            if (p % HD >= hd) qr[p] = 0.f;
+    for (int p = threadIdx.x; p < ng * half; p += 256) {
+        const int j = p / half, i = p - j * half;
+        const QgRot r = qg_rope_rot(i, hd, pos, theta, yarn_scale, orig_ctx, neox);
+        const float* qh = q + (size_t)(h0 + j) * hd;
+        const float q0 = qh[r.i0], q1 = qh[r.i1];
+        qr[j * HD + r.i0] = q0 * r.c - q1 * r.s;
+        qr[j * HD + r.i1] = q0 * r.s + q1 * r.c;
+        if (owner && j == 0) {
+            const float k0 = kh[r.i0], k1 = kh[r.i1];
+            kr[r.i0] = k0 * r.c - k1 * r.s;
+            kr[r.i1] = k0 * r.s + k1 * r.c;
+            vr[r.i0] = vh[r.i0];
+            vr[r.i1] = vh[r.i1];
+        }
+    }
+    __syncthreads();
+    if (owner) {
+        float* kd = kc + (size_t)pos * kv_dim + (size_t)g * hd;
+        float* vd = vc + (size_t)pos * kv_dim + (size_t)g * hd;
+        for (int i = threadIdx.x; i < hd; i += 256) {
+            kd[i] = kr[i];
+            vd[i] = vr[i];
+        }
+    }
+    // running state of this wavefront's heads j = w, w + 4, ... (< ng)
+    float m[GW], l[GW], o[GW][HD / 64];
+#pragma unroll
+    for (int a = 0; a < GW; a++) {
+        m[a] = -1e30f;
+        l[a] = 0.f;
+#pragma unroll
+        for (int d = 0; d < HD / 64; d++) o[a][d] = 0.f;
+    }
     for (int sl = c; sl * QA_ROWS < seq; sl += nch) {
         const int t0 = sl * QA_ROWS, nv = min(QA_ROWS, seq - t0);
 #pragma unroll
         for (int u = 0; u < IT; u++) {
             const int i = threadIdx.x + 256 * u, r = i / (HD / 4), c4 = i % (HD / 4);
-            *reinterpret_cast<f4*>(kl + r * kp + 4 * c4) = kk[u];
-            *reinterpret_cast<f4*>(vl + r * HD + 4 * c4) = vv[u];
+            f4 ks = kk[u], vs = vv[u];
+            if (owner && t0 + r >= pos) {  // row pos (and the rows past it, which read it again)
+                const int cc = min(c4, q4 - 1);  // a valid column, as fetch reads (kr is unset past hd)
+                ks = *reinterpret_cast<const f4*>(kr + 4 * cc);
+                vs = *reinterpret_cast<const f4*>(vr + 4 * cc);
+            }
+            *reinterpret_cast<f4*>(kl + r * kp + 4 * c4) = ks;
+            *reinterpret_cast<f4*>(vl + r * HD + 4 * c4) = vs;
         }
         __syncthreads();
         fetch(sl + nch);

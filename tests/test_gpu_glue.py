@@ -157,7 +157,7 @@ def test_embed_lookup_bit_exact(qh, oracle, t):
     assert np.array_equal(out.download(np.uint32)[:dim], ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("heads", [(32, 8), (4, 2), (8, 8), (6, 4), (16, 1)], ids=str)
+@pytest.mark.parametrize("heads", [(32, 8), (4, 2), (8, 8), (6, 4), (16, 1), (8, 2, 64), (4, 4, 96)], ids=str)
 @pytest.mark.parametrize("pos", [0, 5, 31, 32, 33, 100, 1000, 2047, 5000])
 def test_attention_step(qh, heads, pos):
     """hip_attention_step (RoPE q/k + K/V append at pos + attention over pos + 1
@@ -166,8 +166,8 @@ def test_attention_step(qh, heads, pos):
     the output (2e-4 at pos >= 1000, the f32 RoPE angle's rounding), the
     appended k row at the same bar and the v row bit-exact; rows before pos are
     left untouched."""
-    nh, nkv = heads
-    hd, theta = 128, 500000.0
+    nh, nkv = heads[:2]
+    hd, theta = (heads[2] if len(heads) > 2 else 128), 500000.0  # head_dim below the kernel's 128 too
     kvd = nkv * hd
     neox = pos % 2
     rng = np.random.default_rng(pos * 7 + nh)
