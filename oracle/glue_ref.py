@@ -32,7 +32,12 @@ token's value; swiglu(0, .) = 0 and swiglu(g, 1) = silu(g); the OAI form
 clamps at 7; moe_route's order against numpy's stable argsort on distinct
 values, -0 < +0 and NaN placement by sign, k = n_exp weights summing to 1, and
 the OLMoE weights against a float64 softmax; moe_ffn with one expert of weight
-1 against the dense FFN.
+1 against the dense FFN.  forward_step as a composition is pinned by
+tests/test_forward_step_ref.py: at pos 0 the output ignores q/k and attention
+returns each group's v; zero o/down weights keep the hidden state and leave
+logits = head @ rms_norm; the FFN block uses ffn_norm and silu(gate) * up; the
+pos 1 attention is the closed-form two-row softmax; K/V rows land at pos only;
+two layers compose in order.
 """
 import struct
 
