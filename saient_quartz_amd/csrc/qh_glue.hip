@@ -70,6 +70,21 @@ __global__ __launch_bounds__(1024) void qg_rms_norm(float* out, const float* x, 
     // row blockIdx.x of a token-major batch (one row: the reference's kernel)
     out += (size_t)blockIdx.x * n;
     x += (size_t)blockIdx.x * n;
+    if (n <= 4 * (int)blockDim.x && (n & 3) == 0 &&
+        !(((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15u)) {
+        // x and w read once into registers: one round trip to memory, not two
+        const int i = 4 * (int)threadIdx.x;
+        float4 xv = {0.f, 0.f, 0.f, 0.f}, wv = xv;
+        if (i < n) {
+            xv = *reinterpret_cast<const float4*>(x + i);
+            wv = *reinterpret_cast<const float4*>(w + i);
+        }
+        float s = (xv.x * xv.x + xv.y * xv.y) + (xv.z * xv.z + xv.w * xv.w);
+        s = qg_block_sum(s, sm);
+        const float r = rsqrtf(s / (float)n + 1e-5f);
+        if (i < n) *reinterpret_cast<float4*>(out + i) = float4{xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w};
+        return;
+    }
     float s = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) s += x[i] * x[i];
     s = qg_block_sum(s, sm);
@@ -547,7 +562,8 @@ hipError_t qh_glue_vec(int op, float* dst, const float* src, float scale, int n,
 }
 
 hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st, int rows) {
-    const int blk = n >= 4096 ? 1024 : n >= 1024 ? 256 : 64;
+    int blk = n >= 4096 ? 1024 : n >= 1024 ? 256 : 64;
+    if (n % 4 == 0 && n <= 4096) blk = (n / 4 + 63) / 64 * 64;  // one float4 per thread (the register path)
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(qg_rms_norm, dim3((unsigned)rows), dim3(blk), 0, st, out, x, w, n);
     return hipGetLastError();
