@@ -131,6 +131,16 @@ int hip_gemm_grouped_norm_async(uint32_t ggml_type, int count, const uint8_t* co
                                 const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
                                 float* d_scratch, void* stream);
 
+/* hip_gemm_grouped_norm_async over count (1..8) matrices of mixed types
+ * (types[k] for W[k]): a batch's norm + q/k/v when v has its own type, as
+ * Q4_K_M models have (src/cuda.rs:549-562).  For 2..4 tokens, two types among
+ * Q4_K/Q5_K + Q6_K and in_dim <= 4096, one launch computes every matrix; each
+ * token's result then equals the per-type call's bit for bit.  Otherwise one
+ * hip_gemm_grouped_norm_async per type, with its scratch rule. */
+int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* const* d_data, const float* d_x,
+                              const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
+                              float* d_scratch, void* stream);
+
 /* Y[t][j] for t < rows with ggml-cuda's int8 MMQ rounding (Q4_K, Q6_K): the
  * GPU twin of the reference's CPU oracles gemm_q4k_q8_1_mmq / gemm_q6k_q8_1_mmq
  * and their _stream_k forms (src/dequant.rs:202-645), bit-exact to them: x is

@@ -366,6 +366,48 @@ int hip_gemm_grouped_ex_async(uint32_t type, int count, const uint8_t* const* W,
     return QH_OK;
 }
 
+int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* const* W, const float* x,
+                              const float* norm_w, float* const* y, int n, const int* out_dims, int in_dim,
+                              float* scratch, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    if (count < 1 || count > 8 || n < 0) return QH_ERR_RANGE;
+    if (n == 0) return QH_OK;
+    if (!types || !W || !x || !norm_w || !y || !out_dims) return QH_ERR_NULL;
+    uint32_t ut[8];
+    int nut = 0, idx[8][8], cnt[8] = {0};
+    for (int k = 0; k < count; k++) {
+        int u = 0;
+        while (u < nut && ut[u] != types[k]) u++;
+        if (u == nut) ut[nut++] = types[k];
+        idx[u][cnt[u]++] = k;
+    }
+    const uint8_t* wu[8][8];
+    float* yu[8][8];
+    int ou[8][8];
+    for (int u = 0; u < nut; u++)
+        for (int i = 0; i < cnt[u]; i++) {
+            wu[u][i] = W[idx[u][i]];
+            yu[u][i] = y[idx[u][i]];
+            ou[u][i] = out_dims[idx[u][i]];
+        }
+    if (n >= 2 && n <= 4 && nut == 2 && cnt[0] <= 4 && cnt[1] <= 4 && !qh_force_valu()) {
+        bool ok = true;
+        for (int k = 0; k < count; k++)
+            ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
+        if (ok) {
+            hipError_t e = qh_launch_mmv16_mix_tokens(ut[0], wu[0], yu[0], ou[0], ou[0], cnt[0], ut[1], wu[1], yu[1],
+                                                      ou[1], ou[1], cnt[1], x, in_dim, n, in_dim, norm_w, 0, st);
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
+        }
+    }
+    for (int u = 0; u < nut; u++) {
+        int rc = hip_gemm_grouped_norm_async(ut[u], cnt[u], wu[u], x, norm_w, yu[u], n, ou[u], in_dim, scratch, stream);
+        if (rc) return rc;
+    }
+    return QH_OK;
+}
+
 int hip_gemm_grouped_norm_async(uint32_t type, int count, const uint8_t* const* W, const float* x,
                                 const float* norm_w, float* const* y, int n, const int* out_dims, int in_dim,
                                 float* scratch, void* stream) {

@@ -55,6 +55,10 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
 hipError_t qh_launch_mmv16_mix(uint32_t t1, const uint8_t* const* Ws1, float* const* ys1, const int* outs1, int n1,
                                uint32_t t2, const uint8_t* const* Ws2, float* const* ys2, const int* outs2, int n2,
                                const float* x, int in_dim, const float* nw, int accum, hipStream_t st);
+hipError_t qh_launch_mmv16_mix_tokens(uint32_t t1, const uint8_t* const* Ws1, float* const* ys1, const int* outs1,
+                                      const int* ldys1, int n1, uint32_t t2, const uint8_t* const* Ws2,
+                                      float* const* ys2, const int* outs2, const int* ldys2, int n2, const float* x,
+                                      int ldx, int ntok, int in_dim, const float* nw, int accum, hipStream_t st);
 hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* Ws, float* const* ys, const int* outs,
                                   const int* ldys, const float* x, int ldx, int ntok, int in_dim, int accum,
                                   hipStream_t st, const float* nw = nullptr);

@@ -809,16 +809,16 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float*
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
 // workgroups below g1 run F1's body on mm1's matrices, the others F2's on mm2's.
-template <class F1, class F2, int W, int GPW, bool X1>
+template <class F1, class F2, int W, int GPW, bool X1, int NT = 1>
 __global__ __launch_bounds__(64 * W) void qh_mmv16_mix(const QhMats mm1, const QhMats mm2, const float* __restrict__ x,
                                                        uint32_t rb1, uint32_t rb2, int ngroups, int g1) {
-    constexpr int L1 = qh_mmv16_lds<F1, W, GPW>(), L2 = qh_mmv16_lds<F2, W, GPW>();
+    constexpr int L1 = qh_mmv16_lds<F1, W, GPW, NT>(), L2 = qh_mmv16_lds<F2, W, GPW, NT>();
     __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
     if ((int)blockIdx.x < g1)
-        qh_mmv16_body<F1, W, GPW, X1, true, false>(mm1, x, rb1, ngroups, lds, (int)blockIdx.x, g1);
+        qh_mmv16_body<F1, W, GPW, X1, true, false, NT>(mm1, x, rb1, ngroups, lds, (int)blockIdx.x, g1);
     else
-        qh_mmv16_body<F2, W, GPW, X1, true, false>(mm2, x, rb2, ngroups, lds, (int)blockIdx.x - g1,
-                                                   (int)gridDim.x - g1);
+        qh_mmv16_body<F2, W, GPW, X1, true, false, NT>(mm2, x, rb2, ngroups, lds, (int)blockIdx.x - g1,
+                                                       (int)gridDim.x - g1);
 }
 
 // nm matrices (each's weights < 2^31 bytes) in one launch.
@@ -1151,28 +1151,34 @@ hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* W
 // Two formats sharing x in one launch: matrices Ws1 (format F1) and Ws2 (F2),
 // each group <= QH_MULTI matrices < 2^31 bytes.  The resident workgroups are
 // split between the two bodies in proportion to their weight bytes.
-template <class F1, class F2, int W, int GPW, bool X1>
+// Tokens (NT > 1): ntok tokens of x at stride ldx; matrix k's results at ys[k] +
+// t * ldys[k] (the one-token launch passes ldys = nullptr).
+template <class F1, class F2, int W, int GPW, bool X1, int NT = 1>
 static hipError_t launch_mmv16_mix(const uint8_t* const* Ws1, float* const* ys1, const int* outs1, int n1,
                                    const uint8_t* const* Ws2, float* const* ys2, const int* outs2, int n2,
                                    const float* x, int in_dim, uint32_t rb1, uint32_t rb2, const float* nw, int accum,
-                                   hipStream_t st) {
+                                   hipStream_t st, const int* ldys1 = nullptr, const int* ldys2 = nullptr,
+                                   int ldx = 0, int ntok = 1) {
     if (nw && !X1) return hipErrorNotSupported;
     static int resident = 0;
     if (!resident) {
         int dev = 0, per_cu = 0;
         hipDeviceProp_t prop;
         if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16_mix<F1, F2, W, GPW, X1>, 64 * W, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, qh_mmv16_mix<F1, F2, W, GPW, X1, NT>, 64 * W, 0) !=
                 hipSuccess ||
             per_cu < 1)
             return hipErrorNotSupported;
         resident = per_cu * prop.multiProcessorCount;
     }
     auto fill = [&](QhMats& mm, const uint8_t* const* Ws, float* const* ys, const int* outs, int nm, uint32_t rb,
-                    int rows_per_tile) {
+                    int rows_per_tile, const int* ldys) {
         int tiles = 0;
+        mm.ntok = ntok;
+        mm.ldx = ldx;
         for (int k = 0; k < QH_MULTI; k++) {
             const bool on = k < nm;
+            mm.ldy[k] = on && ldys ? ldys[k] : 0;
             mm.w[k] = on ? Ws[k] : nullptr;
             mm.y[k] = on ? ys[k] : nullptr;
             mm.rows[k] = on ? outs[k] : 0;
@@ -1186,7 +1192,8 @@ static hipError_t launch_mmv16_mix(const uint8_t* const* Ws1, float* const* ys1,
         return tiles;
     };
     QhMats mm1, mm2;
-    const int t1 = fill(mm1, Ws1, ys1, outs1, n1, rb1, F1::ROWS), t2 = fill(mm2, Ws2, ys2, outs2, n2, rb2, F2::ROWS);
+    const int t1 = fill(mm1, Ws1, ys1, outs1, n1, rb1, F1::ROWS, ldys1),
+              t2 = fill(mm2, Ws2, ys2, outs2, n2, rb2, F2::ROWS, ldys2);
     if (t1 == 0 || t2 == 0) return hipErrorNotSupported;  // one format: the plain launch
     // Split the resident workgroups so that the side with the longer chain of
     // tiles per workgroup (tiles x tile bytes) is as short as possible.  Small
@@ -1207,11 +1214,27 @@ static hipError_t launch_mmv16_mix(const uint8_t* const* Ws1, float* const* ys1,
     g1 = g1 > t1 ? t1 : g1;
     int g2 = resident - g1;
     g2 = g2 < 1 ? 1 : (g2 > t2 ? t2 : g2);
-    if ((t1 + g1 - 1) / g1 > QH_MAXT) g1 = (t1 + QH_MAXT - 1) / QH_MAXT;
-    if ((t2 + g2 - 1) / g2 > QH_MAXT) g2 = (t2 + QH_MAXT - 1) / QH_MAXT;
-    hipLaunchKernelGGL((qh_mmv16_mix<F1, F2, W, GPW, X1>), dim3((unsigned)(g1 + g2)), dim3(64 * W), 0, st, mm1, mm2, x,
-                       rb1, rb2, in_dim / 256, g1);
+    // tiles per workgroup within the LDS ring of finished rows (more workgroups
+    // than resident then, which run in a second round)
+    constexpr int MAXT = qh_maxt<NT>();
+    if ((t1 + g1 - 1) / g1 > MAXT) g1 = (t1 + MAXT - 1) / MAXT;
+    if ((t2 + g2 - 1) / g2 > MAXT) g2 = (t2 + MAXT - 1) / MAXT;
+    hipLaunchKernelGGL((qh_mmv16_mix<F1, F2, W, GPW, X1, NT>), dim3((unsigned)(g1 + g2)), dim3(64 * W), 0, st, mm1,
+                       mm2, x, rb1, rb2, in_dim / 256, g1);
     return hipGetLastError();
+}
+
+template <class F1, class F2>
+static hipError_t dispatch_mix_tokens(const uint8_t* const* Ws1, float* const* ys1, const int* outs1, const int* ldys1,
+                                      int n1, const uint8_t* const* Ws2, float* const* ys2, const int* outs2,
+                                      const int* ldys2, int n2, const float* x, int ldx, int ntok, int in_dim,
+                                      uint32_t rb1, uint32_t rb2, const float* nw, int accum, hipStream_t st) {
+    if (in_dim > 256 * 16) return hipErrorNotSupported;  // X1 only, as the one-token norm fusion
+    if (ntok <= 2)
+        return launch_mmv16_mix<F1, F2, 16, 1, true, 2>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2,
+                                                        nw, accum, st, ldys1, ldys2, ldx, ntok);
+    return launch_mmv16_mix<F1, F2, 16, 1, true, 4>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw,
+                                                    accum, st, ldys1, ldys2, ldx, ntok);
 }
 
 template <class F1, class F2>
@@ -1246,5 +1269,32 @@ hipError_t qh_launch_mmv16_mix(uint32_t t1, const uint8_t* const* Ws1, float* co
         return dispatch_mix<M16Q5K, M16Q6K>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw, accum, st);
     if (t1 == QT_Q4_K && t2 == QT_Q5_K)
         return dispatch_mix<M16Q4K, M16Q5K>(Ws1, ys1, outs1, n1, Ws2, ys2, outs2, n2, x, in_dim, rb1, rb2, nw, accum, st);
+    return hipErrorNotSupported;
+}
+
+// 2-4 tokens of the two-format launch (token t of x at x + t ldx, its results at
+// ys[k] + t ldys[k]); each token's result is the one-token launch's bit for bit.
+// X1 shapes only (in_dim <= 4096); hipErrorNotSupported otherwise.
+hipError_t qh_launch_mmv16_mix_tokens(uint32_t t1, const uint8_t* const* Ws1, float* const* ys1, const int* outs1,
+                                      const int* ldys1, int n1, uint32_t t2, const uint8_t* const* Ws2,
+                                      float* const* ys2, const int* outs2, const int* ldys2, int n2, const float* x,
+                                      int ldx, int ntok, int in_dim, const float* nw, int accum, hipStream_t st) {
+    if (!qh_tokens_enabled() || ntok < 2 || ntok > 4 || n1 < 1 || n1 > QH_MULTI || n2 < 1 || n2 > QH_MULTI ||
+        in_dim % 256 || ((uintptr_t)x & 15u) || (ldx & 3) || qh_mmv16_variant_env() >= 0)
+        return hipErrorNotSupported;
+    const uint32_t rb1 = (uint32_t)qh_type_size(t1, (size_t)in_dim), rb2 = (uint32_t)qh_type_size(t2, (size_t)in_dim);
+    for (int k = 0; k < n1; k++)
+        if ((int64_t)outs1[k] * rb1 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+    for (int k = 0; k < n2; k++)
+        if ((int64_t)outs2[k] * rb2 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+    if (t1 > t2)
+        return qh_launch_mmv16_mix_tokens(t2, Ws2, ys2, outs2, ldys2, n2, t1, Ws1, ys1, outs1, ldys1, n1, x, ldx, ntok,
+                                          in_dim, nw, accum, st);
+    if (t1 == QT_Q4_K && t2 == QT_Q6_K)
+        return dispatch_mix_tokens<M16Q4K, M16Q6K>(Ws1, ys1, outs1, ldys1, n1, Ws2, ys2, outs2, ldys2, n2, x, ldx,
+                                                   ntok, in_dim, rb1, rb2, nw, accum, st);
+    if (t1 == QT_Q5_K && t2 == QT_Q6_K)
+        return dispatch_mix_tokens<M16Q5K, M16Q6K>(Ws1, ys1, outs1, ldys1, n1, Ws2, ys2, outs2, ldys2, n2, x, ldx,
+                                                   ntok, in_dim, rb1, rb2, nw, accum, st);
     return hipErrorNotSupported;
 }

@@ -23,7 +23,7 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import (gemm_grouped_async, gemm_grouped_ex_async, gemm_grouped_norm_async, gemm_moe_async,
+from .host import (gemm_group_norm_async, gemm_grouped_async, gemm_grouped_ex_async, gemm_moe_async,
                    gemv_group_async, gemv_multi_async)
 
 Q4_K, Q6_K = 12, 14
@@ -435,21 +435,18 @@ class BatchStep:
 
     def _gemm_norm(self, names, layer, norm, ys, sp):
         """y = W rms_norm(hidden) * norm for the matrices `names`.  Up to 4 tokens:
-        the norm fused into the GEMMs (one hip_gemm_grouped_norm call per weight
-        type); more: one hip_rms_norm_rows shared by every type's GEMMs."""
+        the norm fused into the GEMMs (one hip_gemm_group_norm call, which runs
+        q/k (Q4_K) and v (Q6_K) in one launch); more: one hip_rms_norm_rows shared
+        by every type's GEMMs."""
         if self.n > 4:
             check("hip_rms_norm_rows_async", self.L.hip_rms_norm_rows_async(
                 self.xn.data_ptr(), self.hidden.data_ptr(), norm.data_ptr(), self.n, self.cfg.hidden, sp))
             self._gemm(names, layer, self.xn, ys, self.cfg.hidden, sp)
             return
-        by_type = {}
-        for nm, y in zip(names, ys):
-            by_type.setdefault(self.cfg.type_of(nm), []).append((nm, y))
-        for t, group in by_type.items():
-            ws = [(self.w[nm][layer] if layer is not None else self.w[nm]).data_ptr() for nm, _ in group]
-            gemm_grouped_norm_async(self.L, t, ws, self.hidden.data_ptr(), norm.data_ptr(),
-                                    [y.data_ptr() for _, y in group], self.n, [y.shape[1] for _, y in group],
-                                    self.cfg.hidden, sp, self.scratch.data_ptr())
+        ws = [(self.w[nm][layer] if layer is not None else self.w[nm]).data_ptr() for nm in names]
+        gemm_group_norm_async(self.L, [self.cfg.type_of(nm) for nm in names], ws, self.hidden.data_ptr(),
+                              norm.data_ptr(), [y.data_ptr() for y in ys], self.n, [y.shape[1] for y in ys],
+                              self.cfg.hidden, sp, self.scratch.data_ptr())
 
     def issue(self, tokens, pos: int, stream=None, logits: bool = True):
         """Enqueue one lockstep decode step: sequence i takes tokens[i] at `pos`."""

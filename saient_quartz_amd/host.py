@@ -175,6 +175,17 @@ def gemm_grouped_norm_async(L, ggml_type, w_ptrs, x_ptr, norm_w_ptr, y_ptrs, n, 
                                         stream_ptr))
 
 
+def gemm_group_norm_async(L, types, w_ptrs, x_ptr, norm_w_ptr, y_ptrs, n, out_dims, in_dim, stream_ptr,
+                          scratch_ptr=None):
+    """hip_gemm_group_norm_async: gemm_grouped_norm_async over matrices of mixed types."""
+    import ctypes as C
+    k = len(w_ptrs)
+    check("hip_gemm_group_norm_async",
+          L.hip_gemm_group_norm_async(k, (C.c_uint32 * k)(*types), (C.c_void_p * k)(*w_ptrs), x_ptr, norm_w_ptr,
+                                      (C.c_void_p * k)(*y_ptrs), n, (C.c_int * k)(*out_dims), in_dim, scratch_ptr,
+                                      stream_ptr))
+
+
 def gemm_moe_async(L, ggml_type, experts_ptr, expert_ids, tok_off, x_ptr, y_ptr, in_dim, out_dim, stream_ptr):
     """hip_gemm_moe_async: expert_ids[i] takes gathered tokens tok_off[i] .. tok_off[i+1]-1."""
     import ctypes as C

@@ -381,3 +381,47 @@ def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
         ref = oracle.gemm(t, xn, d, in_dim, o, n)
         for r in range(n):
             assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21)], ids=str)
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("in_dim", [4096, 2048, 5120])
+def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
+    """hip_gemm_group_norm_async (mixed types: a Q4_K_M layer's q, k (Q4_K) and v
+    (Q6_K)): bit-identical to one hip_gemm_grouped_norm_async per type (the
+    two-format launch for 2-4 tokens, the per-type calls otherwise), and within
+    the GEMV bar of the oracle on the normalised rows (float64 norm).  5120 is
+    past the one-workgroup norm; IQ3_S + Q4_K has no two-format kernel."""
+    import ctypes as C
+    outs = [300, 77, 64][:len(types)]
+    rng = np.random.default_rng(n + in_dim + sum(types))
+    x = (rng.standard_normal((n, in_dim)) * rng.uniform(0.1, 10, (n, 1))).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    datas = [synth.weights(t, o, in_dim, seed=o + n + t) for t, o in zip(types, outs)]
+    dw = [GpuBuf.upload(d) for d in datas]
+    dx, dn = GpuBuf.upload_f32(x.reshape(-1)), GpuBuf.upload_f32(w)
+    dy = [GpuBuf.alloc_f32(n * o) for o in outs]
+    scratch = GpuBuf.alloc_f32(n * in_dim)
+    k = len(outs)
+    check("hip_gemm_group_norm_async", qh.hip_gemm_group_norm_async(
+        k, (C.c_uint32 * k)(*types), (C.c_void_p * k)(*[b.ptr for b in dw]), dx.ptr, dn.ptr,
+        (C.c_void_p * k)(*[b.ptr for b in dy]), n, (C.c_int * k)(*outs), in_dim, scratch.ptr, None))
+    # the per-type reference calls
+    ey = [GpuBuf.alloc_f32(n * o) for o in outs]
+    for t in sorted(set(types)):
+        ks = [i for i, tt in enumerate(types) if tt == t]
+        m = len(ks)
+        check("hip_gemm_grouped_norm_async", qh.hip_gemm_grouped_norm_async(
+            t, m, (C.c_void_p * m)(*[dw[i].ptr for i in ks]), dx.ptr, dn.ptr, (C.c_void_p * m)(*[ey[i].ptr for i in ks]),
+            n, (C.c_int * m)(*[outs[i] for i in ks]), in_dim, scratch.ptr, None))
+    check("hip_sync", qh.hip_sync())
+    xd = x.astype(np.float64)
+    xn = (xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5) * w).astype(np.float32)
+    for b, e, d, o, t in zip(dy, ey, datas, outs, types):
+        got = b.download(np.float32)[:n * o].reshape(n, o)
+        exp = e.download(np.float32)[:n * o].reshape(n, o)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), (t, o)
+        ref = oracle.gemm(t, xn, d, in_dim, o, n)
+        for r in range(n):
+            assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
