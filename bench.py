@@ -47,7 +47,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
-                                   "(the GEMV shards by output rows, see DESIGN.md)"}))
+                                   "(across GPUs the GEMV would shard by output rows, each GPU holding its rows' blocks)"}))
         sys.exit(2)
     import torch
 
