@@ -572,6 +572,23 @@ int o_gemv(uint32_t t, const float* x, const uint8_t* data, int in_dim, int out_
     }
 }
 
+/* The `_` arm of src/dequant.rs:26-29 as the reference runs it: dequant() of
+ * the WHOLE matrix into one f32 buffer (src/dequant.rs:1239-1258, w here,
+ * out_dim * in_dim floats, caller-owned), then crate::matmul's row-parallel
+ * zip-map-sum (src/main.rs:710-718).  Same values and sum order as o_gemv's
+ * row-by-row form; timed as the CPU baseline of the types that take this arm. */
+int o_gemv_dequant_matmul(uint32_t t, const float* x, const uint8_t* data, int in_dim, int out_dim, float* w,
+                          float* y) {
+    int rc = dims_ok(t, in_dim, out_dim);
+    if (rc) return rc;
+    size_t rb = o_type_size(t, (size_t)in_dim);
+#pragma omp parallel for schedule(static)
+    for (int j = 0; j < out_dim; j++) o_dequant(t, data + (size_t)j * rb, (size_t)in_dim, w + (size_t)j * in_dim);
+#pragma omp parallel for schedule(static)
+    for (int j = 0; j < out_dim; j++) y[j] = row_dot_iter(x, w + (size_t)j * in_dim, in_dim);
+    return 0;
+}
+
 /* src/dequant.rs:38-77 q4k_row_batched / :81-122 q6k_row_batched: decode each
  * superblock once into wv[256], then acc[t] += Σ_i xt[i]*wv[i] (s from 0.0). */
 static void rowb_k(uint32_t t, const float* x, int in_dim, int n, const uint8_t* row, float* acc) {

@@ -14,6 +14,8 @@ size_t o_type_size(uint32_t ggml_type, size_t n_elems);   /* 0 = unsupported typ
 int o_block_elems(uint32_t ggml_type);                     /* 0 = unsupported type */
 int o_dequant(uint32_t ggml_type, const uint8_t* data, size_t n_elems, float* out);
 int o_gemv(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, int out_dim, float* y);
+int o_gemv_dequant_matmul(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, int out_dim,
+                          float* w_scratch, float* y);
 int o_gemm(uint32_t ggml_type, const float* x, const uint8_t* data, int in_dim, int out_dim, int n, float* y);
 void o_set_threads(int n);
 int o_get_threads(void);

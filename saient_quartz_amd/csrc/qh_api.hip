@@ -48,9 +48,15 @@ static int qh_check_dims(uint32_t type, int in_dim, int out_dim) {
 // Unknown type: zero y and say so, as cuda_gemv does (src/cuda_kernels.cu:1070-1074).
 static int qh_unknown_type(const char* fn, uint32_t type, float* y, size_t n, hipStream_t st) {
     fprintf(stderr, "%s: unsupported ggml_type %u\n", fn, type);
-    if (y && n) {
-        hipError_t e = hipMemsetAsync(y, 0, n * sizeof(float), st);
-        if (e != hipSuccess) qh_fail(e, fn);
+    // The library's zero-fill kernel rather than hipMemsetAsync, so a call made
+    // under HIP graph capture records a kernel node, not a memset node.
+    for (size_t off = 0; y && off < n; off += (size_t)1 << 30) {
+        const size_t m = n - off < ((size_t)1 << 30) ? n - off : ((size_t)1 << 30);
+        hipError_t e = qh_glue_vec(2, y + off, nullptr, 0.f, (int)m, st);
+        if (e != hipSuccess) {
+            qh_fail(e, fn);
+            break;
+        }
     }
     return QH_ERR_TYPE;
 }
@@ -394,6 +400,14 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
         bool ok = true;
         for (int k = 0; k < count; k++)
             ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
+        // The per-type call takes 3-4 tokens through the GEMV kernel only up to
+        // 16 MB of weights per type (qh_launch_mmq_grouped); the mixed launch
+        // follows the same rule, so each type's result is the per-type call's.
+        for (int u = 0; ok && n > 2 && u < 2; u++) {
+            int64_t wb = 0;
+            for (int i = 0; i < cnt[u]; i++) wb += (int64_t)qh_type_size(ut[u], (size_t)in_dim) * ou[u][i];
+            ok = wb <= ((int64_t)16 << 20);
+        }
         if (ok) {
             hipError_t e = qh_launch_mmv16_mix_tokens(ut[0], wu[0], yu[0], ou[0], ou[0], cnt[0], ut[1], wu[1], yu[1],
                                                       ou[1], ou[1], cnt[1], x, in_dim, n, in_dim, norm_w, 0, st);

@@ -32,6 +32,9 @@ class Oracle:
         L.o_dequant.argtypes = [C.c_uint32, C.c_void_p, C.c_size_t, C.c_void_p]
         L.o_gemv.restype = C.c_int
         L.o_gemv.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+        L.o_gemv_dequant_matmul.restype = C.c_int
+        L.o_gemv_dequant_matmul.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                            C.c_void_p]
         L.o_gemm.restype = C.c_int
         L.o_gemm.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
         L.o_set_threads.argtypes = [C.c_int]
@@ -67,6 +70,22 @@ class Oracle:
         rc = self.L.o_gemv(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, y.ctypes.data)
         if rc:
             raise ValueError(f"o_gemv rc={rc}")
+        return y
+
+    def gemv_dequant_matmul(self, t, x: np.ndarray, data: np.ndarray, in_dim: int, out_dim: int,
+                            w_scratch: np.ndarray = None) -> np.ndarray:
+        """The `_` arm as the reference runs it: the whole matrix dequantized
+        into w_scratch (out_dim * in_dim f32), then the row-parallel matmul."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        if w_scratch is None:
+            w_scratch = np.empty(out_dim * in_dim, dtype=np.float32)
+        assert w_scratch.dtype == np.float32 and w_scratch.size >= out_dim * in_dim
+        y = np.empty(out_dim, dtype=np.float32)
+        rc = self.L.o_gemv_dequant_matmul(t, x.ctypes.data, data.ctypes.data, in_dim, out_dim, w_scratch.ctypes.data,
+                                          y.ctypes.data)
+        if rc:
+            raise ValueError(f"o_gemv_dequant_matmul rc={rc}")
         return y
 
     def gemm(self, t, x: np.ndarray, data: np.ndarray, in_dim: int, out_dim: int, n: int) -> np.ndarray:

@@ -13,6 +13,7 @@ Rust/CUDA, neither buildable here), so the oracle is pinned by:
 import struct
 
 import numpy as np
+from pathlib import Path
 import pytest
 
 import closed_form as cf
@@ -189,6 +190,44 @@ def test_iq_grids_pinned(oracle):
     assert tuple(cf.grid_bytes("IQ3S")[0]) == (1, 1, 1, 1)
 
 
+# SHA-256 of each codebook's little-endian values (u64 entries for IQ2*, u32 for
+# IQ3S), computed from the reference's tables (src/iq2_tables.rs:3-7,
+# src/iq3_tables.rs:2).  Literal here, independent of iq_grids.h, so a wrong
+# regeneration of the header fails this test even where the reference is absent.
+IQ_GRID_SHA256 = {
+    "IQ2XXS": "05826b5d3e472a3a78f196be62ac78acf81df0f909626e12ab9fa2a5d490dd54",
+    "IQ2XS": "06e47aaca60b4dc1d9b5a3f34540437058a6b142b4d7a59d5ded769b4d1bf1de",
+    "IQ2S": "e1aa1473412b0552c2174c30ef22ab4073f6a181b85a17056e8249bd2932fd88",
+    "IQ3S": "bd1af4945a1717c65610b0284e4628b9a1ba3b306fae3a06f6e5f597356e349f",
+}
+REF_SRC = Path("/root/reference/src")
+
+
+def test_iq_grids_match_pinned_hashes():
+    for name, sha in IQ_GRID_SHA256.items():
+        assert cf.grid_sha256(name) == sha, name
+
+
+@pytest.mark.skipif(not (REF_SRC / "iq2_tables.rs").exists(), reason="reference sources not present")
+def test_iq_grids_equal_reference_tables():
+    """Parse the reference's Rust tables and compare them value by value with
+    the header's (and ksigns / kmask with their closed forms)."""
+    import re
+
+    def table(fname, ident):
+        txt = (REF_SRC / fname).read_text()
+        m = re.search(r"pub static %s: \[u\d+; (\d+)\] = \[(.*?)\];" % ident, txt, re.S)
+        vals = [int(v, 0) for v in re.findall(r"0x[0-9a-fA-F]+|\b\d+\b", m.group(2))]
+        assert len(vals) == int(m.group(1))
+        return np.array(vals, dtype=np.uint64)
+
+    for name, (fname, ident) in {"IQ2XXS": ("iq2_tables.rs", "IQ2XXS_GRID"), "IQ2XS": ("iq2_tables.rs", "IQ2XS_GRID"),
+                                 "IQ2S": ("iq2_tables.rs", "IQ2S_GRID"), "IQ3S": ("iq3_tables.rs", "IQ3S_GRID")}.items():
+        np.testing.assert_array_equal(cf.GRIDS[name][0], table(fname, ident), err_msg=name)
+    np.testing.assert_array_equal(table("iq2_tables.rs", "KSIGNS_IQ2XS").astype(np.uint8), cf.ksigns())
+    np.testing.assert_array_equal(table("iq2_tables.rs", "KMASK_IQ2XS"), 1 << np.arange(8, dtype=np.uint64))
+
+
 @pytest.mark.parametrize("t", ALL_TYPES)
 @pytest.mark.parametrize("shape", [(8, 256), (3, 512), (17, 1024)])
 def test_gemv_vs_f64(oracle, t, shape):
@@ -245,3 +284,18 @@ def test_gemv_thread_count_independent(oracle):
     b = oracle.gemv(12, x, data, 1024, 64)
     oracle.set_threads(n0)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("t", [8, 6, 16, 21, 12])
+def test_gemv_dequant_matmul_equals_gemv(oracle, t):
+    """The whole-matrix dequant + matmul form (timed as the CPU baseline of the
+    `_` arm) gives o_gemv's values bit for bit."""
+    out_dim, in_dim = 33, 1024
+    data = synth.weights(t, out_dim, in_dim, seed=77 + t)
+    x = synth.activations(1, in_dim, seed=5)[0]
+    a = oracle.gemv(t, x, data, in_dim, out_dim)
+    b = oracle.gemv_dequant_matmul(t, x, data, in_dim, out_dim)
+    if t == 12:  # fused-row type: same values up to the f32 sum order
+        assert cf.rel_l2(a, b) < 1e-5
+    else:
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
