@@ -1,28 +1,32 @@
-// qh_gemm.hip -- batched dequant-GEMM for n = 2..16 tokens on the int8 matrix
-// cores (v_mfma_i32_32x32x32_i8), Q4_K / Q5_K / Q6_K / IQ3_S / IQ2_XXS.
+// qh_gemm.hip -- batched dequant-GEMM for n = 2..16 tokens on the f16 matrix
+// cores (v_mfma_f32_32x32x16_f16), Q4_K / Q5_K / Q6_K / IQ3_S / IQ2_XXS.
 //
 // Y[t][j] = sum_k W[j,k] X[t][k], X and Y token-major.  One pass over the weights
 // serves every token: the weights are the B operand (32 weight rows = the 32
-// MFMA columns), the tokens are the A operand (A row 2t + m = digit m of token
-// t's x), so a lane's 16 results all belong to one weight row and one scale.
-//   * x as two balanced int8 digits: per token and K chunk, s = 14 - exponent of
-//     max|x|, x * 2^s is rounded to an integer of at most 2^14 in magnitude (one
-//     FMA against a magic constant) and split into d0 + 256 d1.  The int32 MFMA
-//     sums are exact; x's rounding (<= 2^-15 of the chunk's largest |x| per token)
-//     is the only error added (measured ~3e-5 relative L2 against the oracle,
-//     against the 1e-3 bar).
-//   * Q4_K / Q5_K: one MFMA per 32-weight sub-block (one scale), 16 tokens each.
-//     Q6_K: 16-weight scale groups, so a 32-weight chunk carries two scales: A
-//     rows 0-15 hold tokens' digits for k < 16 and rows 16-31 for k >= 16, 8
-//     tokens per MFMA, and result registers 0-7 / 8-15 take the two scales.
-//   * mins (Q4_K/Q5_K dmin * m_j * sum(x)): one more MFMA per group whose B
-//     operand is the 8 mins and whose A operand is the per-token sums of x over
-//     the sub-blocks, digitised the same way.  Q6_K's -32 is in its B operand
-//     (q - 32 is a signed byte), so its sums are not needed.
-// Weights are read with the same coalesced, LDS-staged, persistent pipeline as
-// qh_mmv16.hip (tiles of 32 rows; the next item's loads are in flight while the
-// current one is computed).  Every item re-digitises x for its K chunk and all
-// tokens (4 NT elements per lane).
+// MFMA columns), the tokens' x the A operand, so a lane's results all belong to
+// one weight row.
+//   * x as two f16 per element: per token and 256-element group, x' = x 2^s
+//     (s = 14 - exponent of max|x|, so |x'| < 2^14) is split into hi = f16(x')
+//     and lo = f16(x' - hi) (both rounded toward zero), 21-22 significant bits
+//     per element whatever the group's other values (an outlier costs its
+//     neighbours nothing).  A rows
+//     2t and 2t + 1 hold token t's hi and lo parts.
+//   * B = the integer weight times its integer scale as f16, exact (|B| <=
+//     2048, or a short integer times a power of two): one K-block of 16 weights
+//     shares one scale in every format (Q6_K's scale groups are 16 weights), so
+//     the MFMA accumulates a whole superblock without per-scale epilogue work.
+//     Bytes become f16 with v_perm into 0x64xx (1024 + byte) and one packed FMA
+//     against (scale, -(1024 + offset) scale), exact as long as that constant
+//     fits f16 (Q6_K uses an add and a multiply instead).
+//   * Q4_K / Q5_K mins (dmin * m_sb * sum(x over sb)): one more f16 MFMA whose A
+//     operand is each token's per-sub-block x sums (hi + lo, scaled by 2^(s-5))
+//     and whose B operand is the 8 mins.
+//   * Products and sums accumulate in f32; the superblock's f16 scale d (and
+//     dmin) multiply the f32 results once per superblock.
+// Each workgroup digitises the x of its K split for all 16 token slots straight
+// into LDS (no separate prologue launch); its W wavefronts (one or two 32-row
+// tiles each) read their A operands from there, while each wavefront's weight
+// slices stream through its own LDS tile with QG_NBUF items in flight.
 //
 // Reference counterpart: dequant::gemm (src/dequant.rs:143-200) with
 // q4k_row_batched / q6k_row_batched (:38-122); the reference has no GPU
@@ -32,21 +36,56 @@
 #include "qh_formats.h"
 #include "qh_internal.h"
 
-typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t qh_i32x16 __attribute__((ext_vector_type(16)));
+typedef float qh_f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 qh_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 
-#define QG_WAVES 4          // wavefronts per workgroup
-#define QG_TARGET_WGS 256   // workgroups a launch aims for (measured best: one per CU; more split K further and lose)
-#define QG_PART_TILES 2048  // (row tile, K split) partials the scratch holds
+#define QG_WAVES 8          // wavefronts (32-row tiles) per workgroup
+#define QG_TARGET_WGS 256   // workgroups a launch aims for (one per CU)
+#define QG_PART_TILES 4096  // row blocks with split-K counters (one per wavefront)
+#define QG_GMAX 6           // groups per workgroup (their x images stay in LDS)
+#define QG_NBUF 2           // items of weights in flight per wavefront (register sets)
+#define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
+
+// ---------------------------------------------------------------- f16 operands
+
+QH_DEV uint32_t qg_h2u(qh_f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+QH_DEV qh_f16x2 qg_u2h(uint32_t u) { return __builtin_bit_cast(qh_f16x2, u); }
+// bytes (b0, b1) or (b2, b3) of w as the f16 pair (1024 + b, 1024 + b')
+#define QG_SEL01 0x04010400u
+#define QG_SEL23 0x04030402u
+QH_DEV qh_f16x2 qg_b2h(uint32_t w, uint32_t sel) { return qg_u2h(__builtin_amdgcn_perm(0x64646464u, w, sel)); }
+// (f, f) for an integer |f| <= 1024 given as a byte-biased value: the f16 pair
+// of byte k of w, minus bias
+QH_DEV qh_f16x2 qg_dup(uint32_t w, int k, _Float16 bias) {
+    const uint32_t sel = (uint32_t)k | 0x0400u | ((uint32_t)k << 16) | 0x04000000u;
+    return qg_u2h(__builtin_amdgcn_perm(0x64646464u, w, sel)) - qh_f16x2{bias, bias};
+}
+// 8 unsigned bytes (w0, w1) -> B operand sc * (byte - off): fma(1024 + b, sc,
+// c) with c = -(1024 + off) sc, exact when |c| <= 65504 and |sc (b - off)| is
+// an f16 integer.
+QH_DEV qh_f16x8 qg_cvt8(uint32_t w0, uint32_t w1, qh_f16x2 scv, qh_f16x2 cv) {
+    qh_f16x8 o;
+    const qh_f16x2 a = __builtin_elementwise_fma(qg_b2h(w0, QG_SEL01), scv, cv);
+    const qh_f16x2 b = __builtin_elementwise_fma(qg_b2h(w0, QG_SEL23), scv, cv);
+    const qh_f16x2 c = __builtin_elementwise_fma(qg_b2h(w1, QG_SEL01), scv, cv);
+    const qh_f16x2 d = __builtin_elementwise_fma(qg_b2h(w1, QG_SEL23), scv, cv);
+    o[0] = a[0]; o[1] = a[1]; o[2] = b[0]; o[3] = b[1];
+    o[4] = c[0]; o[5] = c[1]; o[6] = d[0]; o[7] = d[1];
+    return o;
+}
 
 // ---------------------------------------------------------------- formats
+// Each format gives BYTES, CH (16-byte slices staged per row and superblock,
+// the last from byte LAST), RS (LDS line per row), the header decoded once per
+// group (hdr: d, dmin, scales) and bop<J>: lane half hh's B operand of K-block
+// J (weights 16 J + 8 hh .. + 7 of the lane's row) from the staged line r.
 
 // Q4_K (src/dequant.rs:1471-1519): sub-block sb = 2p + nibble uses qs[32p + l].
 struct GQ4K {
     static constexpr int BYTES = 144, CH = 9, RS = 144, LAST = 128;
-    static constexpr int SUMK = 32, SUMSH = 5;  // x sums over 32 (the mins' pieces)
     static constexpr bool SUMS = true;
-    static constexpr int KIND = 0, GRID = 0;  // sub-block pairs from one qs load
+    static constexpr int GRID = 0;
     struct H { uint32_t sc0, sc1, mn0, mn1; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         const qh_u32x4 h = *reinterpret_cast<const qh_u32x4*>(r);
@@ -59,56 +98,54 @@ struct GQ4K {
         o.dm = qh_f16_hi(h.x);
         return o;
     }
-    // B operands of sub-blocks 2p, 2p+1 for lane half hh (k = 16 hh + e).
-    template <int P>
-    static QH_DEV void bpair(const unsigned char* r, int hh, qh_i32x4& b0, qh_i32x4& b1) {
-        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 16 + 32 * P + 16 * hh);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            b0[i] = (int)(q[i] & 0x0F0F0F0Fu);
-            b1[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
-        }
+    template <int J>
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H& h, const unsigned char*) {
+        constexpr int sb = J >> 1, jj = J & 1, p = sb >> 1, nib = sb & 1;
+        const qh_u32x2 w = *reinterpret_cast<const qh_u32x2*>(r + 16 + 32 * p + 16 * jj + 8 * hh);
+        const uint32_t q0 = nib ? (w.x >> 4) & 0x0F0F0F0Fu : w.x & 0x0F0F0F0Fu;
+        const uint32_t q1 = nib ? (w.y >> 4) & 0x0F0F0F0Fu : w.y & 0x0F0F0F0Fu;
+        const qh_f16x2 scv = qg_dup(sb < 4 ? h.sc0 : h.sc1, sb & 3, (_Float16)1024.0f);
+        return qg_cvt8(q0, q1, scv, scv * (_Float16)-1024.0f);
     }
-    template <int SB>
-    static QH_DEV int scl(const H& h) { return (int)(((SB < 4 ? h.sc0 : h.sc1) >> (8 * (SB & 3))) & 0xFFu); }
-    // B operand of the sums MFMA: the 8 mins in k = 0..7 (lanes of half 0).
-    static QH_DEV qh_i32x4 bmin(const unsigned char*, const H& h, int hh) {
-        return hh == 0 ? qh_i32x4{(int)h.mn0, (int)h.mn1, 0, 0} : qh_i32x4{0, 0, 0, 0};
+    // B operand of the mins MFMA for lane half hh: mins 4 hh .. 4 hh + 3, each
+    // twice (for the hi and lo parts of the x sums)
+    static QH_DEV qh_f16x8 minh(const H& h, int hh) {
+        const uint32_t m = hh ? h.mn1 : h.mn0;
+        const qh_f16x2 a = qg_dup(m, 0, (_Float16)1024.0f), b = qg_dup(m, 1, (_Float16)1024.0f);
+        const qh_f16x2 c = qg_dup(m, 2, (_Float16)1024.0f), d = qg_dup(m, 3, (_Float16)1024.0f);
+        return qh_f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
     }
 };
 
 // Q5_K (src/dequant.rs:1146-1182): as Q4_K plus bit sb of qh[l] as bit 4.
 struct GQ5K {
     static constexpr int BYTES = 176, CH = 11, RS = 176, LAST = 160;
-    static constexpr int SUMK = 32, SUMSH = 5;
     static constexpr bool SUMS = true;
-    static constexpr int KIND = 0, GRID = 0;
+    static constexpr int GRID = 0;
     using H = GQ4K::H;
     static QH_DEV H hdr(const unsigned char* r) { return GQ4K::hdr(r); }
-    template <int P>
-    static QH_DEV void bpair(const unsigned char* r, int hh, qh_i32x4& b0, qh_i32x4& b1) {
-        const qh_u32x4 q = *reinterpret_cast<const qh_u32x4*>(r + 48 + 32 * P + 16 * hh);
-        const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 16 + 16 * hh);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t v = u[i] >> (2 * P);
-            b0[i] = (int)((q[i] & 0x0F0F0F0Fu) | ((v & 0x01010101u) << 4));
-            b1[i] = (int)(((q[i] >> 4) & 0x0F0F0F0Fu) | ((v & 0x02020202u) << 3));
-        }
+    template <int J>
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H& h, const unsigned char*) {
+        constexpr int sb = J >> 1, jj = J & 1, p = sb >> 1, nib = sb & 1;
+        const qh_u32x2 w = *reinterpret_cast<const qh_u32x2*>(r + 48 + 32 * p + 16 * jj + 8 * hh);
+        const qh_u32x2 u = *reinterpret_cast<const qh_u32x2*>(r + 16 + 16 * jj + 8 * hh);
+        const uint32_t q0 = (nib ? (w.x >> 4) & 0x0F0F0F0Fu : w.x & 0x0F0F0F0Fu) | (((u.x >> sb) & 0x01010101u) << 4);
+        const uint32_t q1 = (nib ? (w.y >> 4) & 0x0F0F0F0Fu : w.y & 0x0F0F0F0Fu) | (((u.y >> sb) & 0x01010101u) << 4);
+        const qh_f16x2 scv = qg_dup(sb < 4 ? h.sc0 : h.sc1, sb & 3, (_Float16)1024.0f);
+        return qg_cvt8(q0, q1, scv, scv * (_Float16)-1024.0f);
     }
-    template <int SB>
-    static QH_DEV int scl(const H& h) { return GQ4K::scl<SB>(h); }
-    static QH_DEV qh_i32x4 bmin(const unsigned char* r, const H& h, int hh) { return GQ4K::bmin(r, h, hh); }
+    static QH_DEV qh_f16x8 minh(const H& h, int hh) { return GQ4K::minh(h, hh); }
 };
 
-// Q6_K (src/dequant.rs:1583-1631): chunk c = 4 half + quarter covers 32
-// consecutive weights: ql[64 half + 32 (quarter&1) + l] nibble quarter>>1, qh[32
-// half + l] bits 2 quarter..; scales 2c (l < 16) and 2c + 1 (l >= 16).
+// Q6_K (src/dequant.rs:1583-1631): weight 128 h + 32 k + l (h < 2, k < 4, l <
+// 32) is ql[64 h + 32 (k & 1) + l] nibble k >> 1 with bits 2k, 2k+1 of qh[32 h
+// + l] on top, minus 32, times sc[(128 h + 32 k + l) / 16].  K-block J = 8 h + 2 k
+// + l / 16.  The line is staged with its last slice from byte 194, so d sits at
+// 222 in LDS.
 struct GQ6K {
-    static constexpr int BYTES = 210, CH = 14, RS = 240, LAST = 194;  // d lands at 222
-    static constexpr int SUMK = 16, SUMSH = 4;
-    static constexpr bool SUMS = false;  // the -32 is in the B operand
-    static constexpr int KIND = 2, GRID = 0;  // two scales per 32 weights
+    static constexpr int BYTES = 210, CH = 14, RS = 240, LAST = 194;
+    static constexpr bool SUMS = false;
+    static constexpr int GRID = 0;
     struct H { qh_u32x4 s; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) {
         H o;
@@ -117,93 +154,89 @@ struct GQ6K {
         o.dm = 0.f;
         return o;
     }
-    template <int C>
-    static QH_DEV qh_i32x4 bop(const unsigned char* r, int hh) {
-        constexpr int half = C >> 2, qu = C & 3;
-        const qh_u32x4 l = *reinterpret_cast<const qh_u32x4*>(r + 64 * half + 32 * (qu & 1) + 16 * hh);
-        const qh_u32x4 u = *reinterpret_cast<const qh_u32x4*>(r + 128 + 32 * half + 16 * hh);
-        qh_i32x4 b;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            // q in 0..63 per byte; (q + 0x60) ^ 0x80 is q - 32 as a signed byte (no carries)
-            b[i] = (int)(((((l[i] >> (4 * (qu >> 1))) & 0x0F0F0F0Fu) | (((u[i] >> (2 * qu)) & 0x03030303u) << 4)) +
-                          0x60606060u) ^ 0x80808080u);
-        return b;
+    template <int J>
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H& h, const unsigned char*) {
+        constexpr int hf = J >> 3, k = (J >> 1) & 3, l0 = 16 * (J & 1);
+        const qh_u32x2 ql = *reinterpret_cast<const qh_u32x2*>(r + 64 * hf + 32 * (k & 1) + l0 + 8 * hh);
+        const qh_u32x2 qh = *reinterpret_cast<const qh_u32x2*>(r + 128 + 32 * hf + l0 + 8 * hh);
+        const uint32_t q0 = ((ql.x >> (4 * (k >> 1))) & 0x0F0F0F0Fu) | (((qh.x >> (2 * k)) & 0x03030303u) << 4);
+        const uint32_t q1 = ((ql.y >> (4 * (k >> 1))) & 0x0F0F0F0Fu) | (((qh.y >> (2 * k)) & 0x03030303u) << 4);
+        // the signed scale as an f16 pair: byte ^ 0x80 is sc + 128
+        const qh_f16x2 scv = qg_dup(h.s[J >> 2] ^ 0x80808080u, J & 3, (_Float16)1152.0f);
+        const qh_f16x2 m32 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+        const qh_f16x2 a = (qg_b2h(q0, QG_SEL01) + m32) * scv, b = (qg_b2h(q0, QG_SEL23) + m32) * scv;
+        const qh_f16x2 c = (qg_b2h(q1, QG_SEL01) + m32) * scv, d = (qg_b2h(q1, QG_SEL23) + m32) * scv;
+        return qh_f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
     }
-    template <int G>
-    static QH_DEV int scl(const H& h) { return ((int)(h.s[G >> 2] >> (8 * (G & 3))) << 24) >> 24; }
 };
 
-
-// IQ3_S and IQ2_XXS: the B operand of sub-block K, lane half hh, is the
-// qh_iq3s_piece / qh_iq2xxs_piece of the staged block (signed codebook bytes,
-// the dequantized value / (d scale) exactly), with the codebooks in LDS.
+// IQ3_S (src/dequant.rs:1184-1237) and IQ2_XXS (:1011-1041): K-block J is half
+// J & 1 of sub-block J >> 1; the lane's 8 weights are two codebook entries
+// (IQ3_S) or one (IQ2_XXS) with their signs, times the sub-block's odd scale.
+// Signed bytes b become f16 through b ^ 0x80 = b + 128, so c = -1152 sc.
 extern __device__ uint32_t qh_g_iq3s[512];
 extern __device__ uint64_t qh_g_iq2xxs[256];
 
 struct GIQ3S {
     static constexpr int BYTES = 110, CH = 7, RS = 112, LAST = 94;
-    static constexpr int SUMK = 32, SUMSH = 5;
     static constexpr bool SUMS = false;
-    static constexpr int KIND = 1, GRID = 1;  // one scale per 32 weights; IQ3S codebook in LDS
+    static constexpr int GRID = 1;
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{qh_h2f(qh_rd16(r, 0)), 0.f}; }
-    template <int K>
-    static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
-        uint32_t v[4];
-        qh_iq3s_piece(r, K, hh, reinterpret_cast<const uint32_t*>(grid), v, sc);
-#pragma unroll
-        for (int m = 0; m < 4; m++) b[m] = (int)v[m];
+    template <int J>
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* grid) {
+        constexpr int K = J >> 1, jj = J & 1;
+        const uint32_t* g32 = reinterpret_cast<const uint32_t*>(grid);
+        const uint32_t q = qh_rd16(r, 2 + 8 * K + 4 * jj + 2 * hh);                   // 2 grid indices
+        const uint32_t qh = (uint32_t)r[66 + K] >> (4 * jj + 2 * hh);                  // their 9th bits
+        const uint32_t sg = (uint32_t)r[qh_iq3s_at(74 + 4 * K + 2 * jj + hh)];         // 8 sign bits
+        const uint32_t b0 = qh_negbytes(g32[(q & 0xFFu) | ((qh & 1u) << 8)], qh_signmask4(sg));
+        const uint32_t b1 = qh_negbytes(g32[((q >> 8) & 0xFFu) | ((qh & 2u) << 7)], qh_signmask4(sg >> 4));
+        const int sc = 1 + 2 * (int)((r[qh_iq3s_at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
+        const qh_f16x2 scv = {(_Float16)sc, (_Float16)sc};
+        return qg_cvt8(b0 ^ 0x80808080u, b1 ^ 0x80808080u, scv, scv * (_Float16)-1152.0f);
     }
 };
 
 struct GIQ2XXS {
     static constexpr int BYTES = 66, CH = 5, RS = 80, LAST = 50;
-    static constexpr int SUMK = 32, SUMSH = 5;
     static constexpr bool SUMS = false;
-    static constexpr int KIND = 1, GRID = 2;  // IQ2XXS codebook in LDS
+    static constexpr int GRID = 2;
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{0.125f * qh_h2f(qh_rd16(r, 0)), 0.f}; }
-    template <int K>
-    static QH_DEV void bop(const unsigned char* r, int hh, const unsigned char* grid, qh_i32x4& b, int& sc) {
-        uint32_t v[4];
-        qh_iq2xxs_piece(r, K, hh, reinterpret_cast<const uint64_t*>(grid), v, sc);
-#pragma unroll
-        for (int m = 0; m < 4; m++) b[m] = (int)v[m];
+    template <int J>
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* grid) {
+        constexpr int K = J >> 1, jj = J & 1;
+        const uint64_t* g64 = reinterpret_cast<const uint64_t*>(grid);
+        const uint32_t idx = r[2 + 8 * K + 2 * jj + hh];
+        const uint32_t a1 = qh_rd16(r, qh_iq2xxs_at(6 + 8 * K)) | (qh_rd16(r, qh_iq2xxs_at(8 + 8 * K)) << 16);
+        const uint64_t g = g64[idx];
+        const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * jj + hh))) & 127u);
+        const uint32_t b0 = qh_negbytes((uint32_t)g, qh_signmask4(s8));
+        const uint32_t b1 = qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
+        const int sc = 2 * (int)(a1 >> 28) + 1;
+        const qh_f16x2 scv = {(_Float16)sc, (_Float16)sc};
+        return qg_cvt8(b0 ^ 0x80808080u, b1 ^ 0x80808080u, scv, scv * (_Float16)-1152.0f);
     }
 };
 
-template <class F>
-struct IsQ6 { static constexpr bool value = false; };
-template <>
-struct IsQ6<GQ6K> { static constexpr bool value = true; };
+// ---------------------------------------------------------------- x image in LDS
 
-// ---------------------------------------------------------------- x image
-
-// The x operand of one 256-element group for 16 token slots ("image"), written
-// once per call by qh_mmq_ximg and read by every workgroup with coalesced loads:
-// chunk c is the A operand of one MFMA, lane L's 16 bytes at 1024 c + 16 L
-// (lane L = row L % 32, k half L / 32 of the 32x32x32 MFMA).
-//   KIND 0 / 1 (one scale per 32 weights): chunk k < 8 = sub-block k, row 2t+m =
-//     digit m of token t; KIND 0 adds chunk 8, the sum digits of the 8
-//     sub-blocks (row 2t+m, k half 0, bytes 0..7).
-//   KIND 2 (Q6_K, scales per 16): chunk 8u+c = 32-weight chunk c for tokens
-//     8u..8u+7 (so <= 8 tokens need only chunks 0..7): row 2(t%8)+m takes k < 16, row 16 + 2(t%8)+m takes k >= 16, the
-//     other k half of each row is zero.
-// Then 16 bytes: the digit exponent s of each token slot (127: Inf/NaN seen).
-template <int KIND, bool SUMS>
+// The x operand of one 256-element group for 16 token slots, built in LDS by
+// the workgroup that reads it.  A-operand order of v_mfma_f32_32x32x16_f16:
+// lane L's 16 bytes are row L % 32, k = 8 (L / 32) .. + 7.
+//   XA: K-block j (16 weights) at 1024 j: row 2t + part holds token t's hi
+//     (part 0) or lo (part 1) f16 of elements 16 j + k.
+//   SUM (Q4_K / Q5_K): token t's sum of x over sub-block sb, times 2^(s - 5),
+//     as hi and lo f16, the A operand of the mins MFMA: row rho(t) = 8 (t >> 2)
+//     + 4 ((t >> 1) & 1) + (t & 1) (so its results land where token t's main
+//     results are), k = 8 (sb >> 2) + 2 (sb & 3) + part, stored at 16 (t + 16
+//     (sb >> 2)) + 2 (2 (sb & 3) + part).
+//   EXP: s of each token slot (127: x not finite).
+template <bool SUMS>
 struct XImg {
-    static constexpr int CHUNKS = KIND == 2 ? 16 : (SUMS ? 9 : 8);
-    static constexpr int EXP = 1024 * CHUNKS;
-    static constexpr int BYTES = EXP + 256;  // per group
+    static constexpr int SUM = 16384, EXP = SUMS ? 16896 : 16384, BYTES = EXP + 16;
 };
-#define QG_MAX_GROUPS 256                     // in_dim <= 65536 on the matrix-core path
-#define QG_SCRATCH (4 * QG_MAX_GROUPS * (16 * 1024 + 256))  // 16.6 MB: 4 slots at the largest in_dim
-static __device__ __align__(256) unsigned char qh_mmq_scratch[QG_SCRATCH];
-// Split-K partials (16 tokens x 32 rows per (tile, split)) and per-tile arrival
-// counters; every counter is back at zero when a launch ends.
-static __device__ __align__(256) float qh_mmq_part[QG_PART_TILES * 16 * 32];
-static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES];
 
 #define QG_MAXG 16  // matrices (or row chunks) per grouped launch
 struct QgXs {        // the distinct token blocks of one grouped launch
@@ -216,198 +249,91 @@ struct QgGroups {    // the matrices of one grouped launch
     float* y[QG_MAXG];
     uint32_t wbytes[QG_MAXG];  // buffer range of each matrix's weights
     int rows[QG_MAXG];
-    int n[QG_MAXG];            // tokens of the matrix's x block
     int ldy[QG_MAXG];          // y token stride
-    int slot[QG_MAXG];         // x image slot
+    int slot[QG_MAXG];         // x block (QgXs entry)
     int bstart[QG_MAXG + 1];   // first workgroup of each matrix; entries past the count are INT_MAX
     int accum;                 // y += result (the residual add) instead of y = result
 };
-
-// One workgroup (256 threads) per group: thread T digitises elements 16 (T%16)
-// .. +15 of token T/16 (zeros past n), building the image in LDS, then copies it
-// out.  Digits: fmaf(x, 2^s, 12615808) = 1.5 * 2^23 + 0x8080 + n with n =
-// round(x 2^s), |n| <= 2^14 (s = 14 - exponent of the token's max |x| over the
-// group), so the float's low bytes XOR 0x80 are the balanced digits of n.
-// Sums: exact integer sums of n over each sub-block, in units of 2^SUMSH.
-// Grid (groups, slots): slot s digitises the n[s] tokens at x[s] into image
-// slot s (img + s * ngroups * XI::BYTES).
-template <int KIND, bool SUMS, int SUMSH>
-__global__ __launch_bounds__(256) void qh_mmq_ximg(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
-    using XI = XImg<KIND, SUMS>;
-    __shared__ __align__(16) unsigned char im[XI::BYTES];
-    const int T = threadIdx.x, g = blockIdx.x;
-    const float* __restrict__ x = xs.x[blockIdx.y];
-    const int n = xs.n[blockIdx.y];
-    img += (size_t)blockIdx.y * gridDim.x * XI::BYTES;
-    const int t = T >> 4, p = T & 15;
-    for (int i = 16 * T; i < XI::BYTES; i += 16 * 256) *reinterpret_cast<qh_u32x4*>(im + i) = qh_u32x4{0, 0, 0, 0};
-    __syncthreads();  // the zero fill lands before any thread's image writes
-    float4 v[4];
-    const QhBuf xb = qh_buf(x, 4u * (uint32_t)n * (uint32_t)in_dim);
-    const uint32_t off = t < n ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)g + 16u * p) : 0x80000000u;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const qh_u32x4 u = qh_ld128(xb, off + 16u * i);
-        v[i] = float4{__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
-    }
-    if (const float* x2 = xs.x2[blockIdx.y]) {
-        // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
-        const QhBuf ub = qh_buf(x2, 4u * (uint32_t)n * (uint32_t)in_dim);
-        auto sw = [](float gv, float uv) { return (gv / (1.f + expf(-gv))) * uv; };
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const qh_u32x4 u = qh_ld128(ub, off + 16u * i);
-            v[i] = float4{sw(v[i].x, __uint_as_float(u.x)), sw(v[i].y, __uint_as_float(u.y)),
-                          sw(v[i].z, __uint_as_float(u.z)), sw(v[i].w, __uint_as_float(u.w))};
-        }
-    }
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-    // max over the 16 threads (one DPP row) of the token
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
-    int e = 0;
-    (void)frexpf(m, &e);
-    int s = m > 0.f ? 14 - e : 0;
-    s = s > 126 ? 126 : (s < -126 ? -126 : s);
-    const float scx = ldexpf(1.0f, s);
-    uint32_t a[16];
-    uint32_t hi_or = 0, sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        a[4 * i + 0] = __float_as_uint(fmaf(v[i].x, scx, 12615808.0f));
-        a[4 * i + 1] = __float_as_uint(fmaf(v[i].y, scx, 12615808.0f));
-        a[4 * i + 2] = __float_as_uint(fmaf(v[i].z, scx, 12615808.0f));
-        a[4 * i + 3] = __float_as_uint(fmaf(v[i].w, scx, 12615808.0f));
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        hi_or |= (a[i] >> 16) ^ 0x4B40u;  // nonzero iff a value was not finite (or out of range)
-        sum += a[i];
-    }
-    // 16 bytes of digit m, in element order
-    qh_u32x4 d0, d1;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t t01 = __builtin_amdgcn_perm(a[4 * i + 1], a[4 * i], 0x05010400u);
-        const uint32_t t23 = __builtin_amdgcn_perm(a[4 * i + 3], a[4 * i + 2], 0x05010400u);
-        d0[i] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
-        d1[i] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
-    }
-    const int c32 = p >> 1, kh = p & 1;  // 32-element piece of the group, k half
-    if constexpr (KIND == 2) {
-        const int u = t >> 3, r = 16 * kh + 2 * (t & 7);
-        *reinterpret_cast<qh_u32x4*>(im + 1024 * (8 * u + c32) + 16 * (32 * kh + r)) = d0;
-        *reinterpret_cast<qh_u32x4*>(im + 1024 * (8 * u + c32) + 16 * (32 * kh + r + 1)) = d1;
-    } else {
-        *reinterpret_cast<qh_u32x4*>(im + 1024 * c32 + 16 * (32 * kh + 2 * t)) = d0;
-        *reinterpret_cast<qh_u32x4*>(im + 1024 * c32 + 16 * (32 * kh + 2 * t + 1)) = d1;
-    }
-    if constexpr (SUMS) {
-        // integer sum of n over the sub-block (this thread and its neighbour)
-        sum += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)sum, 0xB1, 0xF, 0xF, false);
-        if (kh == 0) {
-            const int sn = (int)(sum - 32u * 0x4B408080u);
-            const int ns = (sn + (1 << (SUMSH - 1))) >> SUMSH;
-            const uint32_t uu = (uint32_t)(ns + 0x8080);
-            im[1024 * 8 + 16 * (2 * t) + c32] = (unsigned char)((uu & 0xFFu) ^ 0x80u);
-            im[1024 * 8 + 16 * (2 * t + 1) + c32] = (unsigned char)(((uu >> 8) & 0xFFu) ^ 0x80u);
-        }
-    }
-    // the token's non-finite flag, over its 16 threads
-    uint32_t f = hi_or;
-    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0xB1, 0xF, 0xF, false);
-    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x4E, 0xF, 0xF, false);
-    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x141, 0xF, 0xF, false);
-    f |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)f, 0x140, 0xF, 0xF, false);
-    __syncthreads();
-    if (p == 0) im[XI::EXP + t] = (unsigned char)(signed char)(f ? 127 : s);
-    __syncthreads();
-    unsigned char* dst = img + (size_t)g * XI::BYTES;
-    for (int i = 16 * T; i < XI::BYTES; i += 16 * 256)
-        *reinterpret_cast<qh_u32x4*>(dst + i) = *reinterpret_cast<const qh_u32x4*>(im + i);
-}
+// Split-K partials (per (row block, split): W wavefronts x TPW tiles x 16 tokens
+// x 32 rows)
+// and per-(block, wavefront) arrival counters; every counter is back at zero
+// when a launch ends.
+#define QG_PART_FLOATS (8 * 1024 * 1024)
+static __device__ __align__(256) float qh_mmq_part[QG_PART_FLOATS];
+static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVES];
 
 // ---------------------------------------------------------------- kernel
 
-QH_DEV qh_i32x4 qh_as_i32x4(const qh_u32x4& v) { return qh_i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w}; }
+QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<const qh_u32x4*>(p); }
 
-// One workgroup of W wavefronts per (row tile of 32 rows, K split): wavefront w
-// takes the split's groups w, w + W, ...  Per group ("item") it stages the tile's
-// weight slices through its LDS tile (coalesced 16-byte loads, the next item's
-// in flight during the compute) and loads the group's x image straight into
-// the A-operand registers (L2-resident, issued before the weights are staged).
-// The wavefronts' partials meet in LDS at the end; with more than one split,
-// each split stores its partial tile to `part` and the last split to arrive
-// (per-tile counter in `cnt`) adds the splits in order 0, 1, ... and writes y,
-// so the result does not depend on which split finishes last.
-template <class F, int NT, int W>
-__global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const unsigned char* __restrict__ img,
-                                                 uint32_t row_bytes, int ngroups, int splits,
-                                                 float* __restrict__ part, unsigned int* __restrict__ cnt) {
+// One workgroup of W wavefronts per (row block of 32 W TPW rows, K split of at
+// most QG_GMAX groups).  The workgroup first builds the split's x images in LDS
+// (16 threads, one DPP row, per token and group; one barrier), then wavefront w
+// streams the weights of its TPW 32-row tiles (items: group by group, tile by
+// tile) through its own LDS tile (coalesced 16-byte loads, QG_NBUF items in
+// flight in register sets, the first ones while x is digitised) and reads its A
+// operands from the shared images.  A wavefront's results belong to its own
+// rows, so no reduction over wavefronts is needed, and split-K partials are
+// combined per wavefront (see the end).
+template <class F, int NT, int W, int TPW>
+__global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
+                                                 int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
-    constexpr int NH = (32 * CH + 63) / 64;  // 16-byte loads per lane per group
+    constexpr int NH = (32 * CH + 63) / 64;  // 16-byte weight loads per lane per group
     constexpr int TILE = 32 * RS + 16;
-    static_assert(NT == 2 || NT == 4 || NT == 8 || NT == 16, "NT");
-    static_assert(TILE >= NT * 32 * 4, "the wavefront partials reuse the staging tile");
-    using XI = XImg<F::KIND, F::SUMS>;
-    // Image chunks this kernel reads: Q6_K with <= 8 tokens needs only u = 0.
-    constexpr int NC = (F::KIND == 2) ? (NT > 8 ? 16 : 8) : XI::CHUNKS;
+    static_assert(NT == 4 || NT == 8 || NT == 16, "NT");
+    using XI = XImg<F::SUMS>;
+    constexpr int NQ = NT / 4;                 // slot quads (tokens 4q .. 4q + 3)
     constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
-    __shared__ __align__(16) unsigned char lds[W * TILE + GRIDB];
-    __shared__ int last_split;
+    __shared__ __align__(16) unsigned char lds[QG_GMAX * XI::BYTES + W * TILE + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
-    unsigned char* wl = lds + w * TILE;
-    unsigned char* gridl = lds + W * TILE;
+    unsigned char* wl = lds + QG_GMAX * XI::BYTES + w * TILE;
+    unsigned char* gridl = lds + QG_GMAX * XI::BYTES + W * TILE;
     if constexpr (F::GRID != 0) {
         const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
-        __syncthreads();
     }
-    // This workgroup's matrix (uniform), row tile and K split.  Every matrix's
+    // This workgroup's matrix (uniform), row block and K split.  Every matrix's
     // workgroups start at a multiple of `splits`, so blockIdx / splits is a
-    // launch-wide tile index (for the split counters and partials).
+    // launch-wide block index (for the split counters and partials).
     int gi = 0;
 #pragma unroll
     for (int k = 1; k < QG_MAXG; k++) gi += (int)blockIdx.x >= gs.bstart[k];
-    const int out_dim = gs.rows[gi], n = gs.n[gi], ldy = gs.ldy[gi];
+    const int out_dim = gs.rows[gi], slot = gs.slot[gi], ldy = gs.ldy[gi];
+    const int n = xs.n[slot];
     float* __restrict__ y = gs.y[gi];
     const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
-    const QhBuf ib = qh_buf(img + (size_t)gs.slot[gi] * ngroups * XI::BYTES, (uint32_t)ngroups * XI::BYTES);
+    const int ngroups = in_dim >> 8;
     const int lb = blockIdx.x - gs.bstart[gi];
-    const int tile = lb / splits, sp = lb - tile * splits, gt = blockIdx.x / splits;
+    const int blk = lb / splits, sp = lb - blk * splits, gblk = blockIdx.x / splits;
+    const int tile0 = (blk * W + w) * TPW;  // this wavefront's tiles tile0 .. tile0 + TPW - 1
     const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
+    const int nk = g1 - g0;
 
-    // Weight slices of this lane: row rr[h] of the tile, byte offset goff[h] from
-    // the tile's first row, LDS offset soff[h] (lanes past 32 * CH: spare bytes).
-    uint32_t goff[NH], soff[NH];
+    // Weight slices of this lane: row q / CH of a tile, slice q % CH, byte
+    // offset goff[h] in tile tile0 (tile tile0 + tt is 32 tt rows further), LDS
+    // offset soff[h] (lanes past 32 * CH: the spare 16 bytes at the tile's end);
+    // bit h TPW + tt of okb: the slice's row exists in tile tile0 + tt.
+    uint32_t goff[NH], soff[NH], okb = 0;
 #pragma unroll
     for (int h = 0; h < NH; h++) {
         const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
-        const bool ok = q < 32 * CH && tile * 32 + r < out_dim;
-        goff[h] = ok ? (uint32_t)(tile * 32 + r) * row_bytes + (c == CH - 1 ? F::LAST : 16u * c) : 0x80000000u;
+#pragma unroll
+        for (int tt = 0; tt < TPW; tt++)
+            okb |= (q < 32 * CH && (tile0 + tt) * 32 + r < out_dim) ? 1u << (h * TPW + tt) : 0u;
+        goff[h] = (uint32_t)(tile0 * 32 + r) * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
     }
-    auto load_w = [&](int g, qh_u32x4* wo) {
-        const uint32_t go = g < g1 ? (uint32_t)F::BYTES * (uint32_t)g : 0x80000000u;
+    // item i = (group g0 + i / TPW, tile tile0 + i % TPW)
+    auto load_w = [&](int i, qh_u32x4* wo) {
+        const int g = g0 + i / TPW, tt = i % TPW;
+        const uint32_t go = (uint32_t)F::BYTES * (uint32_t)g + (uint32_t)(32 * tt) * row_bytes;
 #pragma unroll
-        for (int h = 0; h < NH; h++) wo[h] = qh_ld128(wb, goff[h] + go);
+        for (int h = 0; h < NH; h++)
+            wo[h] = qh_ld128(wb, (g < g1 && ((okb >> (h * TPW + tt)) & 1u)) ? goff[h] + go : 0x80000000u);
     };
-    // The group's image chunks (1 KB each, coalesced) and its exponents.
-    // Lanes whose A row holds a token slot >= NT load nothing (out of range: zeros).
-    const bool xrow = F::KIND == 2 ? ((R & 15) >> 1) < NT : (R >> 1) < NT;
-    auto load_x = [&](int g, qh_u32x4* xo, qh_u32x4& eo) {
-        const uint32_t base = (uint32_t)g * XI::BYTES;
-        const uint32_t lb = xrow ? base + 16u * lane : 0x80000000u;
-#pragma unroll
-        for (int c = 0; c < NC; c++) xo[c] = qh_ld128(ib, lb + 1024u * c);
-        eo = qh_ld128(ib, base + XI::EXP);
-    };
-    auto stage = [&](const qh_u32x4* wr) {
+    auto stage_w = [&](const qh_u32x4* wr) {
 #pragma unroll
         for (int h = 0; h < NH; h++) *reinterpret_cast<qh_u32x4*>(wl + soff[h]) = wr[h];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -415,169 +341,196 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const unsign
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // Token slots of this lane: t = 4q + 2hh + r (q < 4, r < 2); result register
-    // 4q + 2r + m of a 16-token MFMA holds digit m of slot (q, r).
-    float tot[8];
+    // ---- x of the split -> LDS images.  16 threads (one DPP row) per token
+    // and group, 16 consecutive elements each; pass p covers (group, token)
+    // pairs p 4W .. All x loads go out first, then the wavefront's first two
+    // weight groups; only the x loads are waited for.
+    constexpr int NPASS = (4 * QG_GMAX + W - 1) / W;
+    const int u = lane & 15;
+    float4 xv[NPASS][4];
+    {
+        const float* xp = xs.x[slot];
+        const float* x2p = xs.x2[slot];
+        const QhBuf xb = qh_buf(xp, 4u * (uint32_t)n * (uint32_t)in_dim);
+        const QhBuf ub = qh_buf(x2p, 4u * (uint32_t)n * (uint32_t)in_dim);
 #pragma unroll
-    for (int i = 0; i < 8; i++) tot[i] = 0.f;
-    const unsigned char* wrow = wl + R * RS;
+        for (int pp = 0; pp < NPASS; pp++) {
+            const int idx = pp * 64 * W + threadIdx.x, k = idx >> 8, t = (idx >> 4) & 15;
+            const uint32_t off = (k < nk && t < n)
+                                     ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)(g0 + k) + 16u * u)
+                                     : 0x80000000u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const qh_u32x4 v = qh_ld128(xb, off + 16u * i);
+                xv[pp][i] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+            }
+            if (x2p) {
+                // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
+                auto sw = [](float gv, float uv) { return (gv / (1.f + expf(-gv))) * uv; };
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const qh_u32x4 v = qh_ld128(ub, off + 16u * i);
+                    xv[pp][i] = float4{sw(xv[pp][i].x, __uint_as_float(v.x)), sw(xv[pp][i].y, __uint_as_float(v.y)),
+                                       sw(xv[pp][i].z, __uint_as_float(v.z)), sw(xv[pp][i].w, __uint_as_float(v.w))};
+                }
+            }
+        }
+    }
+    // The first QG_NBUF groups' weights stay in flight while x is digitised.
+    // They are issued after every wavefront's x loads (an execution barrier,
+    // no memory fence): queued behind the weight loads of other wavefronts,
+    // the x loads would return several microseconds later.
+    qh_u32x4 wr[QG_NBUF][NH];
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int pp = 0; pp < NPASS; pp++) {
+        const int idx = pp * 64 * W + threadIdx.x, k = idx >> 8, t = (idx >> 4) & 15;
+        if (k < nk) {  // uniform per DPP row
+            unsigned char* im = lds + k * XI::BYTES;
+            float m = 0.f, sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = xv[pp][i];
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                sum += (v.x + v.y) + (v.z + v.w);
+            }
+            // max over the row's 16 lanes
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
+            int e = 0;
+            (void)frexpf(m, &e);
+            int s = m > 0.f ? 14 - e : 0;
+            s = s > 126 ? 126 : (s < -126 ? -126 : s);
+            const float scx = ldexpf(1.0f, s);
+            // hi and lo f16 (round toward zero: hi = rtz(x'), lo = rtz(x' - hi),
+            // 22 bits) of the 16 elements: K-block u, k halves 0 and 1
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float4 va = xv[pp][2 * c], vb = xv[pp][2 * c + 1];
+                const float v8[8] = {va.x * scx, va.y * scx, va.z * scx, va.w * scx,
+                                     vb.x * scx, vb.y * scx, vb.z * scx, vb.w * scx};
+                uint32_t hi4[4], lo4[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const auto hp = __builtin_amdgcn_cvt_pkrtz(v8[2 * i], v8[2 * i + 1]);
+                    const auto lp = __builtin_amdgcn_cvt_pkrtz(v8[2 * i] - (float)hp[0], v8[2 * i + 1] - (float)hp[1]);
+                    hi4[i] = __builtin_bit_cast(uint32_t, hp);
+                    lo4[i] = __builtin_bit_cast(uint32_t, lp);
+                }
+                *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * t + 32 * c)) =
+                    qh_u32x4{hi4[0], hi4[1], hi4[2], hi4[3]};
+                *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * t + 1 + 32 * c)) =
+                    qh_u32x4{lo4[0], lo4[1], lo4[2], lo4[3]};
+            }
+            // this lane's 16 elements and its neighbour's: sub-block u / 2; an
+            // Inf or NaN anywhere makes the row's sums non-finite
+            sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+            float chk = sum;
+            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x4E, 0xF, 0xF, false));
+            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x141, 0xF, 0xF, false));
+            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x140, 0xF, 0xF, false));
+            const bool fb = !__builtin_isfinite(chk);
+            if constexpr (F::SUMS) {
+                const float s5 = sum * ldexpf(1.0f, s - 5);
+                const auto p5 = __builtin_amdgcn_cvt_pkrtz(s5, 0.f);
+                const auto q5 = __builtin_amdgcn_cvt_pkrtz(s5 - (float)p5[0], 0.f);
+                const int sb = u >> 1;
+                if ((u & 1) == 0) {
+                    _Float16* sp = reinterpret_cast<_Float16*>(im + XI::SUM + 16 * (t + 16 * (sb >> 2))) + 2 * (sb & 3);
+                    sp[0] = p5[0];
+                    sp[1] = q5[0];
+                }
+            }
+            if (u == 0) im[XI::EXP + t] = (unsigned char)(signed char)(fb ? 127 : s);
+        }
+    }
+    __syncthreads();  // images (and the codebook) visible to every wavefront
 
-    auto compute = [&](const qh_u32x4& ex, const qh_u32x4* xa) {
+    // Result slots of this lane: slot (q, r) of tile tt is token t = 4q + 2hh + r
+    // of the tile's row R.
+    float tot[TPW][2 * NQ];
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+        for (int i = 0; i < 2 * NQ; i++) tot[tt][i] = 0.f;
+    const unsigned char* wrow = wl + R * RS;
+    // compact index of this lane's row in the sums (rows rho(t))
+    const int cidx = 4 * (R >> 3) + 2 * ((R >> 2) & 1) + (R & 1) + 16 * hh;
+
+    auto compute = [&](const unsigned char* im, float* tot) {
         const typename F::H hd = F::hdr(wrow);
-        int acc[16];
-        int acc2[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) acc[j] = acc2[j] = 0;
-        if constexpr (F::KIND == 1) {
-            auto sub = [&](auto KC) {
-                constexpr int K = decltype(KC)::value;
-                qh_i32x4 b;
-                int sc;
-                F::template bop<K>(wrow, hh, gridl, b, sc);
-                const qh_i32x4 a = qh_as_i32x4(xa[K]);
-                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-#pragma unroll
-                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(sc, d[j]);
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            sub(std::integral_constant<int, 0>{});
-            sub(std::integral_constant<int, 1>{});
-            sub(std::integral_constant<int, 2>{});
-            sub(std::integral_constant<int, 3>{});
-            sub(std::integral_constant<int, 4>{});
-            sub(std::integral_constant<int, 5>{});
-            sub(std::integral_constant<int, 6>{});
-            sub(std::integral_constant<int, 7>{});
-        } else if constexpr (F::KIND == 0) {
-            auto pair = [&](auto PC) {
-                constexpr int P = decltype(PC)::value;
-                qh_i32x4 b0, b1;
-                F::template bpair<P>(wrow, hh, b0, b1);
-                const qh_i32x4 a0 = qh_as_i32x4(xa[2 * P]);
-                const qh_i32x4 a1 = qh_as_i32x4(xa[2 * P + 1]);
-                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                const qh_i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, z, 0, 0, 0);
-                const int s0 = F::template scl<2 * P>(hd);
-#pragma unroll
-                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(s0, d0[j]);
-                __builtin_amdgcn_sched_barrier(0);
-                const qh_i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, z, 0, 0, 0);
-                const int s1 = F::template scl<2 * P + 1>(hd);
-#pragma unroll
-                for (int j = 0; j < 4 * (NT < 4 ? 1 : NT / 4); j++) acc[j] += __mul24(s1, d1[j]);
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            pair(std::integral_constant<int, 0>{});
-            pair(std::integral_constant<int, 1>{});
-            pair(std::integral_constant<int, 2>{});
-            pair(std::integral_constant<int, 3>{});
-        } else {
-            auto chunk = [&](auto CC) {
-                constexpr int C = decltype(CC)::value;
-                const qh_i32x4 b = F::template bop<C>(wrow, hh);
-                const int slo = F::template scl<2 * C>(hd), shi = F::template scl<2 * C + 1>(hd);
-                const qh_i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                {
-                    const qh_i32x4 a = qh_as_i32x4(xa[C]);
-                    const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-#pragma unroll
-                    for (int j = 0; j < 8; j++) acc[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
-                }
-                if constexpr (NT > 8) {
-                    const qh_i32x4 a = qh_as_i32x4(xa[8 + C]);
-                    const qh_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-#pragma unroll
-                    for (int j = 0; j < 8; j++) acc2[j] += __mul24(slo, d[j]) + __mul24(shi, d[j + 8]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            chunk(std::integral_constant<int, 0>{});
-            chunk(std::integral_constant<int, 1>{});
-            chunk(std::integral_constant<int, 2>{});
-            chunk(std::integral_constant<int, 3>{});
-            chunk(std::integral_constant<int, 4>{});
-            chunk(std::integral_constant<int, 5>{});
-            chunk(std::integral_constant<int, 6>{});
-            chunk(std::integral_constant<int, 7>{});
-        }
-        // sums MFMA: the mins (Q4_K/Q5_K)
-        qh_i32x16 dm = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        qh_f32x16 c0 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        qh_f32x16 c1 = c0, dm = c0;
+        auto kb = [&](auto JC) {
+            constexpr int J = decltype(JC)::value;
+            const qh_f16x8 b = F::template bop<J>(wrow, hh, hd, gridl);
+            const qh_f16x8 a = __builtin_bit_cast(qh_f16x8, qh_lds128(im + 1024 * J + 16 * lane));
+            if constexpr (J & 1)
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+            else
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+        };
+        kb(std::integral_constant<int, 0>{});
+        kb(std::integral_constant<int, 1>{});
+        kb(std::integral_constant<int, 2>{});
+        kb(std::integral_constant<int, 3>{});
+        kb(std::integral_constant<int, 4>{});
+        kb(std::integral_constant<int, 5>{});
+        kb(std::integral_constant<int, 6>{});
+        kb(std::integral_constant<int, 7>{});
+        kb(std::integral_constant<int, 8>{});
+        kb(std::integral_constant<int, 9>{});
+        kb(std::integral_constant<int, 10>{});
+        kb(std::integral_constant<int, 11>{});
+        kb(std::integral_constant<int, 12>{});
+        kb(std::integral_constant<int, 13>{});
+        kb(std::integral_constant<int, 14>{});
+        kb(std::integral_constant<int, 15>{});
         if constexpr (F::SUMS) {
-            const qh_i32x4 as = qh_as_i32x4(xa[8]);
-            dm = __builtin_amdgcn_mfma_i32_32x32x32_i8(as, F::bmin(wrow, hd, hh), dm, 0, 0, 0);
+            const qh_f16x8 sv = __builtin_bit_cast(qh_f16x8, qh_lds128(im + XI::SUM + 16 * cidx));
+            dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, F::minh(hd, hh), dm, 0, 0, 0);
         }
-        // finish: slot (q, r) = token 4q + 2hh + r, exponent byte t of the image
+        // finish: slot (q, r) = token 4q + 2hh + r (rows 2t, 2t + 1: registers
+        // 4q + 2r, 4q + 2r + 1), exponent byte t of the image
+        const qh_u32x4 ex = qh_lds128(im + XI::EXP);
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+        for (int q = 0; q < NQ; q++)
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                if (4 * q >= NT) continue;  // slot beyond the tokens for both lane halves
                 const int t = 4 * q + 2 * hh + r;
                 const int se = ((int)(ex[t >> 2] << (24 - 8 * (t & 3)))) >> 24;
                 const float rs = se == 127 ? __builtin_nanf("") : ldexpf(1.0f, -se);
-                int i0, i1;
-                if constexpr (F::KIND != 2) {
-                    i0 = acc[4 * q + 2 * r];
-                    i1 = acc[4 * q + 2 * r + 1];
-                } else {
-                    // Q6_K: MFMA u = q/2 holds slot q in register 4 (q%2) + 2r + m
-                    const int* ap = (q < 2) ? acc : acc2;
-                    i0 = ap[4 * (q & 1) + 2 * r];
-                    i1 = ap[4 * (q & 1) + 2 * r + 1];
-                }
-                const float P = fmaf((float)i1, 256.0f, (float)i0);
-                if constexpr (F::SUMS) {
-                    const float Pm = fmaf((float)dm[4 * q + 2 * r + 1], 256.0f, (float)dm[4 * q + 2 * r]);
-                    tot[2 * q + r] += (hd.d * P - hd.dm * Pm * (float)(1 << F::SUMSH)) * rs;
-                } else {
+                const float P = (c0[4 * q + 2 * r] + c1[4 * q + 2 * r]) + (c0[4 * q + 2 * r + 1] + c1[4 * q + 2 * r + 1]);
+                if constexpr (F::SUMS)
+                    tot[2 * q + r] += (hd.d * P - hd.dm * 32.0f * dm[4 * q + r]) * rs;
+                else
                     tot[2 * q + r] += hd.d * P * rs;
-                }
             }
     };
 
-    // This wavefront's groups g0 + w + W j, j < nw, taken from j = rot on
-    // (rotating with the workgroup): workgroups that run together then read
-    // different groups' x images instead of all hitting the same L2 lines.
-    const int nw = g1 - g0 > w ? (g1 - g0 - w + W - 1) / W : 0;
-    const int rot = nw ? (int)(blockIdx.x % (unsigned)nw) : 0;
-    auto grp = [&](int k) { return k < nw ? g0 + w + W * (k + rot < nw ? k + rot : k + rot - nw) : g1; };
-    qh_u32x4 wr[NH], xr[NC], er;
-    load_w(grp(0), wr);
-    for (int k = 0; k < nw; k++) {
-        const int g = grp(k);
-        load_x(g, xr, er);
-        // Keep the x loads ahead of the stage's wait for the weights (left to
-        // itself the compiler issues them after it, exposing their latency).
-        __builtin_amdgcn_sched_barrier(0);
-        stage(wr);
-        load_w(grp(k + 1), wr);  // past the last group: all offsets out of range, no traffic
-        compute(er, xr);
-    }
-    // Wavefront partials -> this wavefront's staging tile (its own LDS), then
-    // the sum over wavefronts in order 0..W-1.
-    float* red = reinterpret_cast<float*>(wl);
+    // Item i in register set i % QG_NBUF, refilled with item i + QG_NBUF as
+    // soon as it is staged (past the split: out of range, no traffic).
+    static_assert(QG_NBUF % TPW == 0, "an item's tile is b % TPW");
+    const int nitems = nk * TPW;
+    for (int i0 = 0; i0 < nitems; i0 += QG_NBUF) {
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int t = 4 * q + 2 * hh + r;
-            if (t < NT) red[t * 32 + R] = tot[2 * q + r];
+        for (int b = 0; b < QG_NBUF; b++) {
+            if (i0 + b < nitems) {
+                stage_w(wr[b]);
+                load_w(i0 + b + QG_NBUF, wr[b]);
+                compute(lds + ((i0 + b) / TPW) * XI::BYTES, tot[b % TPW]);
+            }
         }
-    __syncthreads();
-    float v[(NT * 32 + 64 * W - 1) / (64 * W)];
-#pragma unroll
-    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
-        const int i = threadIdx.x + 64 * W * j;
-        float a = 0.f;
-        if (i < NT * 32) {
-#pragma unroll
-            for (int k = 0; k < W; k++) a += reinterpret_cast<const float*>(lds + k * TILE)[i];
-        }
-        v[j] = a;
     }
-    auto put = [&](int i, float a) {
-        const int t = i >> 5, row = tile * 32 + (i & 31);
+
+    // Results: this wavefront's 32 rows x NT tokens.
+    auto put = [&](int t, int row, float a) {
         if (t < n && row < out_dim) {
             float* yp = y + (size_t)t * ldy + row;
             *yp = gs.accum ? *yp + a : a;
@@ -585,74 +538,111 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const unsign
     };
     if (splits == 1) {
 #pragma unroll
-        for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
-            const int i = threadIdx.x + 64 * W * j;
-            if (i < NT * 32) put(i, v[j]);
-        }
+        for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+#pragma unroll
+                for (int r = 0; r < 2; r++) put(4 * q + 2 * hh + r, (tile0 + tt) * 32 + R, tot[tt][2 * q + r]);
         return;
     }
-    float* mine = part + (size_t)blockIdx.x * (NT * 32);
+    // Split K: each wavefront stores its partial (NT tokens x 32 rows), and the
+    // last of the splits' wavefronts for the same rows to arrive (counter per
+    // (block, wavefront)) adds the splits in order 0, 1, ... and writes y, so
+    // the result does not depend on which split finishes last.  Wavefronts do
+    // this independently, without workgroup barriers.
+    constexpr int PW = TPW * NT * 32;  // floats of one wavefront partial
+    const size_t wslot = (size_t)gblk * W + w;
+    float* mine = part + (wslot * splits + sp) * PW;
 #pragma unroll
-    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
-        const int i = threadIdx.x + 64 * W * j;
-        if (i < NT * 32) __hip_atomic_store(mine + i, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int t = 4 * q + 2 * hh + r;
+                __hip_atomic_store(mine + (tt * NT + t) * 32 + R, tot[tt][2 * q + r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
     // Agent-scope stores and loads of the partials reach the device's point of
     // coherence without writing back or invalidating whole L2s (which a
-    // release/acquire fence per workgroup would, at a cost measured in tens of
-    // microseconds per launch).  Every thread's stores have completed (vmcnt 0)
-    // before the barrier, and the counter is bumped only after it.
+    // release/acquire fence would, at a cost measured in tens of microseconds
+    // per launch).  This wavefront's stores have completed (vmcnt 0) before its
+    // counter moves.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last_split = __hip_atomic_fetch_add(&cnt[gt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     (unsigned)(splits - 1);
-    __syncthreads();
-    if (!last_split) return;
-    const float* tp = part + (size_t)gt * splits * (NT * 32);
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&cnt[wslot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
+    if (old != (unsigned)(splits - 1)) return;
+    // The partials are read with SC1 buffer loads (the coherence bit of an
+    // agent-scope load, so no stale L2 line of an earlier launch is seen),
+    // which unlike atomic loads issue back to back: every slot of 4 splits in
+    // flight at once, summed in split order.
+    const QhBuf pbuf = qh_buf(part, 4u * QG_PART_FLOATS);
+    const uint32_t bbase = 4u * (uint32_t)(wslot * splits * PW);
+    constexpr int NS = TPW * 2 * NQ;  // result slots per lane
+    float a[NS];
 #pragma unroll
-    for (int j = 0; j < (NT * 32 + 64 * W - 1) / (64 * W); j++) {
-        const int i = threadIdx.x + 64 * W * j;
-        if (i < NT * 32) {
-            float a = 0.f;
-            for (int k = 0; k < splits; k++)
-                a += __hip_atomic_load(tp + k * (NT * 32) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            put(i, a);
-        }
+    for (int i = 0; i < NS; i++) a[i] = 0.f;
+    for (int k0 = 0; k0 < splits; k0 += 4) {
+        uint32_t v[NS][4];
+#pragma unroll
+        for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int uu = 0; uu < 4; uu++) {
+                        const int t = 4 * q + 2 * hh + r;
+                        const uint32_t off = k0 + uu < splits
+                                                 ? bbase + 4u * (uint32_t)((k0 + uu) * PW + (tt * NT + t) * 32 + R)
+                                                 : 0x80000000u;
+                        v[(tt * NQ + q) * 2 + r][uu] = __builtin_amdgcn_raw_buffer_load_b32(pbuf.rs, (int)off, 0, 16);
+                    }
+#pragma unroll
+        for (int i = 0; i < NS; i++)
+#pragma unroll
+            for (int uu = 0; uu < 4; uu++)
+                if (k0 + uu < splits) a[i] += __uint_as_float(v[i][uu]);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(&cnt[gt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+                put(4 * q + 2 * hh + r, (tile0 + tt) * 32 + R, a[(tt * NQ + q) * 2 + r]);
+    if (lane == 0) __hip_atomic_store(&cnt[wslot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
-struct QgScratch { unsigned char* img; float* part; unsigned int* cnt; };
+struct QgScratch { float* part; unsigned int* cnt; };
 static const QgScratch* qh_mmq_scratch_ptrs() {
     static QgScratch ptrs[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     QgScratch& p = ptrs[dev];
-    if (!p.img) {
-        void *a = nullptr, *b = nullptr, *c = nullptr;
-        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qh_mmq_scratch)) != hipSuccess ||
-            hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) != hipSuccess ||
+    if (!p.part) {
+        void *b = nullptr, *c = nullptr;
+        if (hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) != hipSuccess ||
             hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) != hipSuccess)
             return nullptr;
-        p.part = static_cast<float*>(b);
         p.cnt = static_cast<unsigned int*>(c);
-        p.img = static_cast<unsigned char*>(a);
+        p.part = static_cast<float*>(b);
     }
     return &p;
 }
 
-// QUARTZ_HIP_MMQ_WAVES=4|8|16 forces the wavefronts per workgroup (tuning).
-static int qh_mmq_waves_env() {
+// QUARTZ_HIP_MMQ_TPW=1|2 forces the 32-row tiles per wavefront (tuning).
+static int qh_mmq_tpw_env() {
     static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMQ_WAVES");
+        const char* e = getenv("QUARTZ_HIP_MMQ_TPW");
         return e ? atoi(e) : 0;
     }();
     return v;
 }
 
-// QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row tile (tuning).
+// QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row block (tuning).
 static int qh_mmq_splits_env() {
     static const int v = [] {
         const char* e = getenv("QUARTZ_HIP_MMQ_SPLITS");
@@ -661,36 +651,26 @@ static int qh_mmq_splits_env() {
     return v;
 }
 
-template <class F, int NT, int W>
-static void launch_mmq(const QgGroups& gs, int wgs, int splits, const QgScratch& sc, uint32_t row_bytes, int ngroups,
-                       hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq<F, NT, W>), dim3((unsigned)wgs), dim3(64 * W), 0, st, gs, sc.img, row_bytes, ngroups,
-                       splits, sc.part, sc.cnt);
+template <class F, int NT, int TPW>
+static void launch_mmq(const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+                       uint32_t row_bytes, int in_dim, hipStream_t st) {
+    hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, TPW>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
+                       row_bytes, in_dim, splits, sc.part, sc.cnt);
 }
 
 template <class F, int NT>
-static void launch_mmq_w(int waves, const QgGroups& gs, int wgs, int splits, const QgScratch& sc, uint32_t row_bytes,
-                         int ngroups, hipStream_t st) {
-    if (waves == 16) launch_mmq<F, NT, 16>(gs, wgs, splits, sc, row_bytes, ngroups, st);
-    else if (waves == 8) launch_mmq<F, NT, 8>(gs, wgs, splits, sc, row_bytes, ngroups, st);
-    else launch_mmq<F, NT, 4>(gs, wgs, splits, sc, row_bytes, ngroups, st);
+static void launch_mmq_t(int tpw, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+                         uint32_t row_bytes, int in_dim, hipStream_t st) {
+    if (tpw == 2) launch_mmq<F, NT, 2>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq<F, NT, 1>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 template <class F>
-static void launch_mmq_nt(int nt, int waves, const QgGroups& gs, int wgs, int splits, const QgScratch& sc,
-                          uint32_t row_bytes, int ngroups, hipStream_t st) {
-    if (nt <= 2) launch_mmq_w<F, 2>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
-    else if (nt <= 4) launch_mmq_w<F, 4>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
-    else if (nt <= 8) launch_mmq_w<F, 8>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
-    else launch_mmq_w<F, 16>(waves, gs, wgs, splits, sc, row_bytes, ngroups, st);
-}
-
-// Bytes of one x image slot (all groups of in_dim) for a type's kernel.
-static size_t qg_slot_bytes(uint32_t type, int ngroups) {
-    const size_t per = type == QT_Q6_K ? XImg<2, false>::BYTES
-                       : (type == QT_IQ3_S || type == QT_IQ2_XXS) ? XImg<1, false>::BYTES
-                                                                  : XImg<0, true>::BYTES;
-    return per * (size_t)ngroups;
+static void launch_mmq_nt(int nt, int tpw, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
+                          const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
+    if (nt <= 4) launch_mmq_t<F, 4>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 8) launch_mmq_t<F, 8>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq_t<F, 16>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
@@ -701,15 +681,35 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
     int n, rows, ldy;
 };
 
-// One grouped launch pair: the prologue digitises every distinct token block
-// into its image slot, then the main kernel covers every entry's row tiles.
+// K splits per row block: the count s (at least 2 groups per split where K
+// allows, at most QG_GMAX, the groups whose x images fit in LDS) that
+// minimises the rounds of QG_TARGET_WGS workgroups times the groups each one
+// walks, the fewest splits on ties.
+static int qg_pick_splits(int blocks, int ngroups) {
+    const int smin = (ngroups + QG_GMAX - 1) / QG_GMAX;
+    int cap = ngroups / 2 > 1 ? ngroups / 2 : 1;
+    cap = cap > smin ? cap : smin;
+    int best = smin;
+    int64_t best_cost = INT64_MAX;
+    for (int s = smin; s <= cap; s++) {
+        const int64_t rounds = ((int64_t)blocks * s + QG_TARGET_WGS - 1) / QG_TARGET_WGS;
+        const int64_t cost = rounds * ((ngroups + s - 1) / s);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
+// One grouped launch: every entry's row blocks, each workgroup digitising its
+// own K split of its entry's x.
 static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, uint32_t row_bytes,
                          const QgScratch& sc, hipStream_t st, int accum) {
     const int ngroups = in_dim / 256;
-    const int waves = qh_mmq_waves_env() ? qh_mmq_waves_env() : QG_WAVES;
     QgXs xs = {};
     QgGroups gs = {};
-    int nslots = 0, ntmax = 0, tiles = 0;
+    int nslots = 0, ntmax = 0;
     for (int i = 0; i < cnt; i++) {
         int j = 0;
         while (j < nslots && !(xs.x[j] == en[i].x && xs.x2[j] == en[i].x2 && xs.n[j] == en[i].n)) j++;
@@ -723,46 +723,53 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         gs.y[i] = en[i].y;
         gs.wbytes[i] = (uint32_t)(((uint64_t)en[i].rows * row_bytes + 3) & ~(uint64_t)3);
         gs.rows[i] = en[i].rows;
-        gs.n[i] = en[i].n;
         gs.ldy[i] = en[i].ldy;
         gs.slot[i] = j;
         ntmax = en[i].n > ntmax ? en[i].n : ntmax;
-        tiles += (en[i].rows + 31) / 32;
     }
-    // K splits: enough workgroups to fill the chip (about QG_TARGET_WGS), at
-    // least one group per wavefront, and partials within the scratch.
+    // One 32-row tile per wavefront.  Two (512-row blocks, x digitised once
+    // for twice the weight rows) measured slower at every shape tried: 14336 x
+    // 4096 Q4_K at 16 tokens 25.0 us against 21.2, 4096 x 14336 Q6_K 38.6
+    // against 29.3; QUARTZ_HIP_MMQ_TPW=2 selects them.
+    const int tpw = qh_mmq_tpw_env() == 2 ? 2 : 1;
+    const int brows = 32 * QG_WAVES * tpw;
+    int blocks = 0;
+    for (int i = 0; i < cnt; i++) blocks += (en[i].rows + brows - 1) / brows;
+    const int smin = (ngroups + QG_GMAX - 1) / QG_GMAX;  // a split's images must fit in LDS
     int splits = qh_mmq_splits_env();
-    if (splits <= 0) {
-        splits = (QG_TARGET_WGS + tiles - 1) / tiles;
-        const int cap = ngroups / waves > 1 ? ngroups / waves : 1;
-        splits = splits < cap ? splits : cap;
-    }
+    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups);
     splits = splits < ngroups ? splits : ngroups;
-    if ((int64_t)tiles * splits > QG_PART_TILES) splits = QG_PART_TILES / tiles;
-    if (splits < 1) splits = 1;
+    splits = splits > smin ? splits : smin;
+    const int64_t pb = (int64_t)QG_WAVES * tpw * 16 * 32;  // floats of one partial block (16-token bound)
+    // The partials and the per-block counters must hold the launch: otherwise
+    // halve the batch (or, for one entry, its rows) and run the halves in turn.
+    if (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES)) {
+        if (cnt > 1) {
+            hipError_t e = qg_run(type, en, cnt / 2, in_dim, row_bytes, sc, st, accum);
+            return e != hipSuccess ? e : qg_run(type, en + cnt / 2, cnt - cnt / 2, in_dim, row_bytes, sc, st, accum);
+        }
+        const int half = (en[0].rows / 2 + brows - 1) / brows * brows;
+        QgEntry a = en[0], b = en[0];
+        a.rows = half;
+        b.rows = en[0].rows - half;
+        b.w += (size_t)half * row_bytes;
+        b.y += half;
+        hipError_t e = qg_run(type, &a, 1, in_dim, row_bytes, sc, st, accum);
+        return e != hipSuccess ? e : qg_run(type, &b, 1, in_dim, row_bytes, sc, st, accum);
+    }
     int wgs = 0;
     for (int i = 0; i < QG_MAXG; i++) {
         gs.bstart[i] = i < cnt ? wgs : INT_MAX;
-        if (i < cnt) wgs += (en[i].rows + 31) / 32 * splits;
+        if (i < cnt) wgs += (en[i].rows + brows - 1) / brows * splits;
     }
     gs.bstart[QG_MAXG] = INT_MAX;
     gs.accum = accum;
-
-    const dim3 pg((unsigned)ngroups, (unsigned)nslots);
-    if (type == QT_Q6_K)
-        hipLaunchKernelGGL((qh_mmq_ximg<2, false, 4>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
-    else if (type == QT_IQ3_S || type == QT_IQ2_XXS)
-        hipLaunchKernelGGL((qh_mmq_ximg<1, false, 5>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
-    else
-        hipLaunchKernelGGL((qh_mmq_ximg<0, true, 5>), pg, dim3(256), 0, st, xs, sc.img, in_dim);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     switch (type) {
-        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
-        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
-        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
-        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
-        default: launch_mmq_nt<GQ6K>(ntmax, waves, gs, wgs, splits, sc, row_bytes, ngroups, st); break;
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
     }
     return hipGetLastError();
 }
@@ -771,20 +778,19 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
 // in_dim: Y[i][t][:] = W[i] X[i][t][:] for t < n[i] (token-major, y token stride
 // out_dims[i]); hipErrorNotSupported when the type/shape has no kernel here.
 // Tokens go in chunks of up to 16 (one weight pass each); matrices whose
-// weights pass 2 GB go in row chunks.  Per launch, qh_mmq_ximg writes the x
-// images to the library's device scratch and qh_mmq reads them; the scratch is
+// weights pass 2 GB go in row chunks.  The split-K partials and counters are
 // one array per device, so calls that overlap on one device (different
 // streams) must be serialised by the caller.
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
                                  float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
                                  const float* const* X2, int accum, const float* nw) {
     if (in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS || count < 1) return hipErrorNotSupported;
-    // an RMS norm fuses only into the 2-4 token GEMV path (the batched kernel's
-    // 15-bit x image measured less accurate with x * w digitised before the scale)
+    // an RMS norm fuses only into the 2-4 token GEMV path (the batched path
+    // normalises into scratch first)
     if (nw && X2) return hipErrorNotSupported;
     if (!X2 && count <= 4) {
         // 2-4 tokens of one x shared by up to 4 matrices: the GEMV kernel carries
-        // the tokens (no x-image prologue, the weights read once)
+        // the tokens (the weights read once)
         bool same = n[0] >= 2 && n[0] <= 4;
         for (int i = 1; i < count; i++) same = same && X[i] == X[0] && n[i] == n[0];
         // 3-4 tokens: the four MFMAs per token and group make big matrices
@@ -803,10 +809,7 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
     const QgScratch* sc = qh_mmq_scratch_ptrs();
     if (!sc) return hipErrorNotSupported;
     const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
-    const int ngroups = in_dim / 256;
-    int max_slots = (int)(QG_SCRATCH / qg_slot_bytes(type, ngroups));
-    max_slots = max_slots < QG_MAXG ? max_slots : QG_MAXG;
-    if (max_slots < 1) return hipErrorNotSupported;
+    const int max_slots = QG_MAXG;
     const int64_t max_rows = (((int64_t)1 << 31) - 4096) / row_bytes / 32 * 32;
     if (max_rows < 32) return hipErrorNotSupported;
     // Entries go matrix-major: a matrix's token chunks follow each other, so

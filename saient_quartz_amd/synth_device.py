@@ -6,7 +6,7 @@ generator the parity tests use; the two streams differ, the distributions match.
 """
 import torch
 
-Q4_K, Q6_K = 12, 14
+Q4_K, Q5_K, Q6_K = 12, 13, 14
 
 
 def _gen(seed):
@@ -21,6 +21,18 @@ def q4k(out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
     g = _gen(seed)
     nb = out_dim * in_dim // 256
     blk = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device="cuda", generator=g)
+    d = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.01).half()
+    dmin = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.005).half()
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:4] = dmin.view(torch.uint8).view(nb, 2)
+    return blk.reshape(-1)
+
+
+def q5k(out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
+    """Q5_K: as Q4_K (176-byte blocks: d, dmin, 12 scale bytes, 32 qh, 128 qs)."""
+    g = _gen(seed)
+    nb = out_dim * in_dim // 256
+    blk = torch.randint(0, 256, (nb, 176), dtype=torch.uint8, device="cuda", generator=g)
     d = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.01).half()
     dmin = torch.randn(nb, device="cuda", generator=g).abs_().mul_(0.005).half()
     blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
@@ -60,6 +72,8 @@ def iq(ggml_type: int, out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
 def weights(ggml_type: int, out_dim: int, in_dim: int, seed: int) -> torch.Tensor:
     if ggml_type == Q4_K:
         return q4k(out_dim, in_dim, seed)
+    if ggml_type == Q5_K:
+        return q5k(out_dim, in_dim, seed)
     if ggml_type == Q6_K:
         return q6k(out_dim, in_dim, seed)
     if ggml_type in _IQ_BYTES:

@@ -164,13 +164,15 @@ SYM_TYPES = (("q", Q6_K), ("k", Q8_0), ("v", Q6_K), ("o", Q8_0), ("gate", Q6_K),
              ("down", Q6_K), ("head", Q8_0), ("embed", Q6_K))
 BATCH_CASES = {
     "llama_q4km_1layer": dict(types=LLAMA_TYPES, layers=1),
+    "llama_q4km_2layers": dict(types=LLAMA_TYPES, layers=2),
     "sym_2layers": dict(types=SYM_TYPES, layers=2),
     "q5_0": dict(types=Q50_TYPES, layers=1),
     "q2_k_fallback": dict(types=Q2K_TYPES, layers=1),
 }
 
 
-@pytest.mark.parametrize("n, case", [(3, "llama_q4km_1layer"), (16, "llama_q4km_1layer"), (4, "sym_2layers"),
+@pytest.mark.parametrize("n, case", [(3, "llama_q4km_1layer"), (16, "llama_q4km_1layer"), (16, "llama_q4km_2layers"),
+                                     (8, "llama_q4km_2layers"), (4, "sym_2layers"),
                                      (16, "sym_2layers"), (2, "q5_0"),
                                      (2, "q2_k_fallback")])
 def test_batch_step_matches_oracle(qh, oracle, n, case):
@@ -178,11 +180,10 @@ def test_batch_step_matches_oracle(qh, oracle, n, case):
     attention) against oracle/glue_ref.forward_step run per sequence, each
     with its own tokens and K/V cache, over four positions: 1e-3 relative L2
     per sequence on logits and hidden state, with realistically scaled weights.
-    Each batched GEMM is ~1e-4 accurate (x to 15 bits below each token's
-    256-element group peak).  The synthetic Q4_K blocks are far from zero-mean
-    (q uniform in 0..15), which makes a stack of them ill-conditioned: a second
-    layer amplifies the first one's 1e-4 about tenfold, so the Q4_K_M model is
-    checked over one layer and the two-layer check uses zero-mean formats."""
+    The synthetic Q4_K blocks are far from zero-mean (q uniform in 0..15),
+    which makes a stack of them ill-conditioned (a second layer amplifies the
+    first one's error about tenfold); the batched GEMMs keep x to about 21
+    bits per element, so two Q4_K_M layers stay well inside the bar."""
     from saient_quartz_amd.decode import BatchStep
     kw = dict(hidden=512, n_heads=4, n_kv=2, head_dim=128, ffn=1024, vocab=300, layers=2, max_seq=8)
     kw.update(BATCH_CASES[case])

@@ -6,7 +6,7 @@ against oracle/glue_ref.moe_route / moe_ffn, the restatement of moe_ffn
 Bars: expert ids, slot plans and gathers exact; routing weights within 4e-6
 relative (expf against numpy's f32 exp, both within an ulp or two of exp);
 SwiGLU and combine within 1e-6 of float64; the full layer within 1e-3
-relative L2 per token (the GEMV bar; the expert GEMMs contribute ~2e-4)."""
+relative L2 per token (the GEMV bar)."""
 import sys
 from pathlib import Path
 
