@@ -133,6 +133,19 @@ int hip_gemm_grouped_norm_async(uint32_t ggml_type, int count, const uint8_t* co
                                 const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
                                 float* d_scratch, void* stream);
 
+/* hip_gemm_grouped_norm_async without the scratch argument: the normalised
+ * rows go to a static device array of the library (4 MB, one per device, kept
+ * until the process ends), so the call allocates nothing and needs no
+ * workspace from the caller.  No counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  n * in_dim must be <= 1048576
+ * (QH_ERR_RANGE otherwise, with the limit in hip_last_error()).  Every call on
+ * one device shares that array: calls that overlap on one device (different
+ * streams) race and must be serialised by the caller. */
+int hip_gemm_grouped_norm_static_async(uint32_t ggml_type, int count, const uint8_t* const* d_data, const float* d_x,
+                                       const float* d_norm_w, float* const* d_y, int n, const int* out_dims,
+                                       int in_dim, void* stream);
+
 /* hip_gemm_grouped_norm_async over count (1..8) matrices of mixed types
  * (types[k] for W[k]): a batch's norm + q/k/v when v has its own type, as
  * Q4_K_M models have (src/cuda.rs:549-562).  For 2..4 tokens, two types among

@@ -73,6 +73,8 @@ _SIGS = {
     "hip_moe_combine_async": (C.c_int, [C.c_void_p] * 6 + [C.c_int] * 4 + [C.c_void_p]),
     "hip_gemm_grouped_norm_async": (C.c_int, [C.c_uint32, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                              C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
+    "hip_gemm_grouped_norm_static_async": (C.c_int, [C.c_uint32, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                    C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
     "hip_gemm_group_norm_async": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                            C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     "hip_gemm_q8_1_mmq": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p] + [C.c_int] * 5),

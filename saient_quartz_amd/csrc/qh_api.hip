@@ -3,6 +3,7 @@
 // Argument checking, dispatch and status codes.  Reference: the `extern "C"`
 // block of src/cuda_kernels.cu:1025-1125.  Unlike the reference (void returns,
 // no error checks), every HIP call is checked and turned into a status code.
+#include <atomic>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -469,6 +470,49 @@ int hip_gemm_grouped_norm_async(uint32_t type, int count, const uint8_t* const* 
         if (rc) return rc;
     }
     return QH_OK;
+}
+
+// Device scratch of hip_gemm_grouped_norm_static_async: the normalised token
+// rows, at most QH_NORM_SCRATCH_FLOATS floats (4 MB; 64 tokens of 16384).  One
+// array per device, held until the process ends.  Host code uses only the
+// device address hipGetSymbolAddress returns for it (per device, looked up once
+// with that device current), never the array's name.
+#define QH_NORM_SCRATCH_FLOATS (1 << 20)
+static __device__ __align__(256) float qh_norm_scratch[QH_NORM_SCRATCH_FLOATS];
+
+static float* qh_norm_scratch_ptr() {
+    static std::atomic<float*> ptrs[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    float* p = ptrs[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* a = nullptr;
+        hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(qh_norm_scratch));
+        if (e != hipSuccess) {
+            qh_fail(e, "hip_gemm_grouped_norm_static: hipGetSymbolAddress");
+            return nullptr;
+        }
+        p = static_cast<float*>(a);
+        ptrs[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+int hip_gemm_grouped_norm_static_async(uint32_t type, int count, const uint8_t* const* W, const float* x,
+                                       const float* norm_w, float* const* y, int n, const int* out_dims, int in_dim,
+                                       void* stream) {
+    if (count < 0 || n < 0) return QH_ERR_RANGE;
+    if (count == 0 || n == 0) return QH_OK;
+    if (in_dim <= 0) return QH_ERR_DIMS;
+    if ((int64_t)n * in_dim > QH_NORM_SCRATCH_FLOATS) {
+        snprintf(qh_errbuf, sizeof qh_errbuf,
+                 "hip_gemm_grouped_norm_static: n * in_dim = %lld floats exceeds the static scratch (%d floats)",
+                 (long long)n * in_dim, QH_NORM_SCRATCH_FLOATS);
+        return QH_ERR_RANGE;
+    }
+    float* s = qh_norm_scratch_ptr();
+    if (!s) return QH_ERR_HIP;
+    return hip_gemm_grouped_norm_async(type, count, W, x, norm_w, y, n, out_dims, in_dim, s, stream);
 }
 
 int hip_gemm_q8_1_mmq_async(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
