@@ -131,7 +131,11 @@ QH_DEV uint32_t qh_ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u)
 // 0xFF in byte j of the result for every set bit j (j < 4) of s.
 QH_DEV uint32_t qh_signmask4(uint32_t s4) {
     const uint32_t s = qh_spread4(s4 & 0xFu);
-    return (s << 8) - s;  // s * 0xFF, bytes 0 or 0xFF
+    // s * 0xFF (bytes 0 or 0xFF) as a shift and a subtraction: left alone, the
+    // compiler folds them into v_mul_lo_u32, a quarter-rate instruction
+    uint32_t sh = s << 8;
+    asm volatile("" : "+v"(sh));
+    return sh - s;
 }
 
 // IQ pieces for the int8 matrix-core kernels: 16 consecutive weights of one

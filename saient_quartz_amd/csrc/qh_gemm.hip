@@ -42,7 +42,7 @@ typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 
 #define QG_WAVES 8          // wavefronts (32-row tiles) per workgroup
 #define QG_TARGET_WGS 256   // workgroups a launch aims for (one per CU)
-#define QG_PART_TILES 4096  // row blocks with split-K counters (one per wavefront)
+#define QG_PART_TILES 8192  // row blocks with split-K counters (one per wavefront)
 #define QG_GMAX 6           // groups per workgroup (their x images stay in LDS)
 #define QG_NBUF 2           // items of weights in flight per wavefront (register sets)
 #define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
@@ -258,7 +258,7 @@ struct QgGroups {    // the matrices of one grouped launch
 // x 32 rows)
 // and per-(block, wavefront) arrival counters; every counter is back at zero
 // when a launch ends.
-#define QG_PART_FLOATS (8 * 1024 * 1024)
+#define QG_PART_FLOATS (16 * 1024 * 1024)
 static __device__ __align__(256) float qh_mmq_part[QG_PART_FLOATS];
 static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVES];
 
@@ -267,7 +267,7 @@ static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVE
 QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<const qh_u32x4*>(p); }
 
 // One workgroup of W wavefronts per (row block of 32 W TPW rows, K split of at
-// most QG_GMAX groups).  The workgroup first builds the split's x images in LDS
+// most GM groups).  The workgroup first builds the split's x images in LDS
 // (16 threads, one DPP row, per token and group; one barrier), then wavefront w
 // streams the weights of its TPW 32-row tiles (items: group by group, tile by
 // tile) through its own LDS tile (coalesced 16-byte loads, QG_NBUF items in
@@ -275,7 +275,7 @@ QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<con
 // operands from the shared images.  A wavefront's results belong to its own
 // rows, so no reduction over wavefronts is needed, and split-K partials are
 // combined per wavefront (see the end).
-template <class F, int NT, int W, int TPW>
+template <class F, int NT, int W, int TPW, int GM>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
                                                  int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
@@ -285,11 +285,11 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     using XI = XImg<F::SUMS>;
     constexpr int NQ = NT / 4;                 // slot quads (tokens 4q .. 4q + 3)
     constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
-    __shared__ __align__(16) unsigned char lds[QG_GMAX * XI::BYTES + W * TILE + GRIDB];
+    __shared__ __align__(16) unsigned char lds[GM * XI::BYTES + W * TILE + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
-    unsigned char* wl = lds + QG_GMAX * XI::BYTES + w * TILE;
-    unsigned char* gridl = lds + QG_GMAX * XI::BYTES + W * TILE;
+    unsigned char* wl = lds + GM * XI::BYTES + w * TILE;
+    unsigned char* gridl = lds + GM * XI::BYTES + W * TILE;
     if constexpr (F::GRID != 0) {
         const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
@@ -342,10 +342,11 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     };
 
     // ---- x of the split -> LDS images.  16 threads (one DPP row) per token
-    // and group, 16 consecutive elements each; pass p covers (group, token)
-    // pairs p 4W .. All x loads go out first, then the wavefront's first two
-    // weight groups; only the x loads are waited for.
-    constexpr int NPASS = (4 * QG_GMAX + W - 1) / W;
+    // slot and group, 16 consecutive elements each; pass p covers (group,
+    // token) pairs p 4W .. (NT token slots: rows of slots past NT are never
+    // read back).  All x loads go out first, then the wavefront's first weight
+    // items; only the x loads are waited for.
+    constexpr int NPASS = (GM * NT * 16 + 64 * W - 1) / (64 * W);
     const int u = lane & 15;
     float4 xv[NPASS][4];
     {
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
         const QhBuf ub = qh_buf(x2p, 4u * (uint32_t)n * (uint32_t)in_dim);
 #pragma unroll
         for (int pp = 0; pp < NPASS; pp++) {
-            const int idx = pp * 64 * W + threadIdx.x, k = idx >> 8, t = (idx >> 4) & 15;
+            const int idx = pp * 64 * W + threadIdx.x, k = idx / (16 * NT), t = (idx >> 4) % NT;
             const uint32_t off = (k < nk && t < n)
                                      ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)(g0 + k) + 16u * u)
                                      : 0x80000000u;
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int pp = 0; pp < NPASS; pp++) {
-        const int idx = pp * 64 * W + threadIdx.x, k = idx >> 8, t = (idx >> 4) & 15;
+        const int idx = pp * 64 * W + threadIdx.x, k = idx / (16 * NT), t = (idx >> 4) % NT;
         if (k < nk) {  // uniform per DPP row
             unsigned char* im = lds + k * XI::BYTES;
             float m = 0.f, sum = 0.f;
@@ -633,15 +634,6 @@ static const QgScratch* qh_mmq_scratch_ptrs() {
     return &p;
 }
 
-// QUARTZ_HIP_MMQ_TPW=1|2 forces the 32-row tiles per wavefront (tuning).
-static int qh_mmq_tpw_env() {
-    static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMQ_TPW");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
 // QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row block (tuning).
 static int qh_mmq_splits_env() {
     static const int v = [] {
@@ -651,26 +643,30 @@ static int qh_mmq_splits_env() {
     return v;
 }
 
-template <class F, int NT, int TPW>
+// Launch shapes: big launches (two rounds of workgroups or more) run 4
+// wavefronts with 2 groups resident (two workgroups per CU, so one's x
+// digitisation overlaps the other's weight stream); others 8 wavefronts with
+// up to QG_GMAX groups (longer splits, fewer partials).
+template <class F, int NT, int W, int GM>
 static void launch_mmq(const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
                        uint32_t row_bytes, int in_dim, hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, TPW>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
-                       row_bytes, in_dim, splits, sc.part, sc.cnt);
+    hipLaunchKernelGGL((qh_mmq<F, NT, W, 1, GM>), dim3((unsigned)wgs), dim3(64 * W), 0, st, gs, xs, row_bytes, in_dim,
+                       splits, sc.part, sc.cnt);
 }
 
 template <class F, int NT>
-static void launch_mmq_t(int tpw, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+static void launch_mmq_t(bool big, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
                          uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (tpw == 2) launch_mmq<F, NT, 2>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq<F, NT, 1>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    if (big) launch_mmq<F, NT, 4, 2>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq<F, NT, QG_WAVES, QG_GMAX>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 template <class F>
-static void launch_mmq_nt(int nt, int tpw, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
+static void launch_mmq_nt(int nt, bool big, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
                           const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (nt <= 4) launch_mmq_t<F, 4>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else if (nt <= 8) launch_mmq_t<F, 8>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq_t<F, 16>(tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    if (nt <= 4) launch_mmq_t<F, 4>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 8) launch_mmq_t<F, 8>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq_t<F, 16>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
@@ -682,17 +678,17 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
 };
 
 // K splits per row block: the count s (at least 2 groups per split where K
-// allows, at most QG_GMAX, the groups whose x images fit in LDS) that
-// minimises the rounds of QG_TARGET_WGS workgroups times the groups each one
-// walks, the fewest splits on ties.
-static int qg_pick_splits(int blocks, int ngroups) {
-    const int smin = (ngroups + QG_GMAX - 1) / QG_GMAX;
+// allows, at most gmax, the groups whose x images fit in LDS) that minimises
+// the rounds of `target` workgroups times the groups each one walks, the
+// fewest splits on ties.
+static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
+    const int smin = (ngroups + gmax - 1) / gmax;
     int cap = ngroups / 2 > 1 ? ngroups / 2 : 1;
     cap = cap > smin ? cap : smin;
     int best = smin;
     int64_t best_cost = INT64_MAX;
     for (int s = smin; s <= cap; s++) {
-        const int64_t rounds = ((int64_t)blocks * s + QG_TARGET_WGS - 1) / QG_TARGET_WGS;
+        const int64_t rounds = ((int64_t)blocks * s + target - 1) / target;
         const int64_t cost = rounds * ((ngroups + s - 1) / s);
         if (cost < best_cost) {
             best_cost = cost;
@@ -727,20 +723,29 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         gs.slot[i] = j;
         ntmax = en[i].n > ntmax ? en[i].n : ntmax;
     }
-    // One 32-row tile per wavefront.  Two (512-row blocks, x digitised once
-    // for twice the weight rows) measured slower at every shape tried: 14336 x
-    // 4096 Q4_K at 16 tokens 25.0 us against 21.2, 4096 x 14336 Q6_K 38.6
-    // against 29.3; QUARTZ_HIP_MMQ_TPW=2 selects them.
-    const int tpw = qh_mmq_tpw_env() == 2 ? 2 : 1;
-    const int brows = 32 * QG_WAVES * tpw;
-    int blocks = 0;
-    for (int i = 0; i < cnt; i++) blocks += (en[i].rows + brows - 1) / brows;
-    const int smin = (ngroups + QG_GMAX - 1) / QG_GMAX;  // a split's images must fit in LDS
+    // One 32-row tile per wavefront.  Two per wavefront (x digitised once for
+    // twice the weight rows) measured slower at every shape tried (14336 x 4096
+    // Q4_K at 16 tokens 25.0 us against 21.2, 4096 x 14336 Q6_K 38.6 against
+    // 29.3), so the kernel keeps the option (TPW) but runs one.
+    // "big": at least two rounds of 4-wavefront workgroups with 2 resident
+    // groups, for a type whose 4-wave tiles and 2 images fit twice in LDS
+    // (Q6_K's 240-byte lines do not).
+    auto count_blocks = [&](int rows_per_block) {
+        int b = 0;
+        for (int i = 0; i < cnt; i++) b += (en[i].rows + rows_per_block - 1) / rows_per_block;
+        return b;
+    };
+    const int b4 = count_blocks(32 * 4);
+    const bool big = type != QT_Q6_K && (int64_t)b4 * ((ngroups + 1) / 2) >= 4 * QG_TARGET_WGS &&
+                     qh_mmq_splits_env() <= 0;
+    const int brows = big ? 32 * 4 : 32 * QG_WAVES, gmax = big ? 2 : QG_GMAX;
+    const int blocks = big ? b4 : count_blocks(brows);
+    const int smin = (ngroups + gmax - 1) / gmax;  // a split's images must fit in LDS
     int splits = qh_mmq_splits_env();
-    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups);
+    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, gmax, big ? 2 * QG_TARGET_WGS : QG_TARGET_WGS);
     splits = splits < ngroups ? splits : ngroups;
     splits = splits > smin ? splits : smin;
-    const int64_t pb = (int64_t)QG_WAVES * tpw * 16 * 32;  // floats of one partial block (16-token bound)
+    const int64_t pb = (int64_t)(brows / 32) * 16 * 32;  // floats of one partial block (16-token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
     if (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES)) {
@@ -765,11 +770,11 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     gs.bstart[QG_MAXG] = INT_MAX;
     gs.accum = accum;
     switch (type) {
-        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        default: launch_mmq_nt<GQ6K>(ntmax, tpw, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
     }
     return hipGetLastError();
 }
