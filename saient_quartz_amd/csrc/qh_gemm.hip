@@ -172,10 +172,15 @@ struct GQ6K {
 
 // IQ3_S (src/dequant.rs:1184-1237) and IQ2_XXS (:1011-1041): K-block J is half
 // J & 1 of sub-block J >> 1; the lane's 8 weights are two codebook entries
-// (IQ3_S) or one (IQ2_XXS) with their signs, times the sub-block's odd scale.
-// Signed bytes b become f16 through b ^ 0x80 = b + 128, so c = -1152 sc.
+// (IQ3_S) or one (IQ2_XXS) with their 8 sign bits, times the sub-block's odd
+// scale.  Two tables in LDS, built once per workgroup (qg_iq_tables), make
+// this a few lookups: the codebook as f16 (entry e at 8 e bytes for IQ3_S's 4
+// values, 16 e for IQ2_XXS's 8), and for each sign byte the four f16-pair sign
+// masks of its 8 weights (16 bytes each, at IQT_SIGN).
 extern __device__ uint32_t qh_g_iq3s[512];
 extern __device__ uint64_t qh_g_iq2xxs[256];
+#define IQT_SIGN 4096  // sign masks after the 4 KB f16 codebook
+#define IQT_BYTES 8192
 
 struct GIQ3S {
     static constexpr int BYTES = 110, CH = 7, RS = 112, LAST = 94;
@@ -184,17 +189,19 @@ struct GIQ3S {
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{qh_h2f(qh_rd16(r, 0)), 0.f}; }
     template <int J>
-    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* grid) {
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* tab) {
         constexpr int K = J >> 1, jj = J & 1;
-        const uint32_t* g32 = reinterpret_cast<const uint32_t*>(grid);
         const uint32_t q = qh_rd16(r, 2 + 8 * K + 4 * jj + 2 * hh);                   // 2 grid indices
         const uint32_t qh = (uint32_t)r[66 + K] >> (4 * jj + 2 * hh);                  // their 9th bits
         const uint32_t sg = (uint32_t)r[qh_iq3s_at(74 + 4 * K + 2 * jj + hh)];         // 8 sign bits
-        const uint32_t b0 = qh_negbytes(g32[(q & 0xFFu) | ((qh & 1u) << 8)], qh_signmask4(sg));
-        const uint32_t b1 = qh_negbytes(g32[((q >> 8) & 0xFFu) | ((qh & 2u) << 7)], qh_signmask4(sg >> 4));
+        const qh_u32x2 g0 = *reinterpret_cast<const qh_u32x2*>(tab + 8 * ((q & 0xFFu) | ((qh & 1u) << 8)));
+        const qh_u32x2 g1 = *reinterpret_cast<const qh_u32x2*>(tab + 8 * (((q >> 8) & 0xFFu) | ((qh & 2u) << 7)));
+        const qh_u32x4 m = *reinterpret_cast<const qh_u32x4*>(tab + IQT_SIGN + 16 * sg);
         const int sc = 1 + 2 * (int)((r[qh_iq3s_at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
         const qh_f16x2 scv = {(_Float16)sc, (_Float16)sc};
-        return qg_cvt8(b0 ^ 0x80808080u, b1 ^ 0x80808080u, scv, scv * (_Float16)-1152.0f);
+        const qh_f16x2 a = qg_u2h(g0.x ^ m.x) * scv, b = qg_u2h(g0.y ^ m.y) * scv;
+        const qh_f16x2 c = qg_u2h(g1.x ^ m.z) * scv, d = qg_u2h(g1.y ^ m.w) * scv;
+        return qh_f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
     }
 };
 
@@ -205,20 +212,50 @@ struct GIQ2XXS {
     struct H { float d, dm; };
     static QH_DEV H hdr(const unsigned char* r) { return H{0.125f * qh_h2f(qh_rd16(r, 0)), 0.f}; }
     template <int J>
-    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* grid) {
+    static QH_DEV qh_f16x8 bop(const unsigned char* r, int hh, const H&, const unsigned char* tab) {
         constexpr int K = J >> 1, jj = J & 1;
-        const uint64_t* g64 = reinterpret_cast<const uint64_t*>(grid);
         const uint32_t idx = r[2 + 8 * K + 2 * jj + hh];
         const uint32_t a1 = qh_rd16(r, qh_iq2xxs_at(6 + 8 * K)) | (qh_rd16(r, qh_iq2xxs_at(8 + 8 * K)) << 16);
-        const uint64_t g = g64[idx];
+        const qh_u32x4 g = *reinterpret_cast<const qh_u32x4*>(tab + 16 * idx);
         const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * jj + hh))) & 127u);
-        const uint32_t b0 = qh_negbytes((uint32_t)g, qh_signmask4(s8));
-        const uint32_t b1 = qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
+        const qh_u32x4 m = *reinterpret_cast<const qh_u32x4*>(tab + IQT_SIGN + 16 * s8);
         const int sc = 2 * (int)(a1 >> 28) + 1;
         const qh_f16x2 scv = {(_Float16)sc, (_Float16)sc};
-        return qg_cvt8(b0 ^ 0x80808080u, b1 ^ 0x80808080u, scv, scv * (_Float16)-1152.0f);
+        const qh_f16x2 a = qg_u2h(g.x ^ m.x) * scv, b = qg_u2h(g.y ^ m.y) * scv;
+        const qh_f16x2 c = qg_u2h(g.z ^ m.z) * scv, d = qg_u2h(g.w ^ m.w) * scv;
+        return qh_f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
     }
 };
+
+// Build the IQ tables of format GRID (1: IQ3_S, 2: IQ2_XXS) in LDS at tab:
+// thread i < 512 converts codebook bytes to f16, i < 256 writes sign byte i's
+// masks (bit k of the byte -> the sign bit of f16 k, pairs per dword).
+template <int GRIDT>
+QH_DEV void qg_iq_tables(unsigned char* tab, int tid, int nthreads) {
+    for (int i = tid; i < 512; i += nthreads) {
+        if constexpr (GRIDT == 1) {
+            const uint32_t e = qh_g_iq3s[i];
+            const qh_u32x2 v = {__builtin_amdgcn_perm(0x64646464u, e, QG_SEL01), __builtin_amdgcn_perm(0x64646464u, e, QG_SEL23)};
+            const qh_f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+            *reinterpret_cast<qh_u32x2*>(tab + 8 * i) =
+                qh_u32x2{qg_h2u(qg_u2h(v.x) - k1024), qg_h2u(qg_u2h(v.y) - k1024)};
+        } else if (i < 256) {
+            const uint64_t e = qh_g_iq2xxs[i];
+            const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
+            const qh_f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+            *reinterpret_cast<qh_u32x4*>(tab + 16 * i) =
+                qh_u32x4{qg_h2u(qg_b2h(lo, QG_SEL01) - k1024), qg_h2u(qg_b2h(lo, QG_SEL23) - k1024),
+                         qg_h2u(qg_b2h(hi, QG_SEL01) - k1024), qg_h2u(qg_b2h(hi, QG_SEL23) - k1024)};
+        }
+        if (i < 256) {
+            qh_u32x4 m;
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                m[k] = (((uint32_t)i >> (2 * k)) & 1u) << 15 | (((uint32_t)i >> (2 * k + 1)) & 1u) << 31;
+            *reinterpret_cast<qh_u32x4*>(tab + IQT_SIGN + 16 * i) = m;
+        }
+    }
+}
 
 // ---------------------------------------------------------------- x image in LDS
 
@@ -284,16 +321,13 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     static_assert(NT == 4 || NT == 8 || NT == 16, "NT");
     using XI = XImg<F::SUMS>;
     constexpr int NQ = NT / 4;                 // slot quads (tokens 4q .. 4q + 3)
-    constexpr int GRIDB = F::GRID ? 2048 : 0;  // codebook (IQ3S: 512 x u32, IQ2XXS: 256 x u64)
+    constexpr int GRIDB = F::GRID ? IQT_BYTES : 0;  // IQ codebook and sign tables
     __shared__ __align__(16) unsigned char lds[GM * XI::BYTES + W * TILE + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
     unsigned char* wl = lds + GM * XI::BYTES + w * TILE;
     unsigned char* gridl = lds + GM * XI::BYTES + W * TILE;
-    if constexpr (F::GRID != 0) {
-        const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
-        for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
-    }
+    if constexpr (F::GRID != 0) qg_iq_tables<F::GRID>(gridl, threadIdx.x, 64 * W);
     // This workgroup's matrix (uniform), row block and K split.  Every matrix's
     // workgroups start at a multiple of `splits`, so blockIdx / splits is a
     // launch-wide block index (for the split counters and partials).
