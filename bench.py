@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--decode-reps", type=int, default=20)
     ap.add_argument("--only-forward", action="store_true",
                     help="only run the end-to-end decode-step leg (for profiling its kernels)")
+    ap.add_argument("--batched-suite", action="store_true",
+                    help="only time hip_gemm at the batched shapes of configs[3]/[4] (16 tokens; for profiling "
+                         "the matrix-core GEMM kernels)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 256 MiB (torch copy kernel), to calibrate the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes")
@@ -58,6 +61,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel(), "copies": 5}))
+        return
+
+    if args.batched_suite:
+        print(json.dumps({"batched": batched_suite(torch)}), flush=True)
         return
 
     if args.only_forward:
@@ -162,6 +169,42 @@ def main():
         "moe": moe,
     }
     print(json.dumps(rec), flush=True)
+
+
+def batched_suite(torch, reps=50):
+    """hip_gemm with 16 tokens (and 4 for the 4-sequence step's big matrices) at
+    the batched shapes of BASELINE.json configs[3] (Q4_K gate/up, Q6_K down)
+    and configs[4] (IQ3_S / IQ2_XXS expert gate/up and down): each shape's
+    `reps` calls over rotated weights captured in one HIP graph, events around
+    a replay.  Reports us per call and weight GB/s."""
+    from saient_quartz_amd import lib, synth_device, type_size
+    from saient_quartz_amd.api import check
+
+    L = lib()
+    out = {}
+    for t, o, i, n in ((12, 14336, 4096, 16), (14, 4096, 14336, 16), (12, 14336, 4096, 4), (14, 4096, 14336, 4),
+                       (21, 14336, 4096, 16), (21, 4096, 14336, 16), (16, 14336, 4096, 16), (16, 4096, 14336, 16)):
+        wb = type_size(t, o * i)
+        rot = max(3, -(-768 * 2**20 // wb))
+        Ws = [synth_device.weights(t, o, i, seed=40 + k) for k in range(rot)]
+        x = torch.randn(n, i, device="cuda")
+        y = torch.empty(n, o, device="cuda")
+        sp = torch.cuda.current_stream().cuda_stream
+        for k in range(3):
+            check("hip_gemm_async", L.hip_gemm_async(t, Ws[k % rot].data_ptr(), x.data_ptr(), y.data_ptr(), i, o, n, sp))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cs = torch.cuda.current_stream().cuda_stream
+            for k in range(reps):
+                check("hip_gemm_async", L.hip_gemm_async(t, Ws[k % rot].data_ptr(), x.data_ptr(), y.data_ptr(), i, o,
+                                                         n, cs))
+        g.replay()
+        torch.cuda.synchronize()
+        us = timed_replay(torch, g) / reps * 1e3
+        out[f"type{t}_{o}x{i}_n{n}"] = {"us": round(us, 2), "weight_GB_s": round(wb / us / 1e3, 1)}
+        del Ws, g
+        torch.cuda.empty_cache()
+    return out
 
 
 def decode_leg(torch, reps):
