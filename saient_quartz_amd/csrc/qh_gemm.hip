@@ -23,10 +23,11 @@
 //     and whose B operand is the 8 mins.
 //   * Products and sums accumulate in f32; the superblock's f16 scale d (and
 //     dmin) multiply the f32 results once per superblock.
-// Each workgroup digitises the x of its K split for all 16 token slots straight
-// into LDS (no separate prologue launch); its W wavefronts (one or two 32-row
-// tiles each) read their A operands from there, while each wavefront's weight
-// slices stream through its own LDS tile with QG_NBUF items in flight.
+// A launch first digitises each token block's x once (qg_ximage, into the
+// library's image array); the GEMM's workgroups then stream the images of their
+// K split group by group into an LDS pair shared by their W wavefronts (one
+// 32-row tile each), while each wavefront's weight slices stream through its
+// own LDS tile with QG_NBUF items in flight.
 //
 // Reference counterpart: dequant::gemm (src/dequant.rs:143-200) with
 // q4k_row_batched / q6k_row_batched (:38-122); the reference has no GPU
@@ -40,11 +41,14 @@ typedef float qh_f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 qh_f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 
+#ifndef QG_WAVES
 #define QG_WAVES 8          // wavefronts (32-row tiles) per workgroup
+#endif
 #define QG_TARGET_WGS 256   // workgroups a launch aims for (one per CU)
 #define QG_PART_TILES 8192  // row blocks with split-K counters (one per wavefront)
-#define QG_GMAX 6           // groups per workgroup (their x images stay in LDS)
+#ifndef QG_NBUF
 #define QG_NBUF 2           // items of weights in flight per wavefront (register sets)
+#endif
 #define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
 
 // ---------------------------------------------------------------- f16 operands
@@ -270,9 +274,8 @@ QH_DEV void qg_iq_tables(unsigned char* tab, int tid, int nthreads) {
 //     results are), k = 8 (sb >> 2) + 2 (sb & 3) + part, stored at 16 (t + 16
 //     (sb >> 2)) + 2 (2 (sb & 3) + part).
 //   EXP: s of each token slot (127: x not finite).
-template <bool SUMS>
 struct XImg {
-    static constexpr int SUM = 16384, EXP = SUMS ? 16896 : 16384, BYTES = EXP + 16;
+    static constexpr int SUM = 16384, EXP = 16896, BYTES = 16912;  // BYTES: a multiple of 16
 };
 
 #define QG_MAXG 16  // matrices (or row chunks) per grouped launch
@@ -280,6 +283,8 @@ struct QgXs {        // the distinct token blocks of one grouped launch
     const float* x[QG_MAXG];
     const float* x2[QG_MAXG];  // SwiGLU: x is silu(x) * x2 (gate, up) when non-null
     int n[QG_MAXG];  // tokens (<= 16)
+    const unsigned char* img;  // their x images: slot s, group g at (s ngroups + g) XImg::BYTES
+    uint32_t img_bytes;
 };
 struct QgGroups {    // the matrices of one grouped launch
     const uint8_t* w[QG_MAXG];
@@ -297,36 +302,132 @@ struct QgGroups {    // the matrices of one grouped launch
 // when a launch ends.
 #define QG_PART_FLOATS (16 * 1024 * 1024)
 static __device__ __align__(256) float qh_mmq_part[QG_PART_FLOATS];
+// x images of one launch's token blocks (qg_ximage)
+#define QG_IMG_BYTES (24u << 20)
+static __device__ __align__(256) unsigned char qh_mmq_img[QG_IMG_BYTES];
 static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVES];
+
+// ---------------------------------------------------------------- x images
+
+// qg_ximage: the x operand of token block `slot` (blockIdx.y), 256-element
+// group g (blockIdx.x), for the batched kernel, written once per launch to the
+// library's image array and read by every row block.  Thread tid takes token t
+// = tid / 32, elements 8 c .. 8 c + 7 (c = tid % 32) of the group, i.e.
+// K-block c / 2, k half c % 2.  Per token and group, x' = x 2^s (s = 14 -
+// exponent of max|x|) as hi = rtz(x') and lo = rtz(x' - hi); the layout is
+// XImg's:
+//   K-block j (16 weights) at 1024 j: row 2t + part holds token t's hi (part
+//     0) or lo (part 1) f16 of elements 16 j + k (the A operand order of
+//     v_mfma_f32_32x32x16_f16: lane L's 16 bytes are row L % 32, k = 8 (L / 32)
+//     .. + 7);
+//   SUM: token t's sum of x over sub-block sb, times 2^(s - 5), as hi and lo
+//     f16 (the A operand of the Q4_K/Q5_K mins MFMA): row rho(t) = 8 (t >> 2) +
+//     4 ((t >> 1) & 1) + (t & 1), k = 8 (sb >> 2) + 2 (sb & 3) + part, stored
+//     at 16 (t + 16 (sb >> 2)) + 2 (2 (sb & 3) + part);
+//   EXP: s of each token (127: the group holds an Inf or NaN, which makes the
+//     token's results NaN).
+// Tokens past the block's n write nothing (their rows are never read back
+// into results).
+__global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
+    const int g = blockIdx.x, slot = blockIdx.y, ngroups = in_dim >> 8;
+    const int lane = threadIdx.x & 63, xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
+    const int n = xs.n[slot];
+    if (xt >= n) return;  // whole half-wavefronts: the reductions below stay within live lanes
+    const float* xp = xs.x[slot] + (size_t)xt * in_dim + 256 * g + 8 * xc;
+    const float* x2p = xs.x2[slot];
+    float v[8];
+    {
+        const float4 a = *reinterpret_cast<const float4*>(xp), b = *reinterpret_cast<const float4*>(xp + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    if (x2p) {
+        // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
+        const float* up = x2p + (size_t)xt * in_dim + 256 * g + 8 * xc;
+        const float4 a = *reinterpret_cast<const float4*>(up), b = *reinterpret_cast<const float4*>(up + 4);
+        const float u8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (v[i] / (1.f + expf(-v[i]))) * u8[i];
+    }
+    float m = 0.f, sum = 0.f;
+    bool fin = true;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        m = fmaxf(m, fabsf(v[i]));
+        sum += v[i];
+        fin = fin && __builtin_isfinite(v[i]);
+    }
+    // max over the token's 32 lanes (a DPP row of 16, then the other row)
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
+    m = fmaxf(m, __shfl_xor(m, 16));
+    const uint64_t bad = __ballot(!fin);
+    const bool fb = ((bad >> (lane & 32)) & 0xFFFFFFFFull) != 0;
+    int e = 0;
+    (void)frexpf(m, &e);
+    int s = m > 0.f ? 14 - e : 0;
+    s = s > 126 ? 126 : (s < -126 ? -126 : s);
+    const float scx = ldexpf(1.0f, s);
+    uint32_t hi4[4], lo4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = v[2 * i] * scx, b = v[2 * i + 1] * scx;
+        const auto hp = __builtin_amdgcn_cvt_pkrtz(a, b);
+        const auto lp = __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]);
+        hi4[i] = __builtin_bit_cast(uint32_t, hp);
+        lo4[i] = __builtin_bit_cast(uint32_t, lp);
+    }
+    unsigned char* im = img + ((size_t)slot * ngroups + g) * XImg::BYTES;
+    const int u = xc >> 1, c = xc & 1;
+    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 32 * c)) = qh_u32x4{hi4[0], hi4[1], hi4[2], hi4[3]};
+    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 1 + 32 * c)) = qh_u32x4{lo4[0], lo4[1], lo4[2], lo4[3]};
+    // sub-block sb = xc / 4: the sum over 4 lanes (a DPP quad)
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
+    const float s5 = sum * ldexpf(1.0f, s - 5);
+    const auto p5 = __builtin_amdgcn_cvt_pkrtz(s5, 0.f);
+    const auto q5 = __builtin_amdgcn_cvt_pkrtz(s5 - (float)p5[0], 0.f);
+    const int sb = xc >> 2;
+    if ((xc & 3) == 0) {
+        const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, p5[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, q5[0]) << 16);
+        *reinterpret_cast<uint32_t*>(im + XImg::SUM + 16 * (xt + 16 * (sb >> 2)) + 4 * (sb & 3)) = pair;
+    }
+    if (xc == 0) im[XImg::EXP + xt] = (unsigned char)(signed char)(fb ? 127 : s);
+}
 
 // ---------------------------------------------------------------- kernel
 
 QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<const qh_u32x4*>(p); }
 
-// One workgroup of W wavefronts per (row block of 32 W TPW rows, K split of at
-// most GM groups).  The workgroup first builds the split's x images in LDS
-// (16 threads, one DPP row, per token and group; one barrier), then wavefront w
-// streams the weights of its TPW 32-row tiles (items: group by group, tile by
-// tile) through its own LDS tile (coalesced 16-byte loads, QG_NBUF items in
-// flight in register sets, the first ones while x is digitised) and reads its A
-// operands from the shared images.  A wavefront's results belong to its own
-// rows, so no reduction over wavefronts is needed, and split-K partials are
-// combined per wavefront (see the end).
-template <class F, int NT, int W, int TPW, int GM>
+// One workgroup of W wavefronts per (row block of 32 W rows, K split).  Wavefront
+// w owns one 32-row tile and streams its weights group by group through its own
+// LDS tile (coalesced 16-byte loads, QG_NBUF groups in flight in register sets).
+// The x images (qg_ximage's) go through a pair of LDS slots shared by the
+// workgroup, one group ahead of the weights: while group i is computed, group
+// i + 1's image (loaded one iteration earlier) is stored, and group i + 2's
+// image loads go out with the weights.  One workgroup barrier per group orders
+// the slot pair.
+// A wavefront's results belong to its own rows, so no reduction over
+// wavefronts is needed, and split-K partials are combined per wavefront (see
+// the end).
+template <class F, int NT, int W>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
                                                  int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte weight loads per lane per group
     constexpr int TILE = 32 * RS + 16;
     static_assert(NT == 4 || NT == 8 || NT == 16, "NT");
-    using XI = XImg<F::SUMS>;
+    using XI = XImg;
     constexpr int NQ = NT / 4;                 // slot quads (tokens 4q .. 4q + 3)
+    constexpr int TPW = 1;                     // 32-row tiles per wavefront
     constexpr int GRIDB = F::GRID ? IQT_BYTES : 0;  // IQ codebook and sign tables
-    __shared__ __align__(16) unsigned char lds[GM * XI::BYTES + W * TILE + GRIDB];
+    constexpr int IMB = XI::BYTES;
+    __shared__ __align__(16) unsigned char lds[2 * IMB + W * TILE + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
-    unsigned char* wl = lds + GM * XI::BYTES + w * TILE;
-    unsigned char* gridl = lds + GM * XI::BYTES + W * TILE;
+    unsigned char* wl = lds + 2 * IMB + w * TILE;
+    unsigned char* gridl = lds + 2 * IMB + W * TILE;
     if constexpr (F::GRID != 0) qg_iq_tables<F::GRID>(gridl, threadIdx.x, 64 * W);
     // This workgroup's matrix (uniform), row block and K split.  Every matrix's
     // workgroups start at a multiple of `splits`, so blockIdx / splits is a
@@ -341,31 +442,30 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     const int ngroups = in_dim >> 8;
     const int lb = blockIdx.x - gs.bstart[gi];
     const int blk = lb / splits, sp = lb - blk * splits, gblk = blockIdx.x / splits;
-    const int tile0 = (blk * W + w) * TPW;  // this wavefront's tiles tile0 .. tile0 + TPW - 1
+    const int tile0 = blk * W + w;  // this wavefront's tile
     const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
     const int nk = g1 - g0;
+    // Row blocks walk their split's groups from different starting points, so
+    // concurrent workgroups read different parts of x (spreading the L2 load).
+    const int rot = nk > 0 ? blk % nk : 0;
+    auto grp = [&](int i) { const int j = i + rot; return g0 + (j >= nk ? j - nk : j); };
 
-    // Weight slices of this lane: row q / CH of a tile, slice q % CH, byte
-    // offset goff[h] in tile tile0 (tile tile0 + tt is 32 tt rows further), LDS
-    // offset soff[h] (lanes past 32 * CH: the spare 16 bytes at the tile's end);
-    // bit h TPW + tt of okb: the slice's row exists in tile tile0 + tt.
+    // Weight slices of this lane: row q / CH of the tile, slice q % CH, byte
+    // offset goff[h], LDS offset soff[h] (lanes past 32 * CH: the spare 16
+    // bytes at the tile's end); bit h of okb: the slice's row exists.
     uint32_t goff[NH], soff[NH], okb = 0;
 #pragma unroll
     for (int h = 0; h < NH; h++) {
         const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
-#pragma unroll
-        for (int tt = 0; tt < TPW; tt++)
-            okb |= (q < 32 * CH && (tile0 + tt) * 32 + r < out_dim) ? 1u << (h * TPW + tt) : 0u;
+        okb |= (q < 32 * CH && tile0 * 32 + r < out_dim) ? 1u << h : 0u;
         goff[h] = (uint32_t)(tile0 * 32 + r) * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
     }
-    // item i = (group g0 + i / TPW, tile tile0 + i % TPW)
-    auto load_w = [&](int i, qh_u32x4* wo) {
-        const int g = g0 + i / TPW, tt = i % TPW;
-        const uint32_t go = (uint32_t)F::BYTES * (uint32_t)g + (uint32_t)(32 * tt) * row_bytes;
+    auto load_w = [&](int i, qh_u32x4* wo) {  // item i: group grp(i)
+        const uint32_t go = (uint32_t)F::BYTES * (uint32_t)grp(i);
 #pragma unroll
         for (int h = 0; h < NH; h++)
-            wo[h] = qh_ld128(wb, (g < g1 && ((okb >> (h * TPW + tt)) & 1u)) ? goff[h] + go : 0x80000000u);
+            wo[h] = qh_ld128(wb, (i < nk && ((okb >> h) & 1u)) ? goff[h] + go : 0x80000000u);
     };
     auto stage_w = [&](const qh_u32x4* wr) {
 #pragma unroll
@@ -375,117 +475,41 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // ---- x of the split -> LDS images.  16 threads (one DPP row) per token
-    // slot and group, 16 consecutive elements each; pass p covers (group,
-    // token) pairs p 4W .. (NT token slots: rows of slots past NT are never
-    // read back).  All x loads go out first, then the wavefront's first weight
-    // items; only the x loads are waited for.
-    constexpr int NPASS = (GM * NT * 16 + 64 * W - 1) / (64 * W);
-    const int u = lane & 15;
-    float4 xv[NPASS][4];
-    {
-        const float* xp = xs.x[slot];
-        const float* x2p = xs.x2[slot];
-        const QhBuf xb = qh_buf(xp, 4u * (uint32_t)n * (uint32_t)in_dim);
-        const QhBuf ub = qh_buf(x2p, 4u * (uint32_t)n * (uint32_t)in_dim);
+    // ---- x images (built by qg_ximage), one group at a time: 16-byte chunk
+    // id = tid + 64 W p (pass p < XP) of group grp(i)'s image is loaded with
+    // the weights one iteration ahead and stored to the LDS ring.
+    constexpr int NCH = XI::BYTES / 16;
+    constexpr int XP = (NCH + 64 * W - 1) / (64 * W);
+    const QhBuf xb = qh_buf(xs.img, xs.img_bytes);
+    const uint32_t ibase = (uint32_t)slot * (uint32_t)ngroups * (uint32_t)XI::BYTES + 16u * threadIdx.x;
+    qh_u32x4 xr[XP];
+    auto load_x = [&](int i) {  // item i: group grp(i)
 #pragma unroll
-        for (int pp = 0; pp < NPASS; pp++) {
-            const int idx = pp * 64 * W + threadIdx.x, k = idx / (16 * NT), t = (idx >> 4) % NT;
-            const uint32_t off = (k < nk && t < n)
-                                     ? 4u * ((uint32_t)t * (uint32_t)in_dim + 256u * (uint32_t)(g0 + k) + 16u * u)
-                                     : 0x80000000u;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const qh_u32x4 v = qh_ld128(xb, off + 16u * i);
-                xv[pp][i] = float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-            }
-            if (x2p) {
-                // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
-                auto sw = [](float gv, float uv) { return (gv / (1.f + expf(-gv))) * uv; };
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const qh_u32x4 v = qh_ld128(ub, off + 16u * i);
-                    xv[pp][i] = float4{sw(xv[pp][i].x, __uint_as_float(v.x)), sw(xv[pp][i].y, __uint_as_float(v.y)),
-                                       sw(xv[pp][i].z, __uint_as_float(v.z)), sw(xv[pp][i].w, __uint_as_float(v.w))};
-                }
-            }
+        for (int p = 0; p < XP; p++) {
+            const int id = threadIdx.x + 64 * W * p;
+            xr[p] = qh_ld128(xb, (id < NCH && i < nk) ? ibase + (uint32_t)XI::BYTES * (uint32_t)grp(i) + 1024u * W * p
+                                                       : 0x80000000u);
         }
-    }
-    // The first QG_NBUF groups' weights stay in flight while x is digitised.
-    // They are issued after every wavefront's x loads (an execution barrier,
-    // no memory fence): queued behind the weight loads of other wavefronts,
-    // the x loads would return several microseconds later.
+    };
+    auto store_x = [&](unsigned char* im) {
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int id = threadIdx.x + 64 * W * p;
+            if (id < NCH) *reinterpret_cast<qh_u32x4*>(im + 16 * id) = xr[p];
+        }
+    };
+
+    // Prologue: group 0's image, then the first QG_NBUF groups' weights, then
+    // group 0's image to LDS (waiting only for its loads) and group 1's loads.
     qh_u32x4 wr[QG_NBUF][NH];
+    load_x(0);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int pp = 0; pp < NPASS; pp++) {
-        const int idx = pp * 64 * W + threadIdx.x, k = idx / (16 * NT), t = (idx >> 4) % NT;
-        if (k < nk) {  // uniform per DPP row
-            unsigned char* im = lds + k * XI::BYTES;
-            float m = 0.f, sum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 v = xv[pp][i];
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                sum += (v.x + v.y) + (v.z + v.w);
-            }
-            // max over the row's 16 lanes
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
-            int e = 0;
-            (void)frexpf(m, &e);
-            int s = m > 0.f ? 14 - e : 0;
-            s = s > 126 ? 126 : (s < -126 ? -126 : s);
-            const float scx = ldexpf(1.0f, s);
-            // hi and lo f16 (round toward zero: hi = rtz(x'), lo = rtz(x' - hi),
-            // 22 bits) of the 16 elements: K-block u, k halves 0 and 1
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const float4 va = xv[pp][2 * c], vb = xv[pp][2 * c + 1];
-                const float v8[8] = {va.x * scx, va.y * scx, va.z * scx, va.w * scx,
-                                     vb.x * scx, vb.y * scx, vb.z * scx, vb.w * scx};
-                uint32_t hi4[4], lo4[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const auto hp = __builtin_amdgcn_cvt_pkrtz(v8[2 * i], v8[2 * i + 1]);
-                    const auto lp = __builtin_amdgcn_cvt_pkrtz(v8[2 * i] - (float)hp[0], v8[2 * i + 1] - (float)hp[1]);
-                    hi4[i] = __builtin_bit_cast(uint32_t, hp);
-                    lo4[i] = __builtin_bit_cast(uint32_t, lp);
-                }
-                *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * t + 32 * c)) =
-                    qh_u32x4{hi4[0], hi4[1], hi4[2], hi4[3]};
-                *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * t + 1 + 32 * c)) =
-                    qh_u32x4{lo4[0], lo4[1], lo4[2], lo4[3]};
-            }
-            // this lane's 16 elements and its neighbour's: sub-block u / 2; an
-            // Inf or NaN anywhere makes the row's sums non-finite
-            sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
-            float chk = sum;
-            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x4E, 0xF, 0xF, false));
-            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x141, 0xF, 0xF, false));
-            chk += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(chk), 0x140, 0xF, 0xF, false));
-            const bool fb = !__builtin_isfinite(chk);
-            if constexpr (F::SUMS) {
-                const float s5 = sum * ldexpf(1.0f, s - 5);
-                const auto p5 = __builtin_amdgcn_cvt_pkrtz(s5, 0.f);
-                const auto q5 = __builtin_amdgcn_cvt_pkrtz(s5 - (float)p5[0], 0.f);
-                const int sb = u >> 1;
-                if ((u & 1) == 0) {
-                    _Float16* sp = reinterpret_cast<_Float16*>(im + XI::SUM + 16 * (t + 16 * (sb >> 2))) + 2 * (sb & 3);
-                    sp[0] = p5[0];
-                    sp[1] = q5[0];
-                }
-            }
-            if (u == 0) im[XI::EXP + t] = (unsigned char)(signed char)(fb ? 127 : s);
-        }
-    }
-    __syncthreads();  // images (and the codebook) visible to every wavefront
+    store_x(lds);
+    load_x(1);
+    __syncthreads();  // image 0 (and the codebook) visible to every wavefront
 
     // Result slots of this lane: slot (q, r) of tile tt is token t = 4q + 2hh + r
     // of the tile's row R.
@@ -501,15 +525,12 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     auto compute = [&](const unsigned char* im, float* tot) {
         const typename F::H hd = F::hdr(wrow);
         qh_f32x16 c0 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        qh_f32x16 c1 = c0, dm = c0;
+        qh_f32x16 dm = c0;
         auto kb = [&](auto JC) {
             constexpr int J = decltype(JC)::value;
             const qh_f16x8 b = F::template bop<J>(wrow, hh, hd, gridl);
             const qh_f16x8 a = __builtin_bit_cast(qh_f16x8, qh_lds128(im + 1024 * J + 16 * lane));
-            if constexpr (J & 1)
-                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
-            else
-                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
         };
         kb(std::integral_constant<int, 0>{});
         kb(std::integral_constant<int, 1>{});
@@ -541,7 +562,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
                 const int t = 4 * q + 2 * hh + r;
                 const int se = ((int)(ex[t >> 2] << (24 - 8 * (t & 3)))) >> 24;
                 const float rs = se == 127 ? __builtin_nanf("") : ldexpf(1.0f, -se);
-                const float P = (c0[4 * q + 2 * r] + c1[4 * q + 2 * r]) + (c0[4 * q + 2 * r + 1] + c1[4 * q + 2 * r + 1]);
+                const float P = c0[4 * q + 2 * r] + c0[4 * q + 2 * r + 1];
                 if constexpr (F::SUMS)
                     tot[2 * q + r] += (hd.d * P - hd.dm * 32.0f * dm[4 * q + r]) * rs;
                 else
@@ -549,21 +570,25 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
             }
     };
 
-    // Item i in register set i % QG_NBUF, refilled with item i + QG_NBUF as
-    // soon as it is staged (past the split: out of range, no traffic).
-    static_assert(QG_NBUF % TPW == 0, "an item's tile is b % TPW");
-    const int nitems = nk * TPW;
-    for (int i0 = 0; i0 < nitems; i0 += QG_NBUF) {
+    // Item i: stage group i's weights; store image (i + 1) % 2 from the loads
+    // of one iteration ago (every wavefront finished reading that slot before
+    // the last barrier); load group i + 2's image, then refill the register
+    // set with group i + QG_NBUF's weights (image first: a wait for it then
+    // leaves the weight loads in flight); compute group i against slot i % 2.
+    for (int i0 = 0; i0 < nk; i0 += QG_NBUF) {
 #pragma unroll
         for (int b = 0; b < QG_NBUF; b++) {
-            if (i0 + b < nitems) {
+            const int i = i0 + b;
+            if (i < nk) {
                 stage_w(wr[b]);
-                load_w(i0 + b + QG_NBUF, wr[b]);
-                compute(lds + ((i0 + b) / TPW) * XI::BYTES, tot[b % TPW]);
+                if (i + 1 < nk) store_x(lds + ((i + 1) & 1) * IMB);
+                load_x(i + 2);
+                load_w(i + QG_NBUF, wr[b]);
+                compute(lds + (i & 1) * IMB, tot[0]);
+                __syncthreads();
             }
         }
     }
-
     // Results: this wavefront's 32 rows x NT tokens.
     auto put = [&](int t, int row, float a) {
         if (t < n && row < out_dim) {
@@ -651,18 +676,20 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
 }
 
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
-struct QgScratch { float* part; unsigned int* cnt; };
+struct QgScratch { float* part; unsigned int* cnt; unsigned char* img; };
 static const QgScratch* qh_mmq_scratch_ptrs() {
     static QgScratch ptrs[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     QgScratch& p = ptrs[dev];
     if (!p.part) {
-        void *b = nullptr, *c = nullptr;
+        void *b = nullptr, *c = nullptr, *im = nullptr;
         if (hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) != hipSuccess ||
-            hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) != hipSuccess)
+            hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) != hipSuccess ||
+            hipGetSymbolAddress(&im, HIP_SYMBOL(qh_mmq_img)) != hipSuccess)
             return nullptr;
         p.cnt = static_cast<unsigned int*>(c);
+        p.img = static_cast<unsigned char*>(im);
         p.part = static_cast<float*>(b);
     }
     return &p;
@@ -677,30 +704,20 @@ static int qh_mmq_splits_env() {
     return v;
 }
 
-// Launch shapes: big launches (two rounds of workgroups or more) run 4
-// wavefronts with 2 groups resident (two workgroups per CU, so one's x
-// digitisation overlaps the other's weight stream); others 8 wavefronts with
-// up to QG_GMAX groups (longer splits, fewer partials).
-template <class F, int NT, int W, int GM>
-static void launch_mmq(const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
-                       uint32_t row_bytes, int in_dim, hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq<F, NT, W, 1, GM>), dim3((unsigned)wgs), dim3(64 * W), 0, st, gs, xs, row_bytes, in_dim,
-                       splits, sc.part, sc.cnt);
-}
-
+// Launch shape: QG_WAVES wavefronts (32-row tiles) per workgroup.
 template <class F, int NT>
-static void launch_mmq_t(bool big, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+static void launch_mmq_t(const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
                          uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (big) launch_mmq<F, NT, 4, 2>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq<F, NT, QG_WAVES, QG_GMAX>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes,
+                       in_dim, splits, sc.part, sc.cnt);
 }
 
 template <class F>
-static void launch_mmq_nt(int nt, bool big, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
+static void launch_mmq_nt(int nt, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
                           const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (nt <= 4) launch_mmq_t<F, 4>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else if (nt <= 8) launch_mmq_t<F, 8>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq_t<F, 16>(big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    if (nt <= 4) launch_mmq_t<F, 4>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 8) launch_mmq_t<F, 8>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq_t<F, 16>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
@@ -757,32 +774,21 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         gs.slot[i] = j;
         ntmax = en[i].n > ntmax ? en[i].n : ntmax;
     }
-    // One 32-row tile per wavefront.  Two per wavefront (x digitised once for
-    // twice the weight rows) measured slower at every shape tried (14336 x 4096
-    // Q4_K at 16 tokens 25.0 us against 21.2, 4096 x 14336 Q6_K 38.6 against
-    // 29.3), so the kernel keeps the option (TPW) but runs one.
-    // "big": at least two rounds of 4-wavefront workgroups with 2 resident
-    // groups, for a type whose 4-wave tiles and 2 images fit twice in LDS
-    // (Q6_K's 240-byte lines do not).
-    auto count_blocks = [&](int rows_per_block) {
-        int b = 0;
-        for (int i = 0; i < cnt; i++) b += (en[i].rows + rows_per_block - 1) / rows_per_block;
-        return b;
-    };
-    const int b4 = count_blocks(32 * 4);
-    const bool big = type != QT_Q6_K && (int64_t)b4 * ((ngroups + 1) / 2) >= 4 * QG_TARGET_WGS &&
-                     qh_mmq_splits_env() <= 0;
-    const int brows = big ? 32 * 4 : 32 * QG_WAVES, gmax = big ? 2 : QG_GMAX;
-    const int blocks = big ? b4 : count_blocks(brows);
-    const int smin = (ngroups + gmax - 1) / gmax;  // a split's images must fit in LDS
+    // One 32-row tile per wavefront, QG_WAVES per workgroup.  Splits: enough
+    // workgroups for every resident slot (two workgroups per CU fit in LDS
+    // except for Q6_K's 240-byte lines), at least two groups each.
+    const int brows = 32 * QG_WAVES;
+    int blocks = 0;
+    for (int i = 0; i < cnt; i++) blocks += (en[i].rows + brows - 1) / brows;
+    const int per_cu = type == QT_Q6_K ? 1 : 2;
     int splits = qh_mmq_splits_env();
-    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, gmax, big ? 2 * QG_TARGET_WGS : QG_TARGET_WGS);
+    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, ngroups, per_cu * QG_TARGET_WGS);
     splits = splits < ngroups ? splits : ngroups;
-    splits = splits > smin ? splits : smin;
     const int64_t pb = (int64_t)(brows / 32) * 16 * 32;  // floats of one partial block (16-token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
-    if (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES)) {
+    const bool img_fits = (int64_t)nslots * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES;
+    if (!img_fits || (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES))) {
         if (cnt > 1) {
             hipError_t e = qg_run(type, en, cnt / 2, in_dim, row_bytes, sc, st, accum);
             return e != hipSuccess ? e : qg_run(type, en + cnt / 2, cnt - cnt / 2, in_dim, row_bytes, sc, st, accum);
@@ -803,12 +809,16 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     }
     gs.bstart[QG_MAXG] = INT_MAX;
     gs.accum = accum;
+    // the token blocks' x images, once per launch
+    xs.img = sc.img;
+    xs.img_bytes = (uint32_t)(nslots * ngroups * XImg::BYTES);
+    hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
     switch (type) {
-        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        default: launch_mmq_nt<GQ6K>(ntmax, big, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
     }
     return hipGetLastError();
 }
