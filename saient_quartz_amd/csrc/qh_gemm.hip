@@ -46,9 +46,9 @@ typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 #endif
 #define QG_TARGET_WGS 256   // workgroups a launch aims for (one per CU)
 #define QG_PART_TILES 8192  // row blocks with split-K counters (one per wavefront)
-#ifndef QG_NBUF
 #define QG_NBUF 2           // items of weights in flight per wavefront (register sets)
-#endif
+#define QG_GMAX 5           // groups per K split (their x images stay in LDS)
+#define QG_DIG_BLOCKS 128   // row blocks per token block up to which a launch digitises x in the kernel
 #define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
 
 // ---------------------------------------------------------------- f16 operands
@@ -328,26 +328,11 @@ static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVE
 //     token's results NaN).
 // Tokens past the block's n write nothing (their rows are never read back
 // into results).
-__global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
-    const int g = blockIdx.x, slot = blockIdx.y, ngroups = in_dim >> 8;
-    const int lane = threadIdx.x & 63, xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
-    const int n = xs.n[slot];
-    if (xt >= n) return;  // whole half-wavefronts: the reductions below stay within live lanes
-    const float* xp = xs.x[slot] + (size_t)xt * in_dim + 256 * g + 8 * xc;
-    const float* x2p = xs.x2[slot];
-    float v[8];
-    {
-        const float4 a = *reinterpret_cast<const float4*>(xp), b = *reinterpret_cast<const float4*>(xp + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    }
-    if (x2p) {
-        // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
-        const float* up = x2p + (size_t)xt * in_dim + 256 * g + 8 * xc;
-        const float4 a = *reinterpret_cast<const float4*>(up), b = *reinterpret_cast<const float4*>(up + 4);
-        const float u8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (v[i] / (1.f + expf(-v[i]))) * u8[i];
-    }
+// Digitise one 8-element chunk of the image: token t = xt, elements 8 xc ..
+// 8 xc + 7 of the group (xc < 32), values v; the 32 lanes of a token form one
+// half of a wavefront and must all take part (lanes with `on` false hold
+// zeros and write nothing).  `im` is the group's image (global or LDS).
+QH_DEV void qg_digitise(const float* v, bool on, int lane, int xt, int xc, unsigned char* im) {
     float m = 0.f, sum = 0.f;
     bool fin = true;
 #pragma unroll
@@ -378,22 +363,57 @@ __global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* _
         hi4[i] = __builtin_bit_cast(uint32_t, hp);
         lo4[i] = __builtin_bit_cast(uint32_t, lp);
     }
-    unsigned char* im = img + ((size_t)slot * ngroups + g) * XImg::BYTES;
     const int u = xc >> 1, c = xc & 1;
-    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 32 * c)) = qh_u32x4{hi4[0], hi4[1], hi4[2], hi4[3]};
-    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 1 + 32 * c)) = qh_u32x4{lo4[0], lo4[1], lo4[2], lo4[3]};
     // sub-block sb = xc / 4: the sum over 4 lanes (a DPP quad)
     sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
     sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
     const float s5 = sum * ldexpf(1.0f, s - 5);
     const auto p5 = __builtin_amdgcn_cvt_pkrtz(s5, 0.f);
     const auto q5 = __builtin_amdgcn_cvt_pkrtz(s5 - (float)p5[0], 0.f);
+    if (!on) return;
+    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 32 * c)) = qh_u32x4{hi4[0], hi4[1], hi4[2], hi4[3]};
+    *reinterpret_cast<qh_u32x4*>(im + 1024 * u + 16 * (2 * xt + 1 + 32 * c)) = qh_u32x4{lo4[0], lo4[1], lo4[2], lo4[3]};
     const int sb = xc >> 2;
     if ((xc & 3) == 0) {
         const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, p5[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, q5[0]) << 16);
         *reinterpret_cast<uint32_t*>(im + XImg::SUM + 16 * (xt + 16 * (sb >> 2)) + 4 * (sb & 3)) = pair;
     }
     if (xc == 0) im[XImg::EXP + xt] = (unsigned char)(signed char)(fb ? 127 : s);
+}
+
+// x (and the SwiGLU up operand x2) of one token chunk: 8 floats at p (and p2).
+QH_DEV void qg_chunk(const qh_u32x4* xr, const qh_u32x4* ur, bool swiglu, float* v) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] = __uint_as_float(xr[0][i]);
+        v[4 + i] = __uint_as_float(xr[1][i]);
+    }
+    if (swiglu) {
+        // SwiGLU fused in: x = silu(gate) * up, qg_swiglu's expression
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = (v[i] / (1.f + expf(-v[i]))) * __uint_as_float(ur[0][i]);
+            v[4 + i] = (v[4 + i] / (1.f + expf(-v[4 + i]))) * __uint_as_float(ur[1][i]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
+    const int g = blockIdx.x, slot = blockIdx.y, ngroups = in_dim >> 8;
+    const int lane = threadIdx.x & 63, xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
+    const int n = xs.n[slot];
+    if (xt >= n) return;  // whole half-wavefronts: the reductions stay within live lanes
+    const uint32_t off = 4u * ((uint32_t)xt * (uint32_t)in_dim + 256u * (uint32_t)g + 8u * (uint32_t)xc);
+    const QhBuf xb = qh_buf(xs.x[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+    qh_u32x4 xr[2] = {qh_ld128(xb, off), qh_ld128(xb, off + 16u)}, ur[2] = {};
+    if (xs.x2[slot]) {
+        const QhBuf ub = qh_buf(xs.x2[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+        ur[0] = qh_ld128(ub, off);
+        ur[1] = qh_ld128(ub, off + 16u);
+    }
+    float v[8];
+    qg_chunk(xr, ur, xs.x2[slot] != nullptr, v);
+    qg_digitise(v, true, lane, xt, xc, img + ((size_t)slot * ngroups + g) * XImg::BYTES);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -411,7 +431,7 @@ QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<con
 // A wavefront's results belong to its own rows, so no reduction over
 // wavefronts is needed, and split-K partials are combined per wavefront (see
 // the end).
-template <class F, int NT, int W>
+template <class F, int NT, int W, int MODE>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
                                                  int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     constexpr int CH = F::CH, RS = F::RS;
@@ -423,11 +443,13 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     constexpr int TPW = 1;                     // 32-row tiles per wavefront
     constexpr int GRIDB = F::GRID ? IQT_BYTES : 0;  // IQ codebook and sign tables
     constexpr int IMB = XI::BYTES;
-    __shared__ __align__(16) unsigned char lds[2 * IMB + W * TILE + GRIDB];
+    constexpr bool RES = MODE != 0;
+    constexpr int NSLOT = RES ? QG_GMAX : 2;  // image slots in LDS
+    __shared__ __align__(16) unsigned char lds[NSLOT * IMB + W * TILE + GRIDB];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
-    unsigned char* wl = lds + 2 * IMB + w * TILE;
-    unsigned char* gridl = lds + 2 * IMB + W * TILE;
+    unsigned char* wl = lds + NSLOT * IMB + w * TILE;
+    unsigned char* gridl = lds + NSLOT * IMB + W * TILE;
     if constexpr (F::GRID != 0) qg_iq_tables<F::GRID>(gridl, threadIdx.x, 64 * W);
     // This workgroup's matrix (uniform), row block and K split.  Every matrix's
     // workgroups start at a multiple of `splits`, so blockIdx / splits is a
@@ -475,15 +497,23 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // ---- x images (built by qg_ximage), one group at a time: 16-byte chunk
-    // id = tid + 64 W p (pass p < XP) of group grp(i)'s image is loaded with
-    // the weights one iteration ahead and stored to the LDS ring.
+    // ---- x images (built by qg_ximage), 16-byte chunk id = tid + 64 W p
+    // (pass p < XP) of a group's image per thread.
+    //   MODE 1: the split's nk <= QG_GMAX images are copied to LDS once (item
+    //     i's at slot i): all their loads go out first, then the first weight
+    //     items, and only the image loads are waited for.  The item loop then
+    //     runs without workgroup barriers.
+    //   MODE 2: as MODE 1, but the workgroup digitises the split's x (and
+    //     SwiGLU operand) itself: no qg_ximage launch; thread tid < 32 NT
+    //     takes token tid / 32, elements 8 (tid % 32) .. + 7 of each group.
+    //   MODE 0: one group at a time through a slot pair, loaded with the
+    //     weights one iteration ahead; one workgroup barrier per group orders
+    //     the pair.
     constexpr int NCH = XI::BYTES / 16;
     constexpr int XP = (NCH + 64 * W - 1) / (64 * W);
     const QhBuf xb = qh_buf(xs.img, xs.img_bytes);
     const uint32_t ibase = (uint32_t)slot * (uint32_t)ngroups * (uint32_t)XI::BYTES + 16u * threadIdx.x;
-    qh_u32x4 xr[XP];
-    auto load_x = [&](int i) {  // item i: group grp(i)
+    auto load_x = [&](int i, qh_u32x4* xr) {  // item i: group grp(i)
 #pragma unroll
         for (int p = 0; p < XP; p++) {
             const int id = threadIdx.x + 64 * W * p;
@@ -491,25 +521,67 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
                                                        : 0x80000000u);
         }
     };
-    auto store_x = [&](unsigned char* im) {
+    auto store_x = [&](unsigned char* im, const qh_u32x4* xr) {
 #pragma unroll
         for (int p = 0; p < XP; p++) {
             const int id = threadIdx.x + 64 * W * p;
             if (id < NCH) *reinterpret_cast<qh_u32x4*>(im + 16 * id) = xr[p];
         }
     };
-
-    // Prologue: group 0's image, then the first QG_NBUF groups' weights, then
-    // group 0's image to LDS (waiting only for its loads) and group 1's loads.
     qh_u32x4 wr[QG_NBUF][NH];
-    load_x(0);
-    __builtin_amdgcn_sched_barrier(0);
+    qh_u32x4 xq[RES ? 1 : XP];  // streamed: the next group's image
+    if constexpr (MODE == 2) {
+        static_assert(32 * NT <= 64 * W, "one chunk per thread");
+        const int xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
+        const bool xon = (int)threadIdx.x < 32 * NT && xt < n;
+        const QhBuf fb = qh_buf(xs.x[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+        const QhBuf ub = qh_buf(xs.x2[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+        const bool swiglu = xs.x2[slot] != nullptr;
+        const uint32_t xo = 4u * ((uint32_t)xt * (uint32_t)in_dim + 8u * (uint32_t)xc);
+        qh_u32x4 xd[QG_GMAX][2], ud[QG_GMAX][2];
 #pragma unroll
-    for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
-    __builtin_amdgcn_sched_barrier(0);
-    store_x(lds);
-    load_x(1);
-    __syncthreads();  // image 0 (and the codebook) visible to every wavefront
+        for (int k = 0; k < QG_GMAX; k++) {
+            const uint32_t off = (xon && k < nk) ? xo + 1024u * (uint32_t)grp(k) : 0x80000000u;
+            xd[k][0] = qh_ld128(fb, off);
+            xd[k][1] = qh_ld128(fb, off + 16u);
+            const uint32_t uoff = swiglu ? off : 0x80000000u;
+            ud[k][0] = qh_ld128(ub, uoff);
+            ud[k][1] = qh_ld128(ub, uoff + 16u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < QG_GMAX; k++)
+            if (k < nk) {
+                float v[8];
+                qg_chunk(xd[k], ud[k], swiglu, v);
+                qg_digitise(v, xon, lane, xt, xc, lds + k * IMB);
+            }
+    } else if constexpr (RES) {
+        qh_u32x4 xr[QG_GMAX][XP];
+#pragma unroll
+        for (int k = 0; k < QG_GMAX; k++) load_x(k < nk ? k : nk, xr[k]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < QG_GMAX; k++)
+            if (k < nk) store_x(lds + k * IMB, xr[k]);
+    } else {
+        // group 0's image, the first QG_NBUF groups' weights, group 0's image
+        // to LDS (waiting only for its loads), then group 1's image loads
+        load_x(0, xq);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
+        __builtin_amdgcn_sched_barrier(0);
+        store_x(lds, xq);
+        load_x(1, xq);
+    }
+    __syncthreads();  // images (and the codebook) visible to every wavefront
 
     // Result slots of this lane: slot (q, r) of tile tt is token t = 4q + 2hh + r
     // of the tile's row R.
@@ -570,22 +642,25 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
             }
     };
 
-    // Item i: stage group i's weights; store image (i + 1) % 2 from the loads
-    // of one iteration ago (every wavefront finished reading that slot before
-    // the last barrier); load group i + 2's image, then refill the register
-    // set with group i + QG_NBUF's weights (image first: a wait for it then
-    // leaves the weight loads in flight); compute group i against slot i % 2.
+    // Item i in register set i % QG_NBUF, refilled with item i + QG_NBUF as
+    // soon as it is staged (past the split: out of range, no traffic).
+    // Streamed images: image (i + 1) % 2 is stored from the loads of one
+    // iteration ago (every wavefront finished reading that slot before the
+    // last barrier) and group i + 2's image loads go out before the weights
+    // (a wait for them then leaves the weight loads in flight).
     for (int i0 = 0; i0 < nk; i0 += QG_NBUF) {
 #pragma unroll
         for (int b = 0; b < QG_NBUF; b++) {
             const int i = i0 + b;
             if (i < nk) {
                 stage_w(wr[b]);
-                if (i + 1 < nk) store_x(lds + ((i + 1) & 1) * IMB);
-                load_x(i + 2);
+                if constexpr (!RES) {
+                    if (i + 1 < nk) store_x(lds + ((i + 1) & 1) * IMB, xq);
+                    load_x(i + 2, xq);
+                }
                 load_w(i + QG_NBUF, wr[b]);
-                compute(lds + (i & 1) * IMB, tot[0]);
-                __syncthreads();
+                compute(lds + (RES ? i : (i & 1)) * IMB, tot[0]);
+                if constexpr (!RES) __syncthreads();
             }
         }
     }
@@ -695,6 +770,16 @@ static const QgScratch* qh_mmq_scratch_ptrs() {
     return &p;
 }
 
+// QUARTZ_HIP_MMQ_MODE=m forces the image mode (0 streamed, 1 resident, 2
+// resident and digitised in the kernel) where it applies (tuning).
+static int qh_mmq_mode_env() {
+    static const int v = [] {
+        const char* e = getenv("QUARTZ_HIP_MMQ_MODE");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+
 // QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row block (tuning).
 static int qh_mmq_splits_env() {
     static const int v = [] {
@@ -706,18 +791,25 @@ static int qh_mmq_splits_env() {
 
 // Launch shape: QG_WAVES wavefronts (32-row tiles) per workgroup.
 template <class F, int NT>
-static void launch_mmq_t(const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+static void launch_mmq_t(int mode, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
                          uint32_t row_bytes, int in_dim, hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes,
-                       in_dim, splits, sc.part, sc.cnt);
+    if (mode == 2)
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 2>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
+                           row_bytes, in_dim, splits, sc.part, sc.cnt);
+    else if (mode == 1)
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 1>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
+                           row_bytes, in_dim, splits, sc.part, sc.cnt);
+    else
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 0>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
+                           row_bytes, in_dim, splits, sc.part, sc.cnt);
 }
 
 template <class F>
-static void launch_mmq_nt(int nt, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
+static void launch_mmq_nt(int nt, int mode, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
                           const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (nt <= 4) launch_mmq_t<F, 4>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else if (nt <= 8) launch_mmq_t<F, 8>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq_t<F, 16>(gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    if (nt <= 4) launch_mmq_t<F, 4>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 8) launch_mmq_t<F, 8>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq_t<F, 16>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
 }
 
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
@@ -729,8 +821,8 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
 };
 
 // K splits per row block: the count s (at least 2 groups per split where K
-// allows, at most gmax, the groups whose x images fit in LDS) that minimises
-// the rounds of `target` workgroups times the groups each one walks, the
+// allows, at least ngroups / gmax) that minimises the rounds of `target`
+// workgroups times the groups each one walks (counted as at least 4), the
 // fewest splits on ties.
 static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
     const int smin = (ngroups + gmax - 1) / gmax;
@@ -740,7 +832,11 @@ static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
     int64_t best_cost = INT64_MAX;
     for (int s = smin; s <= cap; s++) {
         const int64_t rounds = ((int64_t)blocks * s + target - 1) / target;
-        const int64_t cost = rounds * ((ngroups + s - 1) / s);
+        // a workgroup's fixed costs (pipeline fill, split merge) make splits of
+        // fewer than 4 groups as slow as 4 (measured: 14336 x 4096 Q4_K at 16
+        // tokens 21.7 us with 4 splits of 4 groups, 29.7 with 8 of 2)
+        const int gps = (ngroups + s - 1) / s;
+        const int64_t cost = rounds * (gps > 4 ? gps : 4);
         if (cost < best_cost) {
             best_cost = cost;
             best = s;
@@ -775,15 +871,24 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         ntmax = en[i].n > ntmax ? en[i].n : ntmax;
     }
     // One 32-row tile per wavefront, QG_WAVES per workgroup.  Splits: enough
-    // workgroups for every resident slot (two workgroups per CU fit in LDS
-    // except for Q6_K's 240-byte lines), at least two groups each.
+    // workgroups for one per CU (the kernel's registers allow no second).
     const int brows = 32 * QG_WAVES;
     int blocks = 0;
     for (int i = 0; i < cnt; i++) blocks += (en[i].rows + brows - 1) / brows;
-    const int per_cu = type == QT_Q6_K ? 1 : 2;
+    // Splits for streamed images; when they leave at most QG_GMAX groups per
+    // split (launches of about one round), the split's images stay resident
+    // in LDS instead and the item loop needs no workgroup barriers.
     int splits = qh_mmq_splits_env();
-    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, ngroups, per_cu * QG_TARGET_WGS);
+    if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, ngroups, QG_TARGET_WGS);
     splits = splits < ngroups ? splits : ngroups;
+    const bool res = (ngroups + splits - 1) / splits <= QG_GMAX;
+    // Resident images are digitised in the kernel (no image launch) when few
+    // row blocks share each token block's x; otherwise qg_ximage digitises
+    // each block's x once.
+    int mode = res ? (blocks <= QG_DIG_BLOCKS * nslots ? 2 : 1) : 0;
+    const int fm = qh_mmq_mode_env();
+    if (fm == 0) mode = 0;
+    else if (fm >= 1 && fm <= 2 && res) mode = fm;
     const int64_t pb = (int64_t)(brows / 32) * 16 * 32;  // floats of one partial block (16-token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
@@ -812,13 +917,14 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     // the token blocks' x images, once per launch
     xs.img = sc.img;
     xs.img_bytes = (uint32_t)(nslots * ngroups * XImg::BYTES);
-    hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
+    if (mode != 2)
+        hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
     switch (type) {
-        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        default: launch_mmq_nt<GQ6K>(ntmax, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
     }
     return hipGetLastError();
 }
