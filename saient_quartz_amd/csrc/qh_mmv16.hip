@@ -758,7 +758,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
             // wavefront's slot; the sum over wavefronts waits for a full set.
 #pragma unroll
             for (int k = 0; k < NT; k++) {
-                float v = tot[k] + bad[k];
+                // a non-finite x element in any lane's share makes every row NaN
+                const float bw = __ballot(!__builtin_isfinite(bad[k])) ? __builtin_nanf("") : 0.f;
+                float v = tot[k] + bw;
                 v += __shfl_xor(v, 16);
                 v += __shfl_xor(v, 32);
                 if (lane < 16) red[(((done % (2 * RING)) * NT + k) * W + w) * 16 + lane] = v;

@@ -395,3 +395,24 @@ def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
         ref = oracle.gemm(t, xn, d, in_dim, o, n)
         for r in range(n):
             assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
+
+
+@pytest.mark.parametrize("t", [12, 14, 8, 21])
+@pytest.mark.parametrize("n", [1, 3, 16])
+def test_non_finite_x_flags_rows(qh, oracle, t, n):
+    """An Inf in x (one element of one token): every output row of that token
+    that the reference makes non-finite (+-Inf where the row's weight there is
+    nonzero, NaN where it is zero) is non-finite here too (this build returns
+    NaN for them, not the reference's signed Inf), and the other tokens' rows
+    keep the 1e-3 bar."""
+    out_dim, in_dim = 70, 4096
+    data = synth.weights(t, out_dim, in_dim, seed=1200 + t)
+    x = synth.activations(n, in_dim, seed=1201 + n)
+    x[0, 777] = np.inf
+    got = gpu_gemv(qh, t, x[0], data, in_dim, out_dim)[None] if n == 1 else gpu_gemm(qh, t, x, data, in_dim,
+                                                                                     out_dim, n)
+    ref = oracle.gemv(t, x[0], data, in_dim, out_dim)[None] if n == 1 else oracle.gemm(t, x, data, in_dim, out_dim, n)
+    assert not np.isfinite(ref[0]).any()  # random weights: no zero weight at column 777
+    assert np.array_equal(np.isfinite(got[0]), np.isfinite(ref[0]))
+    for k in range(1, n):
+        assert cf.rel_l2(got[k], ref[k]) < TOL
