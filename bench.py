@@ -5,10 +5,11 @@
 Workload: Q4_K GEMV, W 14336 x 4096 in GGUF Q4_K
 superblocks, f32 x ~ N(0,1), batch 1.  A step is one hip_gemv_async call over
 one of ROT weight copies (>= 768 MB in total, so the 256 MB MALL cannot serve
-repeats); weights and x are resident in HBM before the timed region.  The K
-steps are captured into one HIP graph and timed as one replay.
+repeats); weights and x are resident in HBM before the timed region.  The W
+warm-up steps and the K timed steps are captured into one HIP graph with a
+device timestamp on each side of the K; one replay is timed.
 Prints ONE JSON line.  `value` = algorithmic bytes (weights + x + y) per step x K
-/ wall time of the K steps (HIP events around the replay).
+/ GPU time of the K steps (device wall-clock stamps around them).
 """
 import argparse
 import json
@@ -102,26 +103,40 @@ def main():
     # The K steps are captured into one HIP graph (the same C-ABI calls, on
     # torch's capture stream) so the timing is the GPU's, not Python's launch
     # rate.  Step i uses weight copy i % rot.
+    # One HIP graph holds W untimed warm-up steps, a device timestamp, the K
+    # timed steps and a second timestamp (the same C-ABI calls, captured on
+    # torch's capture stream).  The timed steps run back to back behind steps
+    # already streaming, and the stamps (written by one-thread kernels when the
+    # preceding step has completed) bracket exactly the K steps: no graph
+    # submission or first-launch ramp inside the timed region.  Step i uses
+    # weight copy i % rot.
+    stamps = torch.zeros(2, dtype=torch.int64, device="cuda")
+    khz = L.hip_wallclock_khz()
+    if khz <= 0:
+        raise SystemExit("hip_wallclock_khz failed")
     graph = torch.cuda.CUDAGraph()
+    nw_graph = max(args.warmup, 1)
     with torch.cuda.graph(graph):
         cs = torch.cuda.current_stream().cuda_stream
-        for i in range(args.steps):
+        for i in range(nw_graph):
             step_on(cs, i)
+        check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr(), cs))
+        for i in range(args.steps):
+            step_on(cs, nw_graph + i)
+        check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr() + 8, cs))
     graph.replay()  # warm replay
     torch.cuda.synchronize()
     y_graph = y.clone()
-    step(args.steps - 1)  # the graph's last step, launched eagerly
+    step(nw_graph + args.steps - 1)  # the graph's last step, launched eagerly
     torch.cuda.synchronize()
     if not torch.equal(y, y_graph):
         raise SystemExit("graph replay result differs from the eager launch")
 
-    # Timed region: one replay = K back-to-back steps, events on the replay
-    # stream.  A short spin kernel is queued first, so the graph is submitted
-    # while the GPU is still busy and the events bracket the K steps' GPU time
-    # only (without it a cold 20-step replay carries ~25 us of submission
-    # latency, 1.3 us per step).
+    # Timed region: the K steps of one replay, between the graph's stamps.
+    graph.replay()
     torch.cuda.synchronize()
-    total_ms = timed_replay(torch, graph)
+    t0, t1 = (int(v) for v in stamps.tolist())
+    total_ms = (t1 - t0) / khz
     ms_per_step = total_ms / args.steps
 
     # Kernel duration: the K kernels run back to back inside the graph, so the
@@ -161,8 +176,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "qh_mmv16<M16Q4K, 16, 1, true, false, false, 1>",
                      "kernel_us": round(kern_ms * 1e3, 3),
-                     "kernel_us_source": "HIP events around the K back-to-back launches of the timed replay, per launch "
-                                         "(dispatch gaps included)",
+                     "kernel_us_source": "device wall-clock stamps around the K back-to-back launches of the timed "
+                                         "replay, per launch (dispatch gaps included: an upper bound on the kernel)",
                      "rocprof_kernel_us": profiled_kernel_us(ROOT / "profiles" / "mmv16_q4k_14336x4096_kernel_stats.md")},
         "cpu_baseline": cpu,
         "decode": decode,

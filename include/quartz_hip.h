@@ -224,6 +224,13 @@ int hip_set_ksigns(const uint8_t* host);
 
 /* Diagnostics. */
 const char* hip_status_string(int status);
+/* Device timestamps for timing work inside captured HIP graphs (no counterpart in
+ * the reference; for benchmarks): a one-thread kernel on `stream` writes the
+ * device's constant-rate wall clock (s_memrealtime) to *dst when it runs, i.e.
+ * after the stream's previous work completes.  hip_wallclock_khz gives that
+ * clock's rate (0 on failure). */
+int hip_timestamp_async(uint64_t* dst, void* stream);
+int hip_wallclock_khz(void);
 const char* hip_last_error(void); /* last HIP error seen on this host thread ("" if none) */
 
 /* ---------------------------------------------------------------- decode-step glue

@@ -150,6 +150,8 @@ _SIGS = {
     "hip_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "hip_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "hip_sync": (C.c_int, []),
+    "hip_timestamp_async": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "hip_wallclock_khz": (C.c_int, []),
     "hip_mem_info": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
     "hip_set_iq3s_grid": (C.c_int, [C.c_void_p]),
     "hip_set_iq2s_grid": (C.c_int, [C.c_void_p]),

@@ -846,6 +846,22 @@ int hip_d2h(void* dst, const void* src, size_t bytes) {
     return QH_OK;
 }
 
+__global__ void qh_timestamp_k(uint64_t* dst) { *dst = __builtin_amdgcn_s_memrealtime(); }
+
+int hip_timestamp_async(uint64_t* dst, void* stream) {
+    if (!dst) return QH_ERR_NULL;
+    hipLaunchKernelGGL(qh_timestamp_k, dim3(1), dim3(1), 0, (hipStream_t)stream, dst);
+    QH_CHECK(hipGetLastError(), "hip_timestamp_async");
+    return QH_OK;
+}
+
+int hip_wallclock_khz(void) {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+        return 0;
+    return khz;
+}
+
 int hip_sync(void) {
     QH_CHECK(hipDeviceSynchronize(), "hip_sync");
     return QH_OK;
