@@ -820,23 +820,22 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
     int n, rows, ldy;
 };
 
-// K splits per row block: the count s (at least 2 groups per split where K
-// allows, at least ngroups / gmax) that minimises the rounds of `target`
-// workgroups times the groups each one walks (counted as at least 4), the
-// fewest splits on ties.
+// K splits per row block: the count s (at least ngroups / gmax) that
+// minimises the rounds of `target` workgroups times (3 + the groups each one
+// walks), the fewest splits on ties.
 static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
     const int smin = (ngroups + gmax - 1) / gmax;
-    int cap = ngroups / 2 > 1 ? ngroups / 2 : 1;
-    cap = cap > smin ? cap : smin;
+    const int cap = ngroups > smin ? ngroups : smin;
     int best = smin;
     int64_t best_cost = INT64_MAX;
     for (int s = smin; s <= cap; s++) {
         const int64_t rounds = ((int64_t)blocks * s + target - 1) / target;
-        // a workgroup's fixed costs (pipeline fill, split merge) make splits of
-        // fewer than 4 groups as slow as 4 (measured: 14336 x 4096 Q4_K at 16
-        // tokens 21.7 us with 4 splits of 4 groups, 29.7 with 8 of 2)
+        // a workgroup's fixed costs (pipeline fill, split merge) weigh about
+        // as much as 3 groups of weights (measured: 14336 x 4096 Q4_K at 16
+        // tokens 21.7 us with 4 splits of 4 groups, 29.7 with 8 of 2 in two
+        // rounds; 1024 x 4096 Q6_K 20.6 us with 4 splits on 16 workgroups)
         const int gps = (ngroups + s - 1) / s;
-        const int64_t cost = rounds * (gps > 4 ? gps : 4);
+        const int64_t cost = rounds * (3 + gps);
         if (cost < best_cost) {
             best_cost = cost;
             best = s;
