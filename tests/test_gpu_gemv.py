@@ -173,8 +173,11 @@ def test_gemm_vs_oracle(qh, oracle, t, n):
 # The matrix-core batched path (Q4_K, Q5_K, Q6_K, IQ3_S, IQ2_XXS): token counts that use each
 # token-tile size (2, 4, 8, 16) and the chunking past 16; shapes with several K
 # chunks, a partial last row tile and more tiles than one workgroup keeps.
+# The last two reach the kernel's other x-image modes: 40000 x 1024 (157 row
+# blocks sharing x, one split of 4 groups: images from the prologue launch,
+# resident) and 9000 x 16384 (7 splits of 9-10 groups: images streamed).
 MMQ_CASES = [(40, 4096, 2), (40, 4096, 3), (77, 4096, 5), (300, 14336, 8), (100, 4096, 11), (130, 2048, 16),
-             (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4)]
+             (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4), (40000, 1024, 16), (9000, 16384, 16)]
 
 
 @pytest.mark.parametrize("t", [12, 13, 14, 21, 16])
