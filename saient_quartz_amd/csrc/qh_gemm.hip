@@ -273,9 +273,11 @@ QH_DEV void qg_iq_tables(unsigned char* tab, int tid, int nthreads) {
 //     + 4 ((t >> 1) & 1) + (t & 1) (so its results land where token t's main
 //     results are), k = 8 (sb >> 2) + 2 (sb & 3) + part, stored at 16 (t + 16
 //     (sb >> 2)) + 2 (2 (sb & 3) + part).
-//   EXP: s of each token slot (127: x not finite).
+//   RSF: 2^-s of each token slot as f32 (NaN: x not finite), token t at float
+//     8 ((t >> 1) & 1) + 2 (t >> 2) + (t & 1), so lane half hh reads its eight
+//     tokens' factors (t = 4q + 2hh + r) as two 16-byte words.
 struct XImg {
-    static constexpr int SUM = 16384, EXP = 16896, BYTES = 16912;  // BYTES: a multiple of 16
+    static constexpr int SUM = 16384, RSF = 16896, BYTES = 16960;  // BYTES: a multiple of 16
 };
 
 #define QG_MAXG 16  // matrices (or row chunks) per grouped launch
@@ -324,8 +326,8 @@ static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVE
 //     f16 (the A operand of the Q4_K/Q5_K mins MFMA): row rho(t) = 8 (t >> 2) +
 //     4 ((t >> 1) & 1) + (t & 1), k = 8 (sb >> 2) + 2 (sb & 3) + part, stored
 //     at 16 (t + 16 (sb >> 2)) + 2 (2 (sb & 3) + part);
-//   EXP: s of each token (127: the group holds an Inf or NaN, which makes the
-//     token's results NaN).
+//   RSF: 2^-s of each token as f32 (NaN when the group holds an Inf or NaN,
+//     which makes the token's results NaN).
 // Tokens past the block's n write nothing (their rows are never read back
 // into results).
 // Digitise one 8-element chunk of the image: token t = xt, elements 8 xc ..
@@ -378,7 +380,9 @@ QH_DEV void qg_digitise(const float* v, bool on, int lane, int xt, int xc, unsig
         const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, p5[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, q5[0]) << 16);
         *reinterpret_cast<uint32_t*>(im + XImg::SUM + 16 * (xt + 16 * (sb >> 2)) + 4 * (sb & 3)) = pair;
     }
-    if (xc == 0) im[XImg::EXP + xt] = (unsigned char)(signed char)(fb ? 127 : s);
+    if (xc == 0)
+        reinterpret_cast<float*>(im + XImg::RSF)[8 * ((xt >> 1) & 1) + 2 * (xt >> 2) + (xt & 1)] =
+            fb ? __builtin_nanf("") : ldexpf(1.0f, -s);
 }
 
 // x (and the SwiGLU up operand x2) of one token chunk: 8 floats at p (and p2).
@@ -625,15 +629,14 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
             dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, F::minh(hd, hh), dm, 0, 0, 0);
         }
         // finish: slot (q, r) = token 4q + 2hh + r (rows 2t, 2t + 1: registers
-        // 4q + 2r, 4q + 2r + 1), exponent byte t of the image
-        const qh_u32x4 ex = qh_lds128(im + XI::EXP);
+        // 4q + 2r, 4q + 2r + 1), its 2^-s at float 8 hh + 2q + r of the image
+        const qh_u32x4 rs0 = qh_lds128(im + XI::RSF + 32 * hh), rs1 = qh_lds128(im + XI::RSF + 32 * hh + 16);
+        const uint32_t rsw[8] = {rs0.x, rs0.y, rs0.z, rs0.w, rs1.x, rs1.y, rs1.z, rs1.w};
 #pragma unroll
         for (int q = 0; q < NQ; q++)
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                const int t = 4 * q + 2 * hh + r;
-                const int se = ((int)(ex[t >> 2] << (24 - 8 * (t & 3)))) >> 24;
-                const float rs = se == 127 ? __builtin_nanf("") : ldexpf(1.0f, -se);
+                const float rs = __uint_as_float(rsw[2 * q + r]);
                 const float P = c0[4 * q + 2 * r] + c0[4 * q + 2 * r + 1];
                 if constexpr (F::SUMS)
                     tot[2 * q + r] += (hd.d * P - hd.dm * 32.0f * dm[4 * q + r]) * rs;
