@@ -150,8 +150,12 @@ int hip_gemm_grouped_norm_static_async(uint32_t ggml_type, int count, const uint
  * (types[k] for W[k]): a batch's norm + q/k/v when v has its own type, as
  * Q4_K_M models have (src/cuda.rs:549-562).  For 2..4 tokens, two types among
  * Q4_K/Q5_K + Q6_K and in_dim <= 4096, one launch computes every matrix; each
- * token's result then equals the per-type call's bit for bit.  Otherwise one
- * hip_gemm_grouped_norm_async per type, with its scratch rule. */
+ * token's result then equals the per-type call's bit for bit.  For 5..16
+ * tokens of Q4_K + Q6_K, the rows are normalised once into d_scratch (n *
+ * in_dim floats) and both types run in one batched matrix-core launch; each
+ * token's result equals the per-type batched call's within rounding (the split
+ * of K may differ).  Otherwise one hip_gemm_grouped_norm_async per type, with
+ * its scratch rule. */
 int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* const* d_data, const float* d_x,
                               const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
                               float* d_scratch, void* stream);

@@ -416,6 +416,32 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
             if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
         }
     }
+    // 5-16 tokens of two types (a layer's q/k in Q4_K and v in Q6_K): the rows
+    // normalised once into scratch, then both types in one batched launch.
+    if (n >= 5 && n <= 16 && nut == 2 && scratch && !qh_force_valu()) {
+        bool ok = true;
+        for (int k = 0; k < count; k++)
+            ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
+        if (ok) {
+            QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st, n), "hip_gemm_group_norm");
+            hipError_t e = qh_launch_mmq_mixed(ut[0], cnt[0], wu[0], yu[0], ou[0], ut[1], cnt[1], wu[1], yu[1], ou[1],
+                                               scratch, n, in_dim, st);
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
+            // scratch holds the normalised rows: one grouped call per type
+            for (int u = 0; u < nut; u++) {
+                const float* xs[8];
+                int ns[8];
+                for (int i = 0; i < cnt[u]; i++) {
+                    xs[i] = scratch;
+                    ns[i] = n;
+                }
+                int rc = hip_gemm_grouped_async(ut[u], cnt[u], wu[u], xs, yu[u], ns, ou[u], in_dim, stream);
+                if (rc) return rc;
+            }
+            return QH_OK;
+        }
+    }
     for (int u = 0; u < nut; u++) {
         int rc = hip_gemm_grouped_norm_async(ut[u], cnt[u], wu[u], x, norm_w, yu[u], n, ou[u], in_dim, scratch, stream);
         if (rc) return rc;

@@ -436,8 +436,16 @@ QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<con
 // wavefronts is needed, and split-K partials are combined per wavefront (see
 // the end).
 template <class F, int NT, int W, int MODE>
-__global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
-                                                 int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
+constexpr int qh_mmq_lds() {
+    return (MODE != 0 ? QG_GMAX : 2) * XImg::BYTES + W * (32 * F::RS + 16) + (F::GRID ? IQT_BYTES : 0);
+}
+
+// The kernel body for launch-local workgroup bx (a launch may run two formats'
+// bodies side by side, see qh_mmq_mix); lds holds qh_mmq_lds<...>() bytes.
+template <class F, int NT, int W, int MODE>
+__device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, uint32_t row_bytes, int in_dim,
+                                            int splits, float* __restrict__ part, unsigned int* __restrict__ cnt,
+                                            unsigned char* lds, const int bx) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte weight loads per lane per group
     constexpr int TILE = 32 * RS + 16;
@@ -449,7 +457,7 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     constexpr int IMB = XI::BYTES;
     constexpr bool RES = MODE != 0;
     constexpr int NSLOT = RES ? QG_GMAX : 2;  // image slots in LDS
-    __shared__ __align__(16) unsigned char lds[NSLOT * IMB + W * TILE + GRIDB];
+    static_assert(qh_mmq_lds<F, NT, W, MODE>() == NSLOT * IMB + W * TILE + GRIDB, "LDS layout");
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
     unsigned char* wl = lds + NSLOT * IMB + w * TILE;
@@ -460,14 +468,14 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     // launch-wide block index (for the split counters and partials).
     int gi = 0;
 #pragma unroll
-    for (int k = 1; k < QG_MAXG; k++) gi += (int)blockIdx.x >= gs.bstart[k];
+    for (int k = 1; k < QG_MAXG; k++) gi += bx >= gs.bstart[k];
     const int out_dim = gs.rows[gi], slot = gs.slot[gi], ldy = gs.ldy[gi];
     const int n = xs.n[slot];
     float* __restrict__ y = gs.y[gi];
     const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
     const int ngroups = in_dim >> 8;
-    const int lb = blockIdx.x - gs.bstart[gi];
-    const int blk = lb / splits, sp = lb - blk * splits, gblk = blockIdx.x / splits;
+    const int lb = bx - gs.bstart[gi];
+    const int blk = lb / splits, sp = lb - blk * splits, gblk = bx / splits;
     const int tile0 = blk * W + w;  // this wavefront's tile
     const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
     const int nk = g1 - g0;
@@ -753,6 +761,30 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
     if (lane == 0) __hip_atomic_store(&cnt[wslot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
+template <class F, int NT, int W, int MODE>
+__global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
+                                                 int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
+    __shared__ __align__(16) unsigned char lds[qh_mmq_lds<F, NT, W, MODE>()];
+    qh_mmq_body<F, NT, W, MODE>(gs, xs, row_bytes, in_dim, splits, part, cnt, lds, (int)blockIdx.x);
+}
+
+// Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K),
+// both with resident images digitised in the kernel: workgroups below g1 run
+// F1's body on gs1's matrices, the others F2's on gs2's, each with its own
+// splits and its own region of the split-K partials and counters.
+template <class F1, class F2, int NT, int W>
+__global__ __launch_bounds__(64 * W) void qh_mmq_mix(const QgGroups gs1, const QgGroups gs2, const QgXs xs,
+                                                     uint32_t rb1, uint32_t rb2, int in_dim, int s1, int s2, int g1,
+                                                     float* __restrict__ part, unsigned int* __restrict__ cnt,
+                                                     float* __restrict__ part2, unsigned int* __restrict__ cnt2) {
+    constexpr int L1 = qh_mmq_lds<F1, NT, W, 2>(), L2 = qh_mmq_lds<F2, NT, W, 2>();
+    __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
+    if ((int)blockIdx.x < g1)
+        qh_mmq_body<F1, NT, W, 2>(gs1, xs, rb1, in_dim, s1, part, cnt, lds, (int)blockIdx.x);
+    else
+        qh_mmq_body<F2, NT, W, 2>(gs2, xs, rb2, in_dim, s2, part2, cnt2, lds, (int)blockIdx.x - g1);
+}
+
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
 struct QgScratch { float* part; unsigned int* cnt; unsigned char* img; };
 static const QgScratch* qh_mmq_scratch_ptrs() {
@@ -1009,4 +1041,92 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
                          hipStream_t st) {
     if (n < 2) return hipErrorNotSupported;
     return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st, nullptr, 0, nullptr);
+}
+
+// Two weight types sharing one x of n <= 16 tokens (a layer's q, k in Q4_K and
+// v in Q6_K) in one launch, images digitised in the kernel: Y1[i] = W1[i] X,
+// Y2[i] = W2[i] X (token-major, token stride out_dims).  Splits are chosen
+// jointly: the pair (s1, s2) minimising the rounds of 256 workgroups over both
+// formats times (3 + the longer split), the fewest workgroups on ties.
+// hipErrorNotSupported when the pair, shapes or scratch do not fit; the caller
+// then makes one call per type.
+template <class F1, class F2, int NT>
+static void launch_mmq_mix(const QgGroups& g1s, const QgGroups& g2s, const QgXs& xs, uint32_t rb1, uint32_t rb2,
+                           int in_dim, int s1, int s2, int wgs1, int wgs, const QgScratch& sc, size_t poff, int coff,
+                           hipStream_t st) {
+    hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, g1s, g2s,
+                       xs, rb1, rb2, in_dim, s1, s2, wgs1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
+}
+
+hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
+                               uint32_t t2, int c2, const uint8_t* const* W2, float* const* Y2, const int* o2,
+                               const float* x, int n, int in_dim, hipStream_t st) {
+    if (t1 == QT_Q6_K && t2 == QT_Q4_K)
+        return qh_launch_mmq_mixed(t2, c2, W2, Y2, o2, t1, c1, W1, Y1, o1, x, n, in_dim, st);
+    if (t1 != QT_Q4_K || t2 != QT_Q6_K) return hipErrorNotSupported;
+    if (n < 2 || n > 16 || c1 < 1 || c2 < 1 || c1 > QG_MAXG || c2 > QG_MAXG || in_dim % 256 ||
+        in_dim / 256 > QG_MAX_GROUPS || ((uintptr_t)x & 15u))
+        return hipErrorNotSupported;
+    const QgScratch* sc = qh_mmq_scratch_ptrs();
+    if (!sc) return hipErrorNotSupported;
+    const int ngroups = in_dim / 256, brows = 32 * QG_WAVES;
+    const uint32_t rb1 = (uint32_t)qh_type_size(t1, (size_t)in_dim), rb2 = (uint32_t)qh_type_size(t2, (size_t)in_dim);
+    int b1 = 0, b2 = 0;
+    for (int i = 0; i < c1; i++) {
+        if (o1[i] <= 0 || (int64_t)o1[i] * rb1 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+        b1 += (o1[i] + brows - 1) / brows;
+    }
+    for (int i = 0; i < c2; i++) {
+        if (o2[i] <= 0 || (int64_t)o2[i] * rb2 >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+        b2 += (o2[i] + brows - 1) / brows;
+    }
+    const int smin = (ngroups + QG_GMAX - 1) / QG_GMAX;
+    int s1 = 0, s2 = 0;
+    int64_t best = INT64_MAX, best_wgs = INT64_MAX;
+    for (int a = smin; a <= ngroups; a++)
+        for (int b = smin; b <= ngroups; b++) {
+            const int64_t wgs = (int64_t)b1 * a + (int64_t)b2 * b;
+            const int64_t rounds = (wgs + QG_TARGET_WGS - 1) / QG_TARGET_WGS;
+            const int gps = (ngroups + a - 1) / a > (ngroups + b - 1) / b ? (ngroups + a - 1) / a : (ngroups + b - 1) / b;
+            const int64_t cost = rounds * (3 + gps);
+            if (cost < best || (cost == best && wgs < best_wgs)) {
+                best = cost;
+                best_wgs = wgs;
+                s1 = a;
+                s2 = b;
+            }
+        }
+    const int wgs1 = b1 * s1, wgs = wgs1 + b2 * s2;
+    const int64_t pw = (int64_t)QG_WAVES * 16 * 32;  // floats of one workgroup's partials (16-token bound)
+    if ((int64_t)wgs * pw > QG_PART_FLOATS || b1 + b2 > QG_PART_TILES) return hipErrorNotSupported;
+    QgXs xs = {};
+    xs.x[0] = x;
+    xs.n[0] = n;
+    auto fill = [&](QgGroups& g, int c, const uint8_t* const* Wt, float* const* Y, const int* o, uint32_t rb, int s) {
+        g = QgGroups{};
+        int w = 0;
+        for (int i = 0; i < QG_MAXG; i++) {
+            g.bstart[i] = i < c ? w : INT_MAX;
+            if (i < c) {
+                g.w[i] = Wt[i];
+                g.y[i] = Y[i];
+                g.wbytes[i] = (uint32_t)(((uint64_t)o[i] * rb + 3) & ~(uint64_t)3);
+                g.rows[i] = o[i];
+                g.ldy[i] = o[i];
+                g.slot[i] = 0;
+                w += (o[i] + brows - 1) / brows * s;
+            }
+        }
+        g.bstart[QG_MAXG] = INT_MAX;
+        g.accum = 0;
+    };
+    QgGroups g1s, g2s;
+    fill(g1s, c1, W1, Y1, o1, rb1, s1);
+    fill(g2s, c2, W2, Y2, o2, rb2, s2);
+    const size_t poff = (size_t)wgs1 * pw;
+    const int coff = b1 * QG_WAVES;
+    if (n <= 4) launch_mmq_mix<GQ4K, GQ6K, 4>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
+    else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
+    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
+    return hipGetLastError();
 }

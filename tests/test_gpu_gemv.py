@@ -358,14 +358,17 @@ def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21)], ids=str)
-@pytest.mark.parametrize("n", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("in_dim", [4096, 2048, 5120])
 def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     """hip_gemm_group_norm_async (mixed types: a Q4_K_M layer's q, k (Q4_K) and v
     (Q6_K)): bit-identical to one hip_gemm_grouped_norm_async per type (the
-    two-format launch for 2-4 tokens, the per-type calls otherwise), and within
-    the GEMV bar of the oracle on the normalised rows (float64 norm).  5120 is
-    past the one-workgroup norm; IQ3_S + Q4_K has no two-format kernel."""
+    two-format GEMV launch for 2-4 tokens, the per-type calls otherwise), and
+    within the GEMV bar of the oracle on the normalised rows (float64 norm).
+    Q4_K + Q6_K at 5-16 tokens runs the two-format batched launch, whose K
+    splits may differ from the per-type calls': there the bar is 1e-5 relative
+    against them.  5120 is past the one-workgroup norm; IQ3_S + Q4_K has no
+    two-format kernel."""
     import ctypes as C
     outs = [300, 77, 64][:len(types)]
     rng = np.random.default_rng(n + in_dim + sum(types))
@@ -394,7 +397,11 @@ def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     for b, e, d, o, t in zip(dy, ey, datas, outs, types):
         got = b.download(np.float32)[:n * o].reshape(n, o)
         exp = e.download(np.float32)[:n * o].reshape(n, o)
-        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), (t, o)
+        if n >= 5 and set(types) == {12, 14}:
+            for r in range(n):
+                assert cf.rel_l2(got[r], exp[r]) < 1e-5, (t, o, r)
+        else:
+            assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), (t, o)
         ref = oracle.gemm(t, xn, d, in_dim, o, n)
         for r in range(n):
             assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
