@@ -335,10 +335,12 @@ def moe_leg(torch, reps):
 
 def routed_moe(torch, layer, t, reps):
     """The whole MoE FFN for 64 tokens with top-2 routing on the device
-    (MoeStep: F32 router GEMM, hip_moe_route / plan, one 36-byte tok_off copy to
-    the host, gather, expert GEMMs, SwiGLU, hip_gemm_moe, weighted combine), on
-    the same expert weights.  Not graph-captured (the host reads tok_off), so
-    the time includes that round trip; events around `reps` layer calls."""
+    (MoeStep: F32 router GEMM, hip_moe_route / plan, gather, expert GEMMs with
+    the token ranges read on the device, SwiGLU folded into the down GEMM,
+    weighted combine), on the same expert weights, one HIP graph per layer
+    step; and "host_ranges": the same step with tok_off copied back to build
+    the expert launches on the host (not capturable: events around `reps`
+    eager calls, the round trip included)."""
     from saient_quartz_amd.decode import MoeStep
 
     E, k, n, d, f = layer.E, 2, 64, layer.h, layer.f
@@ -348,9 +350,21 @@ def routed_moe(torch, layer, t, reps):
     x = torch.randn(n, d, device="cuda", generator=gen)
     y = torch.empty(n, d, device="cuda")
     step = MoeStep((t, t, t), layer.wg, layer.wu, layer.wd, rw, E, k, d, f, n_max=n)
+    assert step.device_driven
     step.issue(x, y, n)
     torch.cuda.synchronize()
-    counts = [b - a for a, b in zip(step.tok_off_host.tolist()[:-1], step.tok_off_host.tolist()[1:])]
+    off = step.tok_off.cpu().tolist()
+    counts = [b - a for a, b in zip(off[:-1], off[1:])]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step.issue(x, y, n)
+    g.replay()
+    torch.cuda.synchronize()
+    ms = timed_replay(torch, g, reps) / reps
+    del g
+    step.device_driven = False
+    step.issue(x, y, n)
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -358,10 +372,11 @@ def routed_moe(torch, layer, t, reps):
         step.issue(x, y, n)
     t1.record()
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / reps
+    ms_host = t0.elapsed_time(t1) / reps
     wbytes = sum(3 * layer.slice for c in counts if c)
     return {"ms_per_layer": round(ms, 4), "tokens_per_s": round(n / (ms * 1e-3), 1), "tokens_per_expert": counts,
-            "weight_bytes_touched": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1)}
+            "weight_bytes_touched": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "host_ranges_ms_per_layer": round(ms_host, 4)}
 
 
 def timed_replay(torch, graph, reps=1):

@@ -188,6 +188,23 @@ int hip_gemm_moe(uint32_t ggml_type, const uint8_t* d_experts, int n_sel, const 
 int hip_gemm_moe_async(uint32_t ggml_type, const uint8_t* d_experts, int n_sel, const int* expert_ids,
                        const int* tok_off, const float* d_x, float* d_y, int in_dim, int out_dim, void* stream);
 
+/* The same expert GEMMs with the token ranges on the device: for s < n_sets
+ * (1, or 2 for a gate/up pair sharing x) and e < n_exp, the gathered rows
+ * t = d_tok_off[e] .. d_tok_off[e+1]-1 of d_x (each expert's x digitised once
+ * for both sets) multiply expert e of d_experts[s] (at + e * hip_type_size(type,
+ * in_dim*out_dim)) into the same rows of d_y[s] (y += with accumulate).  With
+ * d_x_up, x is silu(d_x) * d_x_up (a down projection after SwiGLU).  max_tokens
+ * bounds any expert's token count (the launch holds ceil(max_tokens/16) token
+ * chunks per expert; the empty ones exit at once), so nothing is read back to
+ * the host and the call can be captured in a HIP graph.  Replaces the host
+ * round trip of the per-expert loop of src/cuda.rs:667-798 (the reference
+ * copies the router logits back to build it).  Matrix-core types only (Q4_K,
+ * Q5_K, Q6_K, IQ3_S, IQ2_XXS; QH_ERR_TYPE otherwise), in_dim % 256 == 0,
+ * 16-byte aligned d_x. */
+int hip_gemm_moe_dev_async(uint32_t ggml_type, int n_sets, const uint8_t* const* d_experts, float* const* d_y,
+                           int n_exp, const int* d_tok_off, int max_tokens, const float* d_x, const float* d_x_up,
+                           int in_dim, int out_dim, int accumulate, void* stream);
+
 /* Up to 4 expert GEMVs in one call.  Replaces cuda_gemv_moe4
  * (src/cuda_kernels.cu:1085-1106, Rust decl src/cuda.rs:39-45); any type. */
 int hip_gemv_moe4(uint32_t ggml_type, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,

@@ -83,6 +83,8 @@ _SIGS = {
     "hip_gemm_moe": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int]),
     "hip_gemm_moe_async": (C.c_int, [C.c_uint32, C.c_void_p, C.c_int] + [C.c_void_p] * 4 + [C.c_int, C.c_int,
                                                                                           C.c_void_p]),
+    "hip_gemm_moe_dev_async": (C.c_int, [C.c_uint32, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                         C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hip_gguf_open": (C.c_int, [C.c_char_p, C.c_void_p]),
     "hip_gguf_close": (None, [C.c_void_p]),
     "hip_gguf_version": (C.c_uint32, [C.c_void_p]),

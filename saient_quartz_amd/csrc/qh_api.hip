@@ -589,6 +589,28 @@ int hip_gemm_moe_async(uint32_t type, const uint8_t* experts, int n_sel, const i
     return QH_OK;
 }
 
+int hip_gemm_moe_dev_async(uint32_t type, int n_sets, const uint8_t* const* experts, float* const* y, int n_exp,
+                           const int* tok_off, int max_tokens, const float* x, const float* x_up, int in_dim,
+                           int out_dim, int accumulate, void* stream) {
+    if (n_sets < 1 || n_sets > 2 || n_exp < 0 || max_tokens < 0) return QH_ERR_RANGE;
+    if (n_exp == 0 || max_tokens == 0) return QH_OK;
+    if (!experts || !y || !tok_off || !x) return QH_ERR_NULL;
+    for (int s = 0; s < n_sets; s++)
+        if (!experts[s] || !y[s]) return QH_ERR_NULL;
+    if (qh_block_elems(type) == 0) return QH_ERR_TYPE;
+    int rc = qh_check_dims(type, in_dim, out_dim);
+    if (rc) return rc;
+    hipError_t e = qh_launch_mmq_moe_dev(type, n_sets, experts, y, n_exp, tok_off, max_tokens, x, x_up, in_dim,
+                                         out_dim, accumulate ? 1 : 0, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) {
+        qh_set_error("hip_gemm_moe_dev: this type or shape has no device-driven kernel (Q4_K, Q5_K, Q6_K, IQ3_S, "
+                     "IQ2_XXS with in_dim % 256 == 0 and 16-byte aligned x)");
+        return QH_ERR_TYPE;
+    }
+    if (e != hipSuccess) return qh_fail(e, "hip_gemm_moe_dev");
+    return QH_OK;
+}
+
 int hip_gemm_moe(uint32_t type, const uint8_t* experts, int n_sel, const int* expert_ids, const int* tok_off,
                  const float* x, float* y, int in_dim, int out_dim) {
     return hip_gemm_moe_async(type, experts, n_sel, expert_ids, tok_off, x, y, in_dim, out_dim, nullptr);

@@ -287,7 +287,27 @@ struct QgXs {        // the distinct token blocks of one grouped launch
     int n[QG_MAXG];  // tokens (<= 16)
     const unsigned char* img;  // their x images: slot s, group g at (s ngroups + g) XImg::BYTES
     uint32_t img_bytes;
+    // Token ranges on the device (expert layers): when tok_off is set, slot s is
+    // chunk c = s % moe_c of expert e = s / moe_c, tokens tok_off[e] + 16 c ..
+    // min(+16, tok_off[e + 1]) of the gathered x[0] (and x2[0]); n[] is unused.
+    const int* tok_off;
+    int moe_c;
 };
+// The tokens of slot s: x (and x2) of its first token, their count (<= 16)
+// and the index a of the first one in the gathered rows (0 for host slots).
+struct QgTok {
+    const float* x;
+    const float* x2;
+    int n, a;
+};
+QH_DEV QgTok qg_tokens(const QgXs& xs, int slot, int in_dim) {
+    if (!xs.tok_off) return QgTok{xs.x[slot], xs.x2[slot], xs.n[slot], 0};
+    const int e = slot / xs.moe_c, c = slot - e * xs.moe_c;
+    const int a = xs.tok_off[e] + 16 * c;
+    int n = xs.tok_off[e + 1] - a;
+    n = n < 0 ? 0 : (n > 16 ? 16 : n);
+    return QgTok{xs.x[0] + (size_t)a * (size_t)in_dim, xs.x2[0] ? xs.x2[0] + (size_t)a * (size_t)in_dim : nullptr, n, a};
+}
 struct QgGroups {    // the matrices of one grouped launch
     const uint8_t* w[QG_MAXG];
     float* y[QG_MAXG];
@@ -305,7 +325,7 @@ struct QgGroups {    // the matrices of one grouped launch
 #define QG_PART_FLOATS (16 * 1024 * 1024)
 static __device__ __align__(256) float qh_mmq_part[QG_PART_FLOATS];
 // x images of one launch's token blocks (qg_ximage)
-#define QG_IMG_BYTES (24u << 20)
+#define QG_IMG_BYTES (40u << 20)
 static __device__ __align__(256) unsigned char qh_mmq_img[QG_IMG_BYTES];
 static __device__ __align__(256) unsigned int qh_mmq_cnt[QG_PART_TILES * QG_WAVES];
 
@@ -405,18 +425,19 @@ QH_DEV void qg_chunk(const qh_u32x4* xr, const qh_u32x4* ur, bool swiglu, float*
 __global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
     const int g = blockIdx.x, slot = blockIdx.y, ngroups = in_dim >> 8;
     const int lane = threadIdx.x & 63, xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
-    const int n = xs.n[slot];
+    const QgTok tk = qg_tokens(xs, slot, in_dim);
+    const int n = tk.n;
     if (xt >= n) return;  // whole half-wavefronts: the reductions stay within live lanes
     const uint32_t off = 4u * ((uint32_t)xt * (uint32_t)in_dim + 256u * (uint32_t)g + 8u * (uint32_t)xc);
-    const QhBuf xb = qh_buf(xs.x[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+    const QhBuf xb = qh_buf(tk.x, 4u * (uint32_t)n * (uint32_t)in_dim);
     qh_u32x4 xr[2] = {qh_ld128(xb, off), qh_ld128(xb, off + 16u)}, ur[2] = {};
-    if (xs.x2[slot]) {
-        const QhBuf ub = qh_buf(xs.x2[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
+    if (tk.x2) {
+        const QhBuf ub = qh_buf(tk.x2, 4u * (uint32_t)n * (uint32_t)in_dim);
         ur[0] = qh_ld128(ub, off);
         ur[1] = qh_ld128(ub, off + 16u);
     }
     float v[8];
-    qg_chunk(xr, ur, xs.x2[slot] != nullptr, v);
+    qg_chunk(xr, ur, tk.x2 != nullptr, v);
     qg_digitise(v, true, lane, xt, xc, img + ((size_t)slot * ngroups + g) * XImg::BYTES);
 }
 
@@ -469,12 +490,22 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     int gi = 0;
 #pragma unroll
     for (int k = 1; k < QG_MAXG; k++) gi += bx >= gs.bstart[k];
-    const int out_dim = gs.rows[gi], slot = gs.slot[gi], ldy = gs.ldy[gi];
-    const int n = xs.n[slot];
-    float* __restrict__ y = gs.y[gi];
-    const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
+    const int out_dim = gs.rows[gi], ldy = gs.ldy[gi];
     const int ngroups = in_dim >> 8;
-    const int lb = bx - gs.bstart[gi];
+    int lb = bx - gs.bstart[gi], slot = gs.slot[gi];
+    if (xs.tok_off) {
+        // expert layers: entry gi is expert gs.slot[gi]; its workgroups cover
+        // moe_c token chunks, each over all row blocks and splits
+        const int per = (out_dim + 32 * W - 1) / (32 * W) * splits;
+        const int c = lb / per;
+        lb -= c * per;
+        slot = slot * xs.moe_c + c;
+    }
+    const QgTok tk = qg_tokens(xs, slot, in_dim);
+    const int n = tk.n;
+    if (n <= 0) return;  // an empty token chunk (uniform over the workgroup, before any barrier)
+    float* __restrict__ y = gs.y[gi] + (size_t)tk.a * (size_t)ldy;
+    const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
     const int blk = lb / splits, sp = lb - blk * splits, gblk = bx / splits;
     const int tile0 = blk * W + w;  // this wavefront's tile
     const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
@@ -546,9 +577,9 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
         static_assert(32 * NT <= 64 * W, "one chunk per thread");
         const int xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
         const bool xon = (int)threadIdx.x < 32 * NT && xt < n;
-        const QhBuf fb = qh_buf(xs.x[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
-        const QhBuf ub = qh_buf(xs.x2[slot], 4u * (uint32_t)n * (uint32_t)in_dim);
-        const bool swiglu = xs.x2[slot] != nullptr;
+        const QhBuf fb = qh_buf(tk.x, 4u * (uint32_t)n * (uint32_t)in_dim);
+        const QhBuf ub = qh_buf(tk.x2, 4u * (uint32_t)n * (uint32_t)in_dim);
+        const bool swiglu = tk.x2 != nullptr;
         const uint32_t xo = 4u * ((uint32_t)xt * (uint32_t)in_dim + 8u * (uint32_t)xc);
         qh_u32x4 xd[QG_GMAX][2], ud[QG_GMAX][2];
 #pragma unroll
@@ -1129,4 +1160,85 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
     else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
     return hipGetLastError();
+}
+
+// Expert layers with token ranges on the device: for s < sets and e < n_exp,
+// Y[s][t] = E[s][e] X[t] for the gathered rows t = tok_off[e] .. tok_off[e + 1]
+// - 1 (X[t] = silu(X[t]) * X2[t] with X2), expert e's weights at E[s] + e *
+// slice.  Every expert gets max_tokens / 16 (rounded up) token chunks of
+// workgroups; chunks past an expert's tokens exit at once, so nothing is read
+// back to the host (the launch can sit in a captured graph).  Experts go in
+// batches of up to QG_MAXG / sets.
+hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* E, float* const* Y, int n_exp,
+                                 const int* tok_off, int max_tokens, const float* X, const float* X2, int in_dim,
+                                 int out_dim, int accum, hipStream_t st) {
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
+        return hipErrorNotSupported;
+    if (sets < 1 || sets > 2 || n_exp < 1 || max_tokens < 1 || in_dim % 256 || in_dim / 256 > QG_MAX_GROUPS ||
+        out_dim < 1 || ((uintptr_t)X & 15u) || ((uintptr_t)X2 & 15u))
+        return hipErrorNotSupported;
+    const QgScratch* sc = qh_mmq_scratch_ptrs();
+    if (!sc) return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    if ((int64_t)out_dim * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+    const size_t slice = (size_t)row_bytes * (size_t)out_dim;
+    const int ngroups = in_dim / 256, brows = 32 * QG_WAVES, blocks = (out_dim + brows - 1) / brows;
+    const int C = (max_tokens + 15) / 16;
+    const int pw = QG_WAVES * 16 * 32;  // floats of one workgroup's partials (16-token bound)
+    for (int e0 = 0; e0 < n_exp;) {
+        // experts of this launch: bounded by the entries, the partials and the images
+        int ne = n_exp - e0 < QG_MAXG / sets ? n_exp - e0 : QG_MAXG / sets;
+        int splits = 1, mode = 0;
+        for (;; ne--) {
+            if (ne < 1) return hipErrorNotSupported;
+            const int bl = sets * ne * blocks;  // row blocks with one chunk per expert
+            splits = qh_mmq_splits_env();
+            if (splits <= 0) splits = qg_pick_splits(bl, ngroups, ngroups, QG_TARGET_WGS);
+            splits = splits < ngroups ? splits : ngroups;
+            const bool res = (ngroups + splits - 1) / splits <= QG_GMAX;
+            mode = res ? (bl <= QG_DIG_BLOCKS * ne ? 2 : 1) : 0;
+            const int64_t wgs = (int64_t)sets * ne * C * blocks * splits;
+            const bool fits = wgs * pw <= QG_PART_FLOATS && (int64_t)sets * ne * C * blocks <= QG_PART_TILES &&
+                              (mode == 2 || (int64_t)ne * C * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES);
+            if (fits) break;
+        }
+        QgXs xs = {};
+        xs.x[0] = X;
+        xs.x2[0] = X2;
+        xs.tok_off = tok_off + e0;
+        xs.moe_c = C;
+        xs.img = sc->img;
+        xs.img_bytes = (uint32_t)((int64_t)ne * C * ngroups * XImg::BYTES);
+        QgGroups gs = {};
+        int wgs = 0;
+        for (int i = 0; i < QG_MAXG; i++) {
+            gs.bstart[i] = i < sets * ne ? wgs : INT_MAX;
+            if (i < sets * ne) {
+                const int s = i / ne, e = i - s * ne;
+                gs.w[i] = E[s] + (size_t)(e0 + e) * slice;
+                gs.y[i] = Y[s];
+                gs.wbytes[i] = (uint32_t)((slice + 3) & ~(size_t)3);
+                gs.rows[i] = out_dim;
+                gs.ldy[i] = out_dim;
+                gs.slot[i] = e;
+                wgs += C * blocks * splits;
+            }
+        }
+        gs.bstart[QG_MAXG] = INT_MAX;
+        gs.accum = accum;
+        if (mode != 2)
+            hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)(ne * C)), dim3(512), 0, st, xs, sc->img,
+                               in_dim);
+        switch (type) {
+            case QT_Q4_K: launch_mmq_nt<GQ4K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_Q5_K: launch_mmq_nt<GQ5K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ3_S: launch_mmq_nt<GIQ3S>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+            default: launch_mmq_nt<GQ6K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        e0 += ne;
+    }
+    return hipSuccess;
 }

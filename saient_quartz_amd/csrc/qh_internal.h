@@ -49,6 +49,9 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
                                uint32_t t2, int c2, const uint8_t* const* W2, float* const* Y2, const int* o2,
                                const float* x, int n, int in_dim, hipStream_t st);
+hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* E, float* const* Y, int n_exp,
+                                 const int* tok_off, int max_tokens, const float* X, const float* X2, int in_dim,
+                                 int out_dim, int accum, hipStream_t st);
 hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const* W, const float* const* X,
                                  float* const* Y, const int* n, const int* out_dims, int in_dim, hipStream_t st,
                                  const float* const* X2 = nullptr, int accum = 0, const float* nw = nullptr);

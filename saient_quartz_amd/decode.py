@@ -23,10 +23,10 @@ import torch
 
 from . import synth_device
 from .api import check, lib
-from .host import (gemm_group_norm_async, gemm_grouped_async, gemm_grouped_ex_async, gemm_moe_async,
+from .host import (gemm_group_norm_async, gemm_grouped_async, gemm_grouped_ex_async, gemm_moe_async, gemm_moe_dev_async,
                    gemv_group_async, gemv_multi_async)
 
-Q4_K, Q6_K = 12, 14
+Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_S = 12, 13, 14, 16, 21
 
 
 @dataclass(frozen=True)
@@ -174,17 +174,23 @@ class MoeStep:
 
       logits = router_w x (+ router_b)       hip_gemm (F32)
       ids, w = top-k + softmax               hip_moe_route (renorm or OLMoE form)
-      slots  = expert-ordered (token, j)     hip_moe_plan; tok_off copied back
+      slots  = expert-ordered (token, j)     hip_moe_plan
       xg     = x[slot_tok]                   hip_moe_gather
-      g, u   = gate/up of each slot's expert hip_gemm_grouped / hip_gemm_moe
-      act    = swiglu(g + bg, u + bu)        hip_moe_swiglu (plain or OAI clamp)
-      yg     = down act                      hip_gemm_moe
+      g, u   = gate/up of each slot's expert hip_gemm_moe_dev (token ranges read on
+                                             the device; other types: tok_off copied
+                                             back, hip_gemm_grouped / hip_gemm_moe)
+      act    = swiglu(g + bg, u + bu)        hip_moe_swiglu (plain or OAI clamp; the plain
+                                             form without biases is folded into the
+                                             device-driven down GEMM)
+      yg     = down act                      hip_gemm_moe_dev / hip_gemm_moe
       out    = (out +) sum_j w * (yg + bd)   hip_moe_combine
 
     Weights: wg, wu [E][f][d] and wd [E][d][f] stacked GGUF bytes (expert e at
     e * slice, src/cuda.rs:250-258); router_w [E][d] f32; biases optional
-    [E][f] / [E][d] / [E].  The one host round trip is tok_off (E + 1 ints), at
-    the point where the reference copies the router logits back."""
+    [E][f] / [E][d] / [E].  For the matrix-core types there is no host round
+    trip (the step can be captured in a HIP graph); for the others tok_off (E + 1
+    ints) comes back at the point where the reference copies the router logits
+    back."""
 
     def __init__(self, types, wg, wu, wd, router_w, E, k, d, f, n_max, renorm=True, oai=False, router_b=None,
                  gate_b=None, up_b=None, down_b=None):
@@ -210,6 +216,10 @@ class MoeStep:
         self.act = torch.empty(S, f, device=dev)
         self.yg = torch.empty(S, d, device=dev)
         self.tok_off_host = torch.empty(E + 1, dtype=torch.int32, pin_memory=True)
+        # the expert GEMMs read the token ranges on the device (matrix-core types);
+        # otherwise tok_off comes back to the host to build them
+        mc = (Q4_K, Q5_K, Q6_K, IQ3_S, IQ2_XXS)
+        self.device_driven = (all(t in mc for t in types) and d % 256 == 0 and f % 256 == 0)
 
     @staticmethod
     def _p(t):
@@ -229,14 +239,40 @@ class MoeStep:
         check("hip_moe_plan_async",
               L.hip_moe_plan_async(self.ids.data_ptr(), n, k, E, self.tok_off.data_ptr(), self.slot_of.data_ptr(),
                                    self.slot_tok.data_ptr(), self.slot_exp.data_ptr(), sp))
+        S = n * k  # every token takes k slots
+        check("hip_moe_gather_async", L.hip_moe_gather_async(self.xg.data_ptr(), xp, self.slot_tok.data_ptr(), S, d,
+                                                             sp))
+        if self.device_driven:
+            # token ranges read on the device: no host round trip (graph-capturable)
+            if self.tg == self.tu:
+                gemm_moe_dev_async(L, self.tg, [self.wg.data_ptr(), self.wu.data_ptr()],
+                                   [self.g.data_ptr(), self.u.data_ptr()], E, self.tok_off.data_ptr(), n,
+                                   self.xg.data_ptr(), d, f, sp)
+            else:
+                for t, w_, y_ in ((self.tg, self.wg, self.g), (self.tu, self.wu, self.u)):
+                    gemm_moe_dev_async(L, t, [w_.data_ptr()], [y_.data_ptr()], E, self.tok_off.data_ptr(), n,
+                                       self.xg.data_ptr(), d, f, sp)
+            if self.gb is None and self.ub is None and not self.oai:
+                # plain SwiGLU folded into the down GEMM's x digitisation
+                gemm_moe_dev_async(L, self.td, [self.wd.data_ptr()], [self.yg.data_ptr()], E, self.tok_off.data_ptr(),
+                                   n, self.g.data_ptr(), f, d, sp, x_up_ptr=self.u.data_ptr())
+            else:
+                check("hip_moe_swiglu_async",
+                      L.hip_moe_swiglu_async(self.act.data_ptr(), self.g.data_ptr(), self.u.data_ptr(),
+                                             self._p(self.gb), self._p(self.ub), self.slot_exp.data_ptr(), S, f,
+                                             self.oai, sp))
+                gemm_moe_dev_async(L, self.td, [self.wd.data_ptr()], [self.yg.data_ptr()], E, self.tok_off.data_ptr(),
+                                   n, self.act.data_ptr(), f, d, sp)
+            check("hip_moe_combine_async",
+                  L.hip_moe_combine_async(out.data_ptr(), self.yg.data_ptr(), self.slot_of.data_ptr(),
+                                          self.wts.data_ptr(), self.ids.data_ptr(), self._p(self.db), n, k, d,
+                                          int(accumulate), sp))
+            return
         self.tok_off_host.copy_(self.tok_off, non_blocking=True)
         st.synchronize()
         off = self.tok_off_host.tolist()
         sel = [e for e in range(E) if off[e + 1] > off[e]]
         s_off = [off[e] for e in sel] + [off[E]]
-        S = off[E]
-        check("hip_moe_gather_async", L.hip_moe_gather_async(self.xg.data_ptr(), xp, self.slot_tok.data_ptr(), S, d,
-                                                             sp))
         if self.tg == self.tu and 2 * len(sel) <= 16:
             # gate and up of every selected expert in one grouped launch (x digitised once per expert)
             xs = [self.xg.data_ptr() + 4 * d * off[e] for e in sel]

@@ -194,3 +194,16 @@ def gemm_moe_async(L, ggml_type, experts_ptr, expert_ids, tok_off, x_ptr, y_ptr,
     check("hip_gemm_moe_async",
           L.hip_gemm_moe_async(ggml_type, experts_ptr, k, (C.c_int * k)(*expert_ids), (C.c_int * (k + 1))(*tok_off),
                                x_ptr, y_ptr, in_dim, out_dim, stream_ptr))
+
+
+def gemm_moe_dev_async(L, ggml_type, experts_ptrs, y_ptrs, n_exp, tok_off_ptr, max_tokens, x_ptr, in_dim, out_dim,
+                       stream_ptr, x_up_ptr=None, accumulate=False):
+    """hip_gemm_moe_dev_async: token ranges read on the device from tok_off_ptr
+    (n_exp + 1 ints); experts_ptrs / y_ptrs: one or two weight sets sharing x."""
+    import ctypes as C
+    k = len(experts_ptrs)
+    assert len(y_ptrs) == k
+    check("hip_gemm_moe_dev_async",
+          L.hip_gemm_moe_dev_async(ggml_type, k, (C.c_void_p * k)(*experts_ptrs), (C.c_void_p * k)(*y_ptrs), n_exp,
+                                   tok_off_ptr, max_tokens, x_ptr, x_up_ptr, in_dim, out_dim, int(accumulate),
+                                   stream_ptr))

@@ -198,7 +198,8 @@ def moe_case(oracle, types, E, d, f, seed):
     ((16, 16, 16), 8, 4, 7, True, True),
     ((13, 14, 12), 4, 3, 5, True, True),
 ])
-def test_moe_step_vs_oracle(qh, oracle, types, E, k, n, renorm, extras):
+@pytest.mark.parametrize("driven", [True, False], ids=["device_ranges", "host_ranges"])
+def test_moe_step_vs_oracle(qh, oracle, types, E, k, n, renorm, extras, driven):
     d, f = 512, 768
     host, deq, rw = moe_case(oracle, types, E, d, f, seed=E + k + n)
     rng = np.random.default_rng(n)
@@ -214,6 +215,8 @@ def test_moe_step_vs_oracle(qh, oracle, types, E, k, n, renorm, extras):
     T = lambda a: dev(a) if a is not None else None  # noqa: E731
     step = MoeStep(types, dev(host["g"]), dev(host["u"]), dev(host["d"]), dev(rw), E, k, d, f, n_max=64,
                    renorm=renorm, oai=extras, router_b=T(rb), gate_b=T(gb), up_b=T(ub), down_b=T(db))
+    assert step.device_driven
+    step.device_driven = driven  # the host round-trip form stays for the other types
     X = dev(x)
     out = torch.full((n, d), np.nan, device="cuda")
     step.issue(X, out, n)
@@ -230,3 +233,58 @@ def test_moe_step_vs_oracle(qh, oracle, types, E, k, n, renorm, extras):
         ref = g.moe_ffn(x[t], ri, rwt, deq["g"], deq["u"], deq["d"], gb, ub, db, oai=extras)
         err = np.linalg.norm(got[t] - ref) / np.linalg.norm(ref)
         assert err < 1e-3, (t, err)
+
+
+@pytest.mark.parametrize("t", [12, 13, 14, 21, 16])
+@pytest.mark.parametrize("sets, swiglu, acc", [(1, False, False), (2, False, True), (1, True, False)])
+def test_gemm_moe_dev_vs_oracle(qh, oracle, t, sets, swiglu, acc):
+    """Device-held token ranges: empty experts, one token, and more than 16 tokens
+    (several 16-token chunks of one expert) against the oracle per expert."""
+    from saient_quartz_amd import type_size
+    from saient_quartz_amd.host import gemm_moe_dev_async
+    E, in_dim, out_dim = 6, 512, 320
+    counts = [0, 1, 37, 0, 16, 5]
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    S = int(off[-1])
+    rng = np.random.default_rng(t + 10 * sets)
+    blobs = [[synth.weights(t, out_dim, in_dim, seed=7 * t + 31 * s + e) for e in range(E)] for s in range(sets)]
+    W = [dev(np.concatenate(b)) for b in blobs]
+    xg = synth.activations(S, in_dim, seed=t + 5)
+    xu = synth.activations(S, in_dim, seed=t + 6) if swiglu else None
+    base = rng.standard_normal((S, out_dim)).astype(np.float32)
+    Y = [dev(base) if acc else torch.full((S, out_dim), np.nan, device="cuda") for _ in range(sets)]
+    X, XU = dev(xg), (dev(xu) if swiglu else None)
+    sl = type_size(t, in_dim * out_dim)
+    assert sl == len(blobs[0][0])
+    gemm_moe_dev_async(qh, t, [w.data_ptr() for w in W], [y.data_ptr() for y in Y], E, dev(off).data_ptr(),
+                       max(counts), X.data_ptr(), in_dim, out_dim, torch.cuda.current_stream().cuda_stream,
+                       x_up_ptr=XU.data_ptr() if swiglu else None, accumulate=acc)
+    torch.cuda.synchronize()
+    xin = xg.astype(np.float64)
+    if swiglu:
+        xin = xin / (1.0 + np.exp(-xin)) * xu.astype(np.float64)
+    xin = xin.astype(np.float32)
+    for s in range(sets):
+        got = Y[s].cpu().numpy()
+        for e in range(E):
+            a, b = int(off[e]), int(off[e + 1])
+            if a == b:
+                continue
+            ref = oracle.gemm(t, xin[a:b], blobs[s][e], in_dim, out_dim, b - a)
+            if acc:
+                ref = ref + base[a:b]
+            for r in range(b - a):
+                err = np.linalg.norm(got[a + r] - ref[r]) / np.linalg.norm(ref[r])
+                assert err < 1e-3, (s, e, r, err)
+
+
+def test_gemm_moe_dev_rejects_other_types(qh):
+    from saient_quartz_amd.api import QuartzHipError as QuartzError
+    from saient_quartz_amd.host import gemm_moe_dev_async
+    off = dev(np.array([0, 1], np.int32))
+    x = torch.zeros(1, 256, device="cuda")
+    y = torch.zeros(1, 32, device="cuda")
+    w = torch.zeros(32 * 34 * 8, dtype=torch.uint8, device="cuda")
+    with pytest.raises(QuartzError):
+        gemm_moe_dev_async(qh, 8, [w.data_ptr()], [y.data_ptr()], 1, off.data_ptr(), 1, x.data_ptr(), 256, 32,
+                           torch.cuda.current_stream().cuda_stream)
