@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     # MFMA results in ordinary VGPRs: the GEMV kernels consume every result
     # immediately, so accumulation registers only add copies.
     "-mllvm", "--amdgpu-mfma-vgpr-form",
+    # Leading scalar kernel arguments preloaded into SGPRs at wavefront start
+    # (gfx950): a kernel's first loads need no round trip to argument memory.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

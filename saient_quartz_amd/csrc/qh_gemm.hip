@@ -47,7 +47,9 @@ typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 #define QG_TARGET_WGS 256   // workgroups a launch aims for (one per CU)
 #define QG_PART_TILES 8192  // row blocks with split-K counters (one per wavefront)
 #define QG_NBUF 2           // items of weights in flight per wavefront (register sets)
+#ifndef QG_GMAX
 #define QG_GMAX 5           // groups per K split (their x images stay in LDS)
+#endif
 #define QG_DIG_BLOCKS 128   // row blocks per token block up to which a launch digitises x in the kernel
 #define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
 
@@ -300,11 +302,22 @@ struct QgTok {
     const float* x2;
     int n, a;
 };
+// A workgroup-uniform value held in scalar registers (the compiler cannot
+// prove uniformity through a dynamically indexed argument array or a loaded
+// offset, and would wrap every buffer load built on it in a waterfall loop).
+template <class T>
+QH_DEV T* qg_uni(T* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (T*)(((uint64_t)hi << 32) | lo);
+}
+QH_DEV int qg_uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 QH_DEV QgTok qg_tokens(const QgXs& xs, int slot, int in_dim) {
-    if (!xs.tok_off) return QgTok{xs.x[slot], xs.x2[slot], xs.n[slot], 0};
+    if (!xs.tok_off) return QgTok{qg_uni(xs.x[slot]), qg_uni(xs.x2[slot]), qg_uni(xs.n[slot]), 0};
     const int e = slot / xs.moe_c, c = slot - e * xs.moe_c;
-    const int a = xs.tok_off[e] + 16 * c;
-    int n = xs.tok_off[e + 1] - a;
+    const int a = qg_uni(xs.tok_off[e]) + 16 * c;
+    int n = qg_uni(xs.tok_off[e + 1]) - a;
     n = n < 0 ? 0 : (n > 16 ? 16 : n);
     return QgTok{xs.x[0] + (size_t)a * (size_t)in_dim, xs.x2[0] ? xs.x2[0] + (size_t)a * (size_t)in_dim : nullptr, n, a};
 }
@@ -526,11 +539,14 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
         goff[h] = (uint32_t)(tile0 * 32 + r) * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         soff[h] = q < 32 * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(32 * RS);
     }
+    // Past the split (i >= nk) the offsets get bit 31 (out of the buffer's
+    // range: no traffic, zeros) by arithmetic, not a branch: a branch here
+    // leaves the compiler's load counting at the joins conservative, and its
+    // waits for one register set then also wait for the other set's loads.
     auto load_w = [&](int i, qh_u32x4* wo) {  // item i: group grp(i)
-        const uint32_t go = (uint32_t)F::BYTES * (uint32_t)grp(i);
+        const uint32_t go = (uint32_t)F::BYTES * (uint32_t)grp(i) | ((uint32_t)(nk - 1 - i) & 0x80000000u);
 #pragma unroll
-        for (int h = 0; h < NH; h++)
-            wo[h] = qh_ld128(wb, (i < nk && ((okb >> h) & 1u)) ? goff[h] + go : 0x80000000u);
+        for (int h = 0; h < NH; h++) wo[h] = qh_ld128(wb, ((okb >> h) & 1u) ? goff[h] + go : 0x80000000u);
     };
     auto stage_w = [&](const qh_u32x4* wr) {
 #pragma unroll
@@ -690,22 +706,31 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     // iteration ago (every wavefront finished reading that slot before the
     // last barrier) and group i + 2's image loads go out before the weights
     // (a wait for them then leaves the weight loads in flight).
-    for (int i0 = 0; i0 < nk; i0 += QG_NBUF) {
-#pragma unroll
-        for (int b = 0; b < QG_NBUF; b++) {
-            const int i = i0 + b;
-            if (i < nk) {
-                stage_w(wr[b]);
-                if constexpr (!RES) {
-                    if (i + 1 < nk) store_x(lds + ((i + 1) & 1) * IMB, xq);
-                    load_x(i + 2, xq);
-                }
-                load_w(i + QG_NBUF, wr[b]);
-                compute(lds + (RES ? i : (i & 1)) * IMB, tot[0]);
-                if constexpr (!RES) __syncthreads();
-            }
+    // The pair loop's body is straight-line and an odd last item runs after
+    // it: with a conditional second item the compiler's load counting at the
+    // loop header assumes the shorter path, and the first set's wait would
+    // also wait for the second set's loads (memory and compute serialised).
+    static_assert(QG_NBUF == 2, "item pairs");
+    auto item = [&](int b, int i) {
+        // keep each item's stage (and its load wait) after the previous item's
+        // compute: hoisted, it would wait for the newest loads too
+        __builtin_amdgcn_sched_barrier(0);
+        stage_w(wr[b]);
+        if constexpr (!RES) {
+            if (i + 1 < nk) store_x(lds + ((i + 1) & 1) * IMB, xq);
+            load_x(i + 2, xq);
         }
+        load_w(i + QG_NBUF, wr[b]);
+        __builtin_amdgcn_sched_barrier(0);  // the refill goes out before the compute
+        compute(lds + (RES ? i : (i & 1)) * IMB, tot[0]);
+        if constexpr (!RES) __syncthreads();
+    };
+    int i0 = 0;
+    for (; i0 + 1 < nk; i0 += 2) {
+        item(0, i0);
+        item(1, i0 + 1);
     }
+    if (i0 < nk) item(0, i0);
     // Results: this wavefront's 32 rows x NT tokens.
     auto put = [&](int t, int row, float a) {
         if (t < n && row < out_dim) {

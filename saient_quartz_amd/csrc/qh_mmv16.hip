@@ -385,6 +385,20 @@ struct QhMats {
     int ldy[QH_MULTI];
 };
 
+// The one-matrix launch's arguments as leading scalars: the hardware preloads
+// them into SGPRs when a wavefront starts (built with
+// -amdgpu-kernarg-preload-count=16), so the first weight loads go out without
+// a round trip to the kernel-argument memory (a cold miss of about 1 us; an
+// aggregate argument is always read from memory).  Multi-matrix launches read
+// QhMats.
+struct QhOne {
+    const uint8_t* w;
+    float* y;
+    const float* nw;
+    uint32_t wbytes;
+    int rows, ntiles, accum;
+};
+
 // Tokens per launch (NT) share every weight load and B operand; the x digit
 // planes, the ring of wavefront partials and the finished rows grow with NT, so
 // NT > 1 keeps a shorter ring and fewer tiles per workgroup to fit 160 KB of LDS.
@@ -404,8 +418,9 @@ constexpr int qh_mmv16_lds() {
 // The kernel body for workgroup `bid` of `nblk` working on mm's tiles (a
 // launch may run two bodies of different formats side by side, see qh_mmv16_mix).
 template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR, int NT = 1>
-__device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __restrict__ x, uint32_t row_bytes,
-                                              int ngroups, unsigned char* lds, const int bid, const int nblk) {
+__device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one, const float* __restrict__ x,
+                                              uint32_t row_bytes, int ngroups, unsigned char* lds, const int bid,
+                                              const int nblk) {
     static_assert(!PAIR || NT == 1, "SwiGLU pairs run one token");
     constexpr int RING = qh_ring<NT>();
     constexpr int ROWS = F::ROWS, CH = F::CH;
@@ -425,7 +440,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     float* res = red + 2 * RING * W * 16 * NT;  // finished rows of this workgroup's tiles
     float* sqw = res + qh_maxt<NT>() * 16 * NT;  // per-wavefront sums of x^2 (fused RMS norm)
     unsigned char* gridl = reinterpret_cast<unsigned char*>(sqw + W * NT);  // IQ codebook (GRID formats)
-    const int ntiles = mm.tstart[QH_MULTI];
+    const int ntiles = MULTI ? mm.tstart[QH_MULTI] : one.ntiles;
+    const float* const nwp = MULTI ? mm.nw : one.nw;
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
         int m = 0;
@@ -446,7 +462,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         if constexpr (PAIR) return 2 * (bid + (k >> 1) * nblk) + (k & 1);
         return bid + k * nblk;
     };
-    const QhBuf wb0 = qh_buf(mm.w[0], mm.wbytes[0]);  // the one-matrix case, hoisted
+    const QhBuf wb0 = qh_buf(one.w, one.wbytes);  // the one-matrix case
     const int nch = (ngroups + W * GPW - 1) / (W * GPW);
 
     // Slices of this lane in a tile: row rr[h], byte offset goff[h] from the
@@ -481,7 +497,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
         const int g0 = ch * (W * GPW) + w * GPW;
         const int m = mat_of(tile);
         const QhBuf wb = MULTI ? qh_buf(mm.w[m], mm.wbytes[m]) : wb0;
-        const int out_dim = mm.rows[m];
+        const int out_dim = MULTI ? mm.rows[m] : one.rows;
         if (MULTI) tile = local_tile(tile, m);
         const uint32_t base = (uint32_t)(tile * ROWS) * row_bytes;
 #pragma unroll
@@ -513,8 +529,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     // becomes x * nw.  The row scale rsqrt(mean + eps) is applied at the end.
     auto load_nw = [&](qh_u32x4* nv) {
         if constexpr (X1) {
-            if (mm.nw) {
-                const QhBuf nb = qh_buf(mm.nw, 4u * 256u * (uint32_t)ngroups);
+            if (nwp) {
+                const QhBuf nb = qh_buf(nwp, 4u * 256u * (uint32_t)ngroups);
 #pragma unroll
                 for (int t = 0; t < GPW; t++) nv[t] = qh_ld128(nb, 1024u * (uint32_t)(w * GPW + t) + 16u * lane);
             }
@@ -522,7 +538,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     };
     auto norm_x = [&](float4* xo, const qh_u32x4* nv) {
         if constexpr (X1) {
-            if (mm.nw) {
+            if (nwp) {
 #pragma unroll
                 for (int k = 0; k < NT; k++) {
                     float sq = 0.f;
@@ -546,7 +562,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     // Row scale of the fused RMS norm (1 without it); valid after a barrier.
     auto norm_scale = [&](int k) -> float {
         if constexpr (X1) {
-            if (mm.nw) {
+            if (nwp) {
                 float t = 0.f;
 #pragma unroll
                 for (int i = 0; i < W; i++) t += sqw[k * W + i];
@@ -672,9 +688,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
     auto put = [&](int d, int c, float r, int k) {  // y of row c of this workgroup's tile d, token k
         const int tile = wg_tile(d), m = mat_of(tile);
         const int row = local_tile(tile, m) * ROWS + c;
-        if (c < ROWS && row < mm.rows[m] && k < ntok) {
-            float* yp = mm.y[m] + (NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row;
-            *yp = mm.accum ? *yp + r : r;
+        if (c < ROWS && row < (MULTI ? mm.rows[m] : one.rows) && k < ntok) {
+            float* yp = (MULTI ? mm.y[m] : one.y) + (NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row;
+            *yp = (MULTI ? mm.accum : one.accum) ? *yp + r : r;
         }
     };
     // Sum the wavefront partials of tiles d0 .. d0+cnt-1 (one set of the ring)
@@ -802,12 +818,18 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const float* __r
 }
 
 template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false, int NT = 1>
-__global__ __launch_bounds__(64 * W) void qh_mmv16(const QhMats mm, const float* __restrict__ x, uint32_t row_bytes,
-                                                   int ngroups) {
+__global__ __launch_bounds__(64 * W) void qh_mmv16(const float* __restrict__ x, const uint8_t* w0, float* y0,
+                                                   const float* nw0, uint32_t wbytes0, int rows0, int ntiles0,
+                                                   int accum0, uint32_t row_bytes, int ngroups, const QhMats mm) {
     static_assert(qh_mmv16_lds<F, W, GPW, NT>() <= 163840, "LDS");
+    static_assert(MULTI || NT == 1, "one-matrix launches run one token");
     __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW, NT>()];
-    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, x, row_bytes, ngroups, lds, (int)blockIdx.x, (int)gridDim.x);
+    const QhOne one = {w0, y0, nw0, wbytes0, rows0, ntiles0, accum0};
+    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, one, x, row_bytes, ngroups, lds, (int)blockIdx.x,
+                                                  (int)gridDim.x);
 }
+// The leading scalar arguments of a qh_mmv16 launch (matrix 0 of mm).
+#define QH_ONE_ARGS(mm, x) (x), (mm).w[0], (mm).y[0], (mm).nw, (mm).wbytes[0], (mm).rows[0], (mm).tstart[QH_MULTI], (mm).accum
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
 // workgroups below g1 run F1's body on mm1's matrices, the others F2's on mm2's.
@@ -817,9 +839,9 @@ __global__ __launch_bounds__(64 * W) void qh_mmv16_mix(const QhMats mm1, const Q
     constexpr int L1 = qh_mmv16_lds<F1, W, GPW, NT>(), L2 = qh_mmv16_lds<F2, W, GPW, NT>();
     __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
     if ((int)blockIdx.x < g1)
-        qh_mmv16_body<F1, W, GPW, X1, true, false, NT>(mm1, x, rb1, ngroups, lds, (int)blockIdx.x, g1);
+        qh_mmv16_body<F1, W, GPW, X1, true, false, NT>(mm1, QhOne{}, x, rb1, ngroups, lds, (int)blockIdx.x, g1);
     else
-        qh_mmv16_body<F2, W, GPW, X1, true, false, NT>(mm2, x, rb2, ngroups, lds, (int)blockIdx.x - g1,
+        qh_mmv16_body<F2, W, GPW, X1, true, false, NT>(mm2, QhOne{}, x, rb2, ngroups, lds, (int)blockIdx.x - g1,
                                                        (int)gridDim.x - g1);
 }
 
@@ -844,7 +866,7 @@ static hipError_t launch_mmv16_grid(const QhMats& mm, int nm, const float* x, in
         int grid = pairs < resident ? pairs : resident;
         if ((pairs + grid - 1) / grid > QH_MAXT / 2) grid = (pairs + QH_MAXT / 2 - 1) / (QH_MAXT / 2);
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, true>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           mm, x, row_bytes, in_dim / 256);
+                           QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
         return hipGetLastError();
     }
     // One workgroup per tile up to what the device holds at once (tiles go
@@ -854,10 +876,10 @@ static hipError_t launch_mmv16_grid(const QhMats& mm, int nm, const float* x, in
     if ((tiles + grid - 1) / grid > QH_MAXT) grid = (tiles + QH_MAXT - 1) / QH_MAXT;
     if (nm > 1)
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, false>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           mm, x, row_bytes, in_dim / 256);
+                           QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
     else
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, false, false>), dim3((unsigned)grid), dim3(64 * W), 0,
-                           st, mm, x, row_bytes, in_dim / 256);
+                           st, QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
     return hipGetLastError();
 }
 
@@ -1076,8 +1098,8 @@ static hipError_t launch_mmv16_tok(const QhMats& mm, const float* x, int in_dim,
     const int tiles = mm.tstart[QH_MULTI];
     int grid = tiles < resident ? tiles : resident;
     if ((tiles + grid - 1) / grid > qh_maxt<NT>()) grid = (tiles + qh_maxt<NT>() - 1) / qh_maxt<NT>();
-    hipLaunchKernelGGL((qh_mmv16<F, W, 1, X1, true, false, NT>), dim3((unsigned)grid), dim3(64 * W), 0, st, mm, x,
-                       row_bytes, in_dim / 256);
+    hipLaunchKernelGGL((qh_mmv16<F, W, 1, X1, true, false, NT>), dim3((unsigned)grid), dim3(64 * W), 0, st,
+                       QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
     return hipGetLastError();
 }
 
