@@ -328,9 +328,21 @@ struct QgGroups {    // the matrices of one grouped launch
     int rows[QG_MAXG];
     int ldy[QG_MAXG];          // y token stride
     int slot[QG_MAXG];         // x block (QgXs entry)
-    int bstart[QG_MAXG + 1];   // first workgroup of each matrix; entries past the count are INT_MAX
+    int bstart[QG_MAXG + 1];   // first workgroup of each matrix (launch-wide); entries from the count on
+                               // hold the total
+    // each matrix's tokens (what QgXs holds per slot), so a workgroup reads
+    // them in the same round of argument loads as its matrix
+    const float* x[QG_MAXG];
+    const float* x2[QG_MAXG];
+    int n[QG_MAXG];
     int accum;                 // y += result (the residual add) instead of y = result
 };
+// The tokens of matrix gi's token block `slot` (host blocks: the matrix's own
+// fields; device ranges: slot = expert chunk, as qg_tokens).
+QH_DEV QgTok qg_tokens(const QgGroups& gs, int gi, const QgXs& xs, int slot, int in_dim) {
+    if (!xs.tok_off) return QgTok{qg_uni(gs.x[gi]), qg_uni(gs.x2[gi]), qg_uni(gs.n[gi]), 0};
+    return qg_tokens(xs, slot, in_dim);
+}
 // Split-K partials (per (row block, split): W wavefronts x TPW tiles x 16 tokens
 // x 32 rows)
 // and per-(block, wavefront) arrival counters; every counter is back at zero
@@ -474,12 +486,15 @@ constexpr int qh_mmq_lds() {
     return (MODE != 0 ? QG_GMAX : 2) * XImg::BYTES + W * (32 * F::RS + 16) + (F::GRID ? IQT_BYTES : 0);
 }
 
-// The kernel body for launch-local workgroup bx (a launch may run two formats'
+// The kernel body for workgroup lb of matrix gi (a launch may run two formats'
 // bodies side by side, see qh_mmq_mix); lds holds qh_mmq_lds<...>() bytes.
+// Launches are two-dimensional (blockIdx.y = matrix, blockIdx.x = its
+// workgroup), so every per-matrix argument is read in the first round of
+// argument loads; workgroups past a matrix's count exit at once.
 template <class F, int NT, int W, int MODE>
 __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, uint32_t row_bytes, int in_dim,
                                             int splits, float* __restrict__ part, unsigned int* __restrict__ cnt,
-                                            unsigned char* lds, const int bx) {
+                                            unsigned char* lds, const int gi, int lb) {
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte weight loads per lane per group
     constexpr int TILE = 32 * RS + 16;
@@ -497,15 +512,15 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     unsigned char* wl = lds + NSLOT * IMB + w * TILE;
     unsigned char* gridl = lds + NSLOT * IMB + W * TILE;
     if constexpr (F::GRID != 0) qg_iq_tables<F::GRID>(gridl, threadIdx.x, 64 * W);
-    // This workgroup's matrix (uniform), row block and K split.  Every matrix's
-    // workgroups start at a multiple of `splits`, so blockIdx / splits is a
-    // launch-wide block index (for the split counters and partials).
-    int gi = 0;
-#pragma unroll
-    for (int k = 1; k < QG_MAXG; k++) gi += bx >= gs.bstart[k];
+    // This workgroup's row block and K split.  Every matrix's workgroups start
+    // at a multiple of `splits` in the launch-wide count bx, so bx / splits is
+    // a launch-wide block index (for the split counters and partials).
+    const int b0 = gs.bstart[gi];
+    if (lb >= gs.bstart[gi + 1] - b0) return;  // past this matrix (uniform, before any barrier)
+    const int bx = b0 + lb;
     const int out_dim = gs.rows[gi], ldy = gs.ldy[gi];
     const int ngroups = in_dim >> 8;
-    int lb = bx - gs.bstart[gi], slot = gs.slot[gi];
+    int slot = gs.slot[gi];
     if (xs.tok_off) {
         // expert layers: entry gi is expert gs.slot[gi]; its workgroups cover
         // moe_c token chunks, each over all row blocks and splits
@@ -514,14 +529,14 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
         lb -= c * per;
         slot = slot * xs.moe_c + c;
     }
-    const QgTok tk = qg_tokens(xs, slot, in_dim);
+    const QgTok tk = qg_tokens(gs, gi, xs, slot, in_dim);
     const int n = tk.n;
     if (n <= 0) return;  // an empty token chunk (uniform over the workgroup, before any barrier)
     float* __restrict__ y = gs.y[gi] + (size_t)tk.a * (size_t)ldy;
     const QhBuf wb = qh_buf(gs.w[gi], gs.wbytes[gi]);
     const int blk = lb / splits, sp = lb - blk * splits, gblk = bx / splits;
     const int tile0 = blk * W + w;  // this wavefront's tile
-    const int g0 = (int)((int64_t)ngroups * sp / splits), g1 = (int)((int64_t)ngroups * (sp + 1) / splits);
+    const int g0 = ngroups * sp / splits, g1 = ngroups * (sp + 1) / splits;  // ngroups <= 256
     const int nk = g1 - g0;
     // Row blocks walk their split's groups from different starting points, so
     // concurrent workgroups read different parts of x (spreading the L2 load).
@@ -821,24 +836,25 @@ template <class F, int NT, int W, int MODE>
 __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs xs, uint32_t row_bytes, int in_dim,
                                                  int splits, float* __restrict__ part, unsigned int* __restrict__ cnt) {
     __shared__ __align__(16) unsigned char lds[qh_mmq_lds<F, NT, W, MODE>()];
-    qh_mmq_body<F, NT, W, MODE>(gs, xs, row_bytes, in_dim, splits, part, cnt, lds, (int)blockIdx.x);
+    qh_mmq_body<F, NT, W, MODE>(gs, xs, row_bytes, in_dim, splits, part, cnt, lds, (int)blockIdx.y, (int)blockIdx.x);
 }
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K),
-// both with resident images digitised in the kernel: workgroups below g1 run
-// F1's body on gs1's matrices, the others F2's on gs2's, each with its own
+// both with resident images digitised in the kernel: matrices (blockIdx.y)
+// below c1 run F1's body on gs1, the others F2's on gs2, each with its own
 // splits and its own region of the split-K partials and counters.
 template <class F1, class F2, int NT, int W>
 __global__ __launch_bounds__(64 * W) void qh_mmq_mix(const QgGroups gs1, const QgGroups gs2, const QgXs xs,
-                                                     uint32_t rb1, uint32_t rb2, int in_dim, int s1, int s2, int g1,
+                                                     uint32_t rb1, uint32_t rb2, int in_dim, int s1, int s2, int c1,
                                                      float* __restrict__ part, unsigned int* __restrict__ cnt,
                                                      float* __restrict__ part2, unsigned int* __restrict__ cnt2) {
     constexpr int L1 = qh_mmq_lds<F1, NT, W, 2>(), L2 = qh_mmq_lds<F2, NT, W, 2>();
     __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
-    if ((int)blockIdx.x < g1)
-        qh_mmq_body<F1, NT, W, 2>(gs1, xs, rb1, in_dim, s1, part, cnt, lds, (int)blockIdx.x);
+    if ((int)blockIdx.y < c1)
+        qh_mmq_body<F1, NT, W, 2>(gs1, xs, rb1, in_dim, s1, part, cnt, lds, (int)blockIdx.y, (int)blockIdx.x);
     else
-        qh_mmq_body<F2, NT, W, 2>(gs2, xs, rb2, in_dim, s2, part2, cnt2, lds, (int)blockIdx.x - g1);
+        qh_mmq_body<F2, NT, W, 2>(gs2, xs, rb2, in_dim, s2, part2, cnt2, lds, (int)blockIdx.y - c1,
+                                  (int)blockIdx.x);
 }
 
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
@@ -881,26 +897,27 @@ static int qh_mmq_splits_env() {
 }
 
 // Launch shape: QG_WAVES wavefronts (32-row tiles) per workgroup.
+// grid: (the largest matrix's workgroups, matrices); bstart[cnt] = the total.
 template <class F, int NT>
-static void launch_mmq_t(int mode, const QgGroups& gs, const QgXs& xs, int wgs, int splits, const QgScratch& sc,
+static void launch_mmq_t(int mode, const QgGroups& gs, const QgXs& xs, dim3 grid, int splits, const QgScratch& sc,
                          uint32_t row_bytes, int in_dim, hipStream_t st) {
     if (mode == 2)
-        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 2>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
-                           row_bytes, in_dim, splits, sc.part, sc.cnt);
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 2>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
+                           splits, sc.part, sc.cnt);
     else if (mode == 1)
-        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 1>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
-                           row_bytes, in_dim, splits, sc.part, sc.cnt);
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 1>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
+                           splits, sc.part, sc.cnt);
     else
-        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 0>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, gs, xs,
-                           row_bytes, in_dim, splits, sc.part, sc.cnt);
+        hipLaunchKernelGGL((qh_mmq<F, NT, QG_WAVES, 0>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
+                           splits, sc.part, sc.cnt);
 }
 
 template <class F>
-static void launch_mmq_nt(int nt, int mode, const QgGroups& gs, const QgXs& xs, int wgs, int splits,
+static void launch_mmq_nt(int nt, int mode, const QgGroups& gs, const QgXs& xs, dim3 grid, int splits,
                           const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
-    if (nt <= 4) launch_mmq_t<F, 4>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else if (nt <= 8) launch_mmq_t<F, 8>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq_t<F, 16>(mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st);
+    if (nt <= 4) launch_mmq_t<F, 4>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 8) launch_mmq_t<F, 8>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
+    else launch_mmq_t<F, 16>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
 }
 
 struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
@@ -958,6 +975,9 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         gs.rows[i] = en[i].rows;
         gs.ldy[i] = en[i].ldy;
         gs.slot[i] = j;
+        gs.x[i] = en[i].x;
+        gs.x2[i] = en[i].x2;
+        gs.n[i] = en[i].n;
         ntmax = en[i].n > ntmax ? en[i].n : ntmax;
     }
     // One 32-row tile per wavefront, QG_WAVES per workgroup.  Splits: enough
@@ -997,24 +1017,27 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         hipError_t e = qg_run(type, &a, 1, in_dim, row_bytes, sc, st, accum);
         return e != hipSuccess ? e : qg_run(type, &b, 1, in_dim, row_bytes, sc, st, accum);
     }
-    int wgs = 0;
-    for (int i = 0; i < QG_MAXG; i++) {
-        gs.bstart[i] = i < cnt ? wgs : INT_MAX;
-        if (i < cnt) wgs += (en[i].rows + brows - 1) / brows * splits;
+    int wgs = 0, maxw = 0;
+    for (int i = 0; i < cnt; i++) {
+        gs.bstart[i] = wgs;
+        const int wi = (en[i].rows + brows - 1) / brows * splits;
+        wgs += wi;
+        maxw = wi > maxw ? wi : maxw;
     }
-    gs.bstart[QG_MAXG] = INT_MAX;
+    for (int i = cnt; i <= QG_MAXG; i++) gs.bstart[i] = wgs;
     gs.accum = accum;
+    const dim3 grid((unsigned)maxw, (unsigned)cnt);
     // the token blocks' x images, once per launch
     xs.img = sc.img;
     xs.img_bytes = (uint32_t)(nslots * ngroups * XImg::BYTES);
     if (mode != 2)
         hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
     switch (type) {
-        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
-        default: launch_mmq_nt<GQ6K>(ntmax, mode, gs, xs, wgs, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
+        case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ3_S: launch_mmq_nt<GIQ3S>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
+        case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
+        default: launch_mmq_nt<GQ6K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
     }
     return hipGetLastError();
 }
@@ -1108,10 +1131,10 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 // then makes one call per type.
 template <class F1, class F2, int NT>
 static void launch_mmq_mix(const QgGroups& g1s, const QgGroups& g2s, const QgXs& xs, uint32_t rb1, uint32_t rb2,
-                           int in_dim, int s1, int s2, int wgs1, int wgs, const QgScratch& sc, size_t poff, int coff,
+                           int in_dim, int s1, int s2, int c1, dim3 grid, const QgScratch& sc, size_t poff, int coff,
                            hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES>), dim3((unsigned)wgs), dim3(64 * QG_WAVES), 0, st, g1s, g2s,
-                       xs, rb1, rb2, in_dim, s1, s2, wgs1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
+    hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1, rb2,
+                       in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
 }
 
 hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
@@ -1158,22 +1181,25 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     QgXs xs = {};
     xs.x[0] = x;
     xs.n[0] = n;
+    int maxw = 0;
     auto fill = [&](QgGroups& g, int c, const uint8_t* const* Wt, float* const* Y, const int* o, uint32_t rb, int s) {
         g = QgGroups{};
         int w = 0;
-        for (int i = 0; i < QG_MAXG; i++) {
-            g.bstart[i] = i < c ? w : INT_MAX;
-            if (i < c) {
-                g.w[i] = Wt[i];
-                g.y[i] = Y[i];
-                g.wbytes[i] = (uint32_t)(((uint64_t)o[i] * rb + 3) & ~(uint64_t)3);
-                g.rows[i] = o[i];
-                g.ldy[i] = o[i];
-                g.slot[i] = 0;
-                w += (o[i] + brows - 1) / brows * s;
-            }
+        for (int i = 0; i < c; i++) {
+            g.bstart[i] = w;
+            g.w[i] = Wt[i];
+            g.y[i] = Y[i];
+            g.wbytes[i] = (uint32_t)(((uint64_t)o[i] * rb + 3) & ~(uint64_t)3);
+            g.rows[i] = o[i];
+            g.ldy[i] = o[i];
+            g.slot[i] = 0;
+            g.x[i] = x;
+            g.n[i] = n;
+            const int wi = (o[i] + brows - 1) / brows * s;
+            w += wi;
+            maxw = wi > maxw ? wi : maxw;
         }
-        g.bstart[QG_MAXG] = INT_MAX;
+        for (int i = c; i <= QG_MAXG; i++) g.bstart[i] = w;
         g.accum = 0;
     };
     QgGroups g1s, g2s;
@@ -1181,9 +1207,10 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     fill(g2s, c2, W2, Y2, o2, rb2, s2);
     const size_t poff = (size_t)wgs1 * pw;
     const int coff = b1 * QG_WAVES;
-    if (n <= 4) launch_mmq_mix<GQ4K, GQ6K, 4>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
-    else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
-    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, wgs1, wgs, *sc, poff, coff, st);
+    const dim3 grid((unsigned)maxw, (unsigned)(c1 + c2));
+    if (n <= 4) launch_mmq_mix<GQ4K, GQ6K, 4>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
+    else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
+    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
     return hipGetLastError();
 }
 
@@ -1236,30 +1263,30 @@ hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* 
         xs.img_bytes = (uint32_t)((int64_t)ne * C * ngroups * XImg::BYTES);
         QgGroups gs = {};
         int wgs = 0;
-        for (int i = 0; i < QG_MAXG; i++) {
-            gs.bstart[i] = i < sets * ne ? wgs : INT_MAX;
-            if (i < sets * ne) {
-                const int s = i / ne, e = i - s * ne;
-                gs.w[i] = E[s] + (size_t)(e0 + e) * slice;
-                gs.y[i] = Y[s];
-                gs.wbytes[i] = (uint32_t)((slice + 3) & ~(size_t)3);
-                gs.rows[i] = out_dim;
-                gs.ldy[i] = out_dim;
-                gs.slot[i] = e;
-                wgs += C * blocks * splits;
-            }
+        const int per = C * blocks * splits;  // workgroups of each (set, expert)
+        for (int i = 0; i < sets * ne; i++) {
+            const int s = i / ne, e = i - s * ne;
+            gs.bstart[i] = wgs;
+            gs.w[i] = E[s] + (size_t)(e0 + e) * slice;
+            gs.y[i] = Y[s];
+            gs.wbytes[i] = (uint32_t)((slice + 3) & ~(size_t)3);
+            gs.rows[i] = out_dim;
+            gs.ldy[i] = out_dim;
+            gs.slot[i] = e;
+            wgs += per;
         }
-        gs.bstart[QG_MAXG] = INT_MAX;
+        for (int i = sets * ne; i <= QG_MAXG; i++) gs.bstart[i] = wgs;
         gs.accum = accum;
+        const dim3 grid((unsigned)per, (unsigned)(sets * ne));
         if (mode != 2)
             hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)(ne * C)), dim3(512), 0, st, xs, sc->img,
                                in_dim);
         switch (type) {
-            case QT_Q4_K: launch_mmq_nt<GQ4K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_Q5_K: launch_mmq_nt<GQ5K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_IQ3_S: launch_mmq_nt<GIQ3S>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
-            default: launch_mmq_nt<GQ6K>(16, mode, gs, xs, wgs, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_Q4_K: launch_mmq_nt<GQ4K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_Q5_K: launch_mmq_nt<GQ5K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ3_S: launch_mmq_nt<GIQ3S>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            default: launch_mmq_nt<GQ6K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
