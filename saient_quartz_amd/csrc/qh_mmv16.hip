@@ -820,16 +820,22 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
 template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false, int NT = 1>
 __global__ __launch_bounds__(64 * W) void qh_mmv16(const float* __restrict__ x, const uint8_t* w0, float* y0,
                                                    const float* nw0, uint32_t wbytes0, int rows0, int ntiles0,
-                                                   int accum0, uint32_t row_bytes, int ngroups, const QhMats mm) {
+                                                   int nblk, uint32_t row_bytes, int ngroups, int accum0,
+                                                   const QhMats mm) {
     static_assert(qh_mmv16_lds<F, W, GPW, NT>() <= 163840, "LDS");
     static_assert(MULTI || NT == 1, "one-matrix launches run one token");
     __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW, NT>()];
     const QhOne one = {w0, y0, nw0, wbytes0, rows0, ntiles0, accum0};
-    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, one, x, row_bytes, ngroups, lds, (int)blockIdx.x,
-                                                  (int)gridDim.x);
+    // nblk = gridDim.x, passed as a preloaded argument: gridDim comes from the
+    // hidden arguments in memory, and the first loads would wait for it
+    qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, one, x, row_bytes, ngroups, lds, (int)blockIdx.x, nblk);
 }
-// The leading scalar arguments of a qh_mmv16 launch (matrix 0 of mm).
-#define QH_ONE_ARGS(mm, x) (x), (mm).w[0], (mm).y[0], (mm).nw, (mm).wbytes[0], (mm).rows[0], (mm).tstart[QH_MULTI], (mm).accum
+// The leading scalar arguments of a qh_mmv16 launch (matrix 0 of mm), up to
+// the grid size; 14 dwords are preloaded (the rest of the 16 user SGPRs hold
+// the argument pointer), so the accumulate flag, needed only at the end, follows.
+#define QH_ONE_ARGS(mm, x, grid, row_bytes, ngroups) \
+    (x), (mm).w[0], (mm).y[0], (mm).nw, (mm).wbytes[0], (mm).rows[0], (mm).tstart[QH_MULTI], (grid), (row_bytes), \
+        (ngroups), (mm).accum
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
 // workgroups below g1 run F1's body on mm1's matrices, the others F2's on mm2's.
@@ -866,7 +872,7 @@ static hipError_t launch_mmv16_grid(const QhMats& mm, int nm, const float* x, in
         int grid = pairs < resident ? pairs : resident;
         if ((pairs + grid - 1) / grid > QH_MAXT / 2) grid = (pairs + QH_MAXT / 2 - 1) / (QH_MAXT / 2);
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, true>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
+                           QH_ONE_ARGS(mm, x, grid, row_bytes, in_dim / 256), mm);
         return hipGetLastError();
     }
     // One workgroup per tile up to what the device holds at once (tiles go
@@ -876,10 +882,10 @@ static hipError_t launch_mmv16_grid(const QhMats& mm, int nm, const float* x, in
     if ((tiles + grid - 1) / grid > QH_MAXT) grid = (tiles + QH_MAXT - 1) / QH_MAXT;
     if (nm > 1)
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, true, false>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                           QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
+                           QH_ONE_ARGS(mm, x, grid, row_bytes, in_dim / 256), mm);
     else
         hipLaunchKernelGGL((qh_mmv16<F, W, GPW, X1, false, false>), dim3((unsigned)grid), dim3(64 * W), 0,
-                           st, QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
+                           st, QH_ONE_ARGS(mm, x, grid, row_bytes, in_dim / 256), mm);
     return hipGetLastError();
 }
 
@@ -1099,7 +1105,7 @@ static hipError_t launch_mmv16_tok(const QhMats& mm, const float* x, int in_dim,
     int grid = tiles < resident ? tiles : resident;
     if ((tiles + grid - 1) / grid > qh_maxt<NT>()) grid = (tiles + qh_maxt<NT>() - 1) / qh_maxt<NT>();
     hipLaunchKernelGGL((qh_mmv16<F, W, 1, X1, true, false, NT>), dim3((unsigned)grid), dim3(64 * W), 0, st,
-                       QH_ONE_ARGS(mm, x), row_bytes, in_dim / 256, mm);
+                       QH_ONE_ARGS(mm, x, grid, row_bytes, in_dim / 256), mm);
     return hipGetLastError();
 }
 
