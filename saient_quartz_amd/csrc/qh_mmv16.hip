@@ -479,16 +479,19 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     }
     const int n = lane & 15, kg = lane >> 4;
     // A operand of MFMA s: digit plane n%4 of lane kg's piece in rows 4kg..4kg+2.
-    const bool arow = (n >> 2) == kg && (n & 3) < 3;
+    // (set after the first loads are issued: see set_offsets)
     uint32_t aoff[4], xsoff[4];
-    aoff[0] = arow ? 256u * (n & 3) + 16u * F::template piece<0>(kg) : QH_XG_ZERO;
-    aoff[1] = arow ? 256u * (n & 3) + 16u * F::template piece<1>(kg) : QH_XG_ZERO;
-    aoff[2] = arow ? 256u * (n & 3) + 16u * F::template piece<2>(kg) : QH_XG_ZERO;
-    aoff[3] = arow ? 256u * (n & 3) + 16u * F::template piece<3>(kg) : QH_XG_ZERO;
-    xsoff[0] = QH_XG_SUM + 4u * F::template piece<0>(kg);
-    xsoff[1] = QH_XG_SUM + 4u * F::template piece<1>(kg);
-    xsoff[2] = QH_XG_SUM + 4u * F::template piece<2>(kg);
-    xsoff[3] = QH_XG_SUM + 4u * F::template piece<3>(kg);
+    auto set_offsets = [&]() {
+        const bool arow = (n >> 2) == kg && (n & 3) < 3;
+        aoff[0] = arow ? 256u * (n & 3) + 16u * F::template piece<0>(kg) : QH_XG_ZERO;
+        aoff[1] = arow ? 256u * (n & 3) + 16u * F::template piece<1>(kg) : QH_XG_ZERO;
+        aoff[2] = arow ? 256u * (n & 3) + 16u * F::template piece<2>(kg) : QH_XG_ZERO;
+        aoff[3] = arow ? 256u * (n & 3) + 16u * F::template piece<3>(kg) : QH_XG_ZERO;
+        xsoff[0] = QH_XG_SUM + 4u * F::template piece<0>(kg);
+        xsoff[1] = QH_XG_SUM + 4u * F::template piece<1>(kg);
+        xsoff[2] = QH_XG_SUM + 4u * F::template piece<2>(kg);
+        xsoff[3] = QH_XG_SUM + 4u * F::template piece<3>(kg);
+    };
 
     // Weight loads of item (tile, ch).  Rows past out_dim and groups past in_dim
     // get offsets beyond the buffer range and read as zeros, so the load stream
@@ -714,13 +717,6 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     };
     int tile = wg_tile(0), done = 0;
     if (tile >= ntiles) return;  // uniform over the workgroup
-    // Few tiles per workgroup: meet every RING tiles (the end-of-kernel wait
-    // for the slowest wavefront is what short launches pay).  Many tiles: meet
-    // at every tile (PAIR: every pair), which keeps the wavefronts on one tile's
-    // rows at a time.
-    const int my_tiles = PAIR ? 2 * ((ntiles / 2 - bid + nblk - 1) / nblk)
-                              : (ntiles - bid + nblk - 1) / nblk;
-    const int ring = my_tiles <= 2 * RING ? RING : (PAIR ? 2 : 1);
     // Pipeline: the registers of an item are staged into LDS as soon as they
     // arrive and then receive the loads of the next item, which stay in flight
     // while the staged item is computed.  No loaded value is copied between
@@ -736,9 +732,25 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
 #pragma unroll
     for (int k = 0; k < NT; k++) rs[k] = tot[k] = 0.f;
     qh_u32x4 nv[GPW];
+    // A launch's first instructions are fetched from memory (its code is
+    // evicted from L2 by the weight stream of the launches before it), so the
+    // first loads go out ahead of every computation they do not need (the IQ
+    // formats, bound by their decode, measured better without the fence).
+    if constexpr (F::GRID != 0) set_offsets();
     load_x(0, xva);
     load_nw(nv);
     load_w(tile, 0, wra);
+    if constexpr (F::GRID == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        set_offsets();
+    }
+    // Few tiles per workgroup: meet every RING tiles (the end-of-kernel wait
+    // for the slowest wavefront is what short launches pay).  Many tiles: meet
+    // at every tile (PAIR: every pair), which keeps the wavefronts on one tile's
+    // rows at a time.
+    const int my_tiles = PAIR ? 2 * ((ntiles / 2 - bid + nblk - 1) / nblk)
+                              : (ntiles - bid + nblk - 1) / nblk;
+    const int ring = my_tiles <= 2 * RING ? RING : (PAIR ? 2 : 1);
     if constexpr (F::GRID != 0) {
         const uint32_t* src = F::GRID == 1 ? qh_g_iq3s : reinterpret_cast<const uint32_t*>(qh_g_iq2xxs);
         for (int i = threadIdx.x; i < 512; i += 64 * W) reinterpret_cast<uint32_t*>(gridl)[i] = src[i];
