@@ -385,14 +385,15 @@ struct QhMats {
     int ldy[QH_MULTI];
 };
 
-// The one-matrix launch's arguments as leading scalars: the hardware preloads
-// them into SGPRs when a wavefront starts (built with
+// The one-matrix (and SwiGLU pair) launch's arguments as leading scalars: the
+// hardware preloads them into SGPRs when a wavefront starts (built with
 // -amdgpu-kernarg-preload-count=16), so the first weight loads go out without
 // a round trip to the kernel-argument memory (a cold miss of about 1 us; an
-// aggregate argument is always read from memory).  Multi-matrix launches read
-// QhMats.
+// aggregate argument is always read from memory).  Other multi-matrix launches
+// read QhMats.
 struct QhOne {
     const uint8_t* w;
+    const uint8_t* w1;  // SwiGLU pairs: the up matrix (same rows and byte range as w)
     float* y;
     const float* nw;
     uint32_t wbytes;
@@ -440,8 +441,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     float* res = red + 2 * RING * W * 16 * NT;  // finished rows of this workgroup's tiles
     float* sqw = res + qh_maxt<NT>() * 16 * NT;  // per-wavefront sums of x^2 (fused RMS norm)
     unsigned char* gridl = reinterpret_cast<unsigned char*>(sqw + W * NT);  // IQ codebook (GRID formats)
-    const int ntiles = MULTI ? mm.tstart[QH_MULTI] : one.ntiles;
-    const float* const nwp = MULTI ? mm.nw : one.nw;
+    constexpr bool AGG = MULTI && !PAIR;  // matrices from the QhMats aggregate
+    const int ntiles = AGG ? mm.tstart[QH_MULTI] : one.ntiles;
+    const float* const nwp = AGG ? mm.nw : one.nw;
     // matrix of a (workgroup-uniform) tile index
     auto mat_of = [&](int tile) {
         int m = 0;
@@ -463,6 +465,7 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
         return bid + k * nblk;
     };
     const QhBuf wb0 = qh_buf(one.w, one.wbytes);  // the one-matrix case
+    const QhBuf wb1 = qh_buf(PAIR ? one.w1 : one.w, one.wbytes);  // SwiGLU pairs: up
     const int nch = (ngroups + W * GPW - 1) / (W * GPW);
 
     // Slices of this lane in a tile: row rr[h], byte offset goff[h] from the
@@ -499,8 +502,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
         const int g0 = ch * (W * GPW) + w * GPW;
         const int m = mat_of(tile);
-        const QhBuf wb = MULTI ? qh_buf(mm.w[m], mm.wbytes[m]) : wb0;
-        const int out_dim = MULTI ? mm.rows[m] : one.rows;
+        const QhBuf wb = AGG ? qh_buf(mm.w[m], mm.wbytes[m]) : (PAIR && m ? wb1 : wb0);
+        const int out_dim = AGG ? mm.rows[m] : one.rows;
         if (MULTI) tile = local_tile(tile, m);
         const uint32_t base = (uint32_t)(tile * ROWS) * row_bytes;
 #pragma unroll
@@ -817,9 +820,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
         __syncthreads();
         for (int i = threadIdx.x; i < (done >> 1) * 16; i += 64 * W) {
             const int q = i >> 4, c = i & 15, row = local_tile(wg_tile(2 * q), 0) * ROWS + c;
-            if (c < ROWS && row < mm.rows[0]) {
+            if (c < ROWS && row < one.rows) {
                 const float g = res[(2 * q) * 16 + c], u = res[(2 * q + 1) * 16 + c];
-                mm.y[0][row] = (g / (1.f + expf(-g))) * u;
+                one.y[row] = (g / (1.f + expf(-g))) * u;
             }
         }
         return;
@@ -830,24 +833,25 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
 }
 
 template <class F, int W, int GPW, bool X1, bool MULTI, bool PAIR = false, int NT = 1>
-__global__ __launch_bounds__(64 * W) void qh_mmv16(const float* __restrict__ x, const uint8_t* w0, float* y0,
-                                                   const float* nw0, uint32_t wbytes0, int rows0, int ntiles0,
-                                                   int nblk, uint32_t row_bytes, int ngroups, int accum0,
-                                                   const QhMats mm) {
+__global__ __launch_bounds__(64 * W) void qh_mmv16(const float* __restrict__ x, const uint8_t* w0,
+                                                   const uint8_t* w1, const float* nw0, uint32_t wbytes0, int rows0,
+                                                   int ntiles0, int nblk, uint32_t row_bytes, int ngroups, float* y0,
+                                                   int accum0, const QhMats mm) {
     static_assert(qh_mmv16_lds<F, W, GPW, NT>() <= 163840, "LDS");
     static_assert(MULTI || NT == 1, "one-matrix launches run one token");
     __shared__ __align__(16) unsigned char lds[qh_mmv16_lds<F, W, GPW, NT>()];
-    const QhOne one = {w0, y0, nw0, wbytes0, rows0, ntiles0, accum0};
+    const QhOne one = {w0, w1, y0, nw0, wbytes0, rows0, ntiles0, accum0};
     // nblk = gridDim.x, passed as a preloaded argument: gridDim comes from the
     // hidden arguments in memory, and the first loads would wait for it
     qh_mmv16_body<F, W, GPW, X1, MULTI, PAIR, NT>(mm, one, x, row_bytes, ngroups, lds, (int)blockIdx.x, nblk);
 }
-// The leading scalar arguments of a qh_mmv16 launch (matrix 0 of mm), up to
-// the grid size; 14 dwords are preloaded (the rest of the 16 user SGPRs hold
-// the argument pointer), so the accumulate flag, needed only at the end, follows.
+// The leading scalar arguments of a qh_mmv16 launch (matrices 0 and 1 of mm),
+// up to the group count: 14 dwords are preloaded (the rest of the 16 user SGPRs
+// hold the argument pointer), so y and the accumulate flag, needed only at the
+// end, follow.
 #define QH_ONE_ARGS(mm, x, grid, row_bytes, ngroups) \
-    (x), (mm).w[0], (mm).y[0], (mm).nw, (mm).wbytes[0], (mm).rows[0], (mm).tstart[QH_MULTI], (grid), (row_bytes), \
-        (ngroups), (mm).accum
+    (x), (mm).w[0], (mm).w[1], (mm).nw, (mm).wbytes[0], (mm).rows[0], (mm).tstart[QH_MULTI], (grid), (row_bytes), \
+        (ngroups), (mm).y[0], (mm).accum
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K):
 // workgroups below g1 run F1's body on mm1's matrices, the others F2's on mm2's.
