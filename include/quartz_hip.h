@@ -151,10 +151,13 @@ int hip_gemm_grouped_norm_static_async(uint32_t ggml_type, int count, const uint
  * Q4_K_M models have (src/cuda.rs:549-562).  For 2..4 tokens, two types among
  * Q4_K/Q5_K + Q6_K and in_dim <= 4096, one launch computes every matrix; each
  * token's result then equals the per-type call's bit for bit.  For 5..16
- * tokens of Q4_K + Q6_K, the rows are normalised once into d_scratch (n *
+ * tokens of Q4_K + Q6_K, one launch normalises the rows straight into the
+ * batched kernel's x images (in_dim <= 4096; otherwise into d_scratch, n *
  * in_dim floats) and both types run in one batched matrix-core launch; each
  * token's result equals the per-type batched call's within rounding (the split
- * of K may differ).  Otherwise one hip_gemm_grouped_norm_async per type, with
+ * of K may differ).  For 5..16 tokens of one matrix-core type and in_dim <=
+ * 4096, the same fused norm feeds that type's batched launch, bit-identical to
+ * the per-type call.  Otherwise one hip_gemm_grouped_norm_async per type, with
  * its scratch rule. */
 int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* const* d_data, const float* d_x,
                               const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,

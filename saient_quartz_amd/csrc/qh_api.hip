@@ -423,9 +423,14 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
         for (int k = 0; k < count; k++)
             ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
         if (ok) {
-            QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st, n), "hip_gemm_group_norm");
+            // the norm fused into the images (one launch), then both types
             hipError_t e = qh_launch_mmq_mixed(ut[0], cnt[0], wu[0], yu[0], ou[0], ut[1], cnt[1], wu[1], yu[1], ou[1],
-                                               scratch, n, in_dim, st);
+                                               x, n, in_dim, st, norm_w);
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
+            QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st, n), "hip_gemm_group_norm");
+            e = qh_launch_mmq_mixed(ut[0], cnt[0], wu[0], yu[0], ou[0], ut[1], cnt[1], wu[1], yu[1], ou[1], scratch, n,
+                                    in_dim, st);
             if (e == hipSuccess) return QH_OK;
             if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
             // scratch holds the normalised rows: one grouped call per type
@@ -440,6 +445,18 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
                 if (rc) return rc;
             }
             return QH_OK;
+        }
+    }
+    // 5-16 tokens of one type (a layer's gate and up, the output head): the
+    // norm fused into the images (one launch), then the batched kernel on them
+    if (n >= 5 && n <= 16 && nut == 1 && !qh_force_valu()) {
+        bool ok = true;
+        for (int k = 0; k < count; k++)
+            ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
+        if (ok) {
+            hipError_t e = qh_launch_mmq_norm(ut[0], cnt[0], wu[0], yu[0], ou[0], x, norm_w, n, in_dim, st);
+            if (e == hipSuccess) return QH_OK;
+            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
         }
     }
     for (int u = 0; u < nut; u++) {

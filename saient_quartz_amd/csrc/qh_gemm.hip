@@ -840,21 +840,22 @@ __global__ __launch_bounds__(64 * W) void qh_mmq(const QgGroups gs, const QgXs x
 }
 
 // Two formats sharing x in one launch (a layer's q/k in Q4_K and v in Q6_K),
-// both with resident images digitised in the kernel: matrices (blockIdx.y)
+// both with resident images (MODE 2: digitised in the kernel; MODE 1: built by
+// qg_norm_image before the launch): matrices (blockIdx.y)
 // below c1 run F1's body on gs1, the others F2's on gs2, each with its own
 // splits and its own region of the split-K partials and counters.
-template <class F1, class F2, int NT, int W>
+template <class F1, class F2, int NT, int W, int MODE>
 __global__ __launch_bounds__(64 * W) void qh_mmq_mix(const QgGroups gs1, const QgGroups gs2, const QgXs xs,
                                                      uint32_t rb1, uint32_t rb2, int in_dim, int s1, int s2, int c1,
                                                      float* __restrict__ part, unsigned int* __restrict__ cnt,
                                                      float* __restrict__ part2, unsigned int* __restrict__ cnt2) {
-    constexpr int L1 = qh_mmq_lds<F1, NT, W, 2>(), L2 = qh_mmq_lds<F2, NT, W, 2>();
+    constexpr int L1 = qh_mmq_lds<F1, NT, W, MODE>(), L2 = qh_mmq_lds<F2, NT, W, MODE>();
     __shared__ __align__(16) unsigned char lds[L1 > L2 ? L1 : L2];
     if ((int)blockIdx.y < c1)
-        qh_mmq_body<F1, NT, W, 2>(gs1, xs, rb1, in_dim, s1, part, cnt, lds, (int)blockIdx.y, (int)blockIdx.x);
+        qh_mmq_body<F1, NT, W, MODE>(gs1, xs, rb1, in_dim, s1, part, cnt, lds, (int)blockIdx.y, (int)blockIdx.x);
     else
-        qh_mmq_body<F2, NT, W, 2>(gs2, xs, rb2, in_dim, s2, part2, cnt2, lds, (int)blockIdx.y - c1,
-                                  (int)blockIdx.x);
+        qh_mmq_body<F2, NT, W, MODE>(gs2, xs, rb2, in_dim, s2, part2, cnt2, lds, (int)blockIdx.y - c1,
+                                     (int)blockIdx.x);
 }
 
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
@@ -954,8 +955,10 @@ static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
 
 // One grouped launch: every entry's row blocks, each workgroup digitising its
 // own K split of its entry's x.
+// img_ready: the launch's one token block already has its images in slot 0
+// (qg_norm_image), so no image launch and no in-kernel digitisation.
 static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, uint32_t row_bytes,
-                         const QgScratch& sc, hipStream_t st, int accum) {
+                         const QgScratch& sc, hipStream_t st, int accum, bool img_ready = false) {
     const int ngroups = in_dim / 256;
     QgXs xs = {};
     QgGroups gs = {};
@@ -999,14 +1002,20 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     const int fm = qh_mmq_mode_env();
     if (fm == 0) mode = 0;
     else if (fm >= 1 && fm <= 2 && res) mode = fm;
+    if (img_ready) {
+        if (nslots != 1) return hipErrorNotSupported;
+        mode = res ? 1 : 0;
+    }
     const int64_t pb = (int64_t)(brows / 32) * 16 * 32;  // floats of one partial block (16-token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
     const bool img_fits = (int64_t)nslots * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES;
     if (!img_fits || (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES))) {
         if (cnt > 1) {
-            hipError_t e = qg_run(type, en, cnt / 2, in_dim, row_bytes, sc, st, accum);
-            return e != hipSuccess ? e : qg_run(type, en + cnt / 2, cnt - cnt / 2, in_dim, row_bytes, sc, st, accum);
+            hipError_t e = qg_run(type, en, cnt / 2, in_dim, row_bytes, sc, st, accum, img_ready);
+            return e != hipSuccess ? e
+                                   : qg_run(type, en + cnt / 2, cnt - cnt / 2, in_dim, row_bytes, sc, st, accum,
+                                            img_ready);
         }
         const int half = (en[0].rows / 2 + brows - 1) / brows * brows;
         QgEntry a = en[0], b = en[0];
@@ -1014,8 +1023,8 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         b.rows = en[0].rows - half;
         b.w += (size_t)half * row_bytes;
         b.y += half;
-        hipError_t e = qg_run(type, &a, 1, in_dim, row_bytes, sc, st, accum);
-        return e != hipSuccess ? e : qg_run(type, &b, 1, in_dim, row_bytes, sc, st, accum);
+        hipError_t e = qg_run(type, &a, 1, in_dim, row_bytes, sc, st, accum, img_ready);
+        return e != hipSuccess ? e : qg_run(type, &b, 1, in_dim, row_bytes, sc, st, accum, img_ready);
     }
     int wgs = 0, maxw = 0;
     for (int i = 0; i < cnt; i++) {
@@ -1030,7 +1039,7 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     // the token blocks' x images, once per launch
     xs.img = sc.img;
     xs.img_bytes = (uint32_t)(nslots * ngroups * XImg::BYTES);
-    if (mode != 2)
+    if (mode != 2 && !img_ready)
         hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
     switch (type) {
         case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
@@ -1122,6 +1131,28 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
     return qh_launch_mmq_grouped(type, 1, &W, &x, &y, &n, &out_dim, in_dim, st, nullptr, 0, nullptr);
 }
 
+hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W, float* const* Y, const int* out_dims,
+                              const float* x, const float* nw, int n, int in_dim, hipStream_t st) {
+    if (n < 5 || n > 16 || count < 1 || count > QG_MAXG || in_dim % 256 || in_dim > 4096 || !nw)
+        return hipErrorNotSupported;
+    if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
+        return hipErrorNotSupported;
+    const QgScratch* sc = qh_mmq_scratch_ptrs();
+    if (!sc) return hipErrorNotSupported;
+    const uint32_t row_bytes = (uint32_t)qh_type_size(type, (size_t)in_dim);
+    QgEntry en[QG_MAXG];
+    int cnt = 0;
+    for (int i = 0; i < count; i++) {
+        if (out_dims[i] <= 0) continue;
+        if ((int64_t)out_dims[i] * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
+        en[cnt++] = QgEntry{W[i], x, nullptr, Y[i], n, out_dims[i], out_dims[i]};
+    }
+    if (cnt == 0) return hipSuccess;
+    hipError_t e = qh_glue_norm_image(sc->img, x, nw, n, in_dim, st);
+    if (e != hipSuccess) return e;
+    return qg_run(type, en, cnt, in_dim, row_bytes, *sc, st, 0, true);
+}
+
 // Two weight types sharing one x of n <= 16 tokens (a layer's q, k in Q4_K and
 // v in Q6_K) in one launch, images digitised in the kernel: Y1[i] = W1[i] X,
 // Y2[i] = W2[i] X (token-major, token stride out_dims).  Splits are chosen
@@ -1132,16 +1163,20 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 template <class F1, class F2, int NT>
 static void launch_mmq_mix(const QgGroups& g1s, const QgGroups& g2s, const QgXs& xs, uint32_t rb1, uint32_t rb2,
                            int in_dim, int s1, int s2, int c1, dim3 grid, const QgScratch& sc, size_t poff, int coff,
-                           hipStream_t st) {
-    hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1, rb2,
-                       in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
+                           hipStream_t st, bool img_ready) {
+    if (img_ready)
+        hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES, 1>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1,
+                           rb2, in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
+    else
+        hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES, 2>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1,
+                           rb2, in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
 }
 
 hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
                                uint32_t t2, int c2, const uint8_t* const* W2, float* const* Y2, const int* o2,
-                               const float* x, int n, int in_dim, hipStream_t st) {
+                               const float* x, int n, int in_dim, hipStream_t st, const float* nw) {
     if (t1 == QT_Q6_K && t2 == QT_Q4_K)
-        return qh_launch_mmq_mixed(t2, c2, W2, Y2, o2, t1, c1, W1, Y1, o1, x, n, in_dim, st);
+        return qh_launch_mmq_mixed(t2, c2, W2, Y2, o2, t1, c1, W1, Y1, o1, x, n, in_dim, st, nw);
     if (t1 != QT_Q4_K || t2 != QT_Q6_K) return hipErrorNotSupported;
     if (n < 2 || n > 16 || c1 < 1 || c2 < 1 || c1 > QG_MAXG || c2 > QG_MAXG || in_dim % 256 ||
         in_dim / 256 > QG_MAX_GROUPS || ((uintptr_t)x & 15u))
@@ -1181,6 +1216,15 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     QgXs xs = {};
     xs.x[0] = x;
     xs.n[0] = n;
+    // nw: x's rows RMS-normalised with nw and digitised by qg_norm_image into
+    // image slot 0 first; the kernel then copies the images (MODE 1)
+    const bool img_ready = nw != nullptr;
+    if (img_ready) {
+        hipError_t e = qh_glue_norm_image(sc->img, x, nw, n, in_dim, st);
+        if (e != hipSuccess) return e;
+        xs.img = sc->img;
+        xs.img_bytes = (uint32_t)(ngroups * XImg::BYTES);
+    }
     int maxw = 0;
     auto fill = [&](QgGroups& g, int c, const uint8_t* const* Wt, float* const* Y, const int* o, uint32_t rb, int s) {
         g = QgGroups{};
@@ -1208,9 +1252,12 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     const size_t poff = (size_t)wgs1 * pw;
     const int coff = b1 * QG_WAVES;
     const dim3 grid((unsigned)maxw, (unsigned)(c1 + c2));
-    if (n <= 4) launch_mmq_mix<GQ4K, GQ6K, 4>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
-    else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
-    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st);
+    if (n <= 4) launch_mmq_mix<GQ4K, GQ6K, 4>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
+                                              img_ready);
+    else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
+                                              img_ready);
+    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
+                                              img_ready);
     return hipGetLastError();
 }
 

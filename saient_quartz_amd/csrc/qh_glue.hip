@@ -92,6 +92,47 @@ __global__ __launch_bounds__(1024) void qg_rms_norm(float* out, const float* x, 
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * r * w[i];
 }
 
+// RMS norm of each token's row fused with the batched GEMM's x images: token
+// t = blockIdx.x of a token-major batch (<= 16 tokens) is normalised exactly as
+// qg_rms_norm's one-float4-per-thread path computes it (the same per-thread
+// sums, block sum and products), and digitised straight into image slot 0
+// (qg_digitise: one half-wavefront per 256-element group), so the GEMM reads
+// the images (no normalised rows in memory, no image launch of its own).
+// n % 256 == 0, n <= 4 blockDim.x, 16-byte aligned x and w.
+__global__ __launch_bounds__(1024) void qg_norm_image(unsigned char* __restrict__ img, const float* x,
+                                                      const float* w, int n) {
+    __shared__ float sm[16];
+    const int t = blockIdx.x;
+    x += (size_t)t * n;
+    const int i = 4 * (int)threadIdx.x;
+    float4 xv = {0.f, 0.f, 0.f, 0.f};
+    if (i < n) xv = *reinterpret_cast<const float4*>(x + i);
+    float s = (xv.x * xv.x + xv.y * xv.y) + (xv.z * xv.z + xv.w * xv.w);
+    s = qg_block_sum(s, sm);
+    const float r = rsqrtf(s / (float)n + 1e-5f);
+    const int lane = threadIdx.x & 63, xc = threadIdx.x & 31, ngroups = n >> 8, nh = (int)blockDim.x >> 5;
+    // group loop uniform over each wavefront (both halves call qg_digitise)
+    for (int g0 = 0; g0 < ngroups; g0 += nh) {
+        const int g = g0 + ((int)threadIdx.x >> 5);
+        const bool on = g < ngroups;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (on) {
+            const int e = 256 * g + 8 * xc;
+            const float4 a = *reinterpret_cast<const float4*>(x + e), b = *reinterpret_cast<const float4*>(x + e + 4);
+            const float4 wa = *reinterpret_cast<const float4*>(w + e), wb = *reinterpret_cast<const float4*>(w + e + 4);
+            v[0] = a.x * r * wa.x;
+            v[1] = a.y * r * wa.y;
+            v[2] = a.z * r * wa.z;
+            v[3] = a.w * r * wa.w;
+            v[4] = b.x * r * wb.x;
+            v[5] = b.y * r * wb.y;
+            v[6] = b.z * r * wb.z;
+            v[7] = b.w * r * wb.w;
+        }
+        qg_digitise(v, on, lane, t, xc, img + (size_t)(on ? g : 0) * XImg::BYTES);
+    }
+}
+
 // RoPE with YaRN on n_heads heads of head_dim (rope_yarn_f32, :577-605): pair i
 // of a head rotates (i, i + head_dim/2) (NEOX) or (2i, 2i+1) (NORM) by pos *
 // inv_freq(i), inv_freq ramped between theta^(-2i/d) and that / yarn_scale for
@@ -566,6 +607,16 @@ hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, h
     if (n % 4 == 0 && n <= 4096) blk = (n / 4 + 63) / 64 * 64;  // one float4 per thread (the register path)
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(qg_rms_norm, dim3((unsigned)rows), dim3(blk), 0, st, out, x, w, n);
+    return hipGetLastError();
+}
+
+hipError_t qh_glue_norm_image(unsigned char* img, const float* x, const float* w, int n_tok, int in_dim,
+                              hipStream_t st) {
+    // the launch shape of qh_glue_rms_norm's register path, so the norm is its
+    if (n_tok < 1 || n_tok > 16 || in_dim % 256 || in_dim > 4096 || (((uintptr_t)x | (uintptr_t)w) & 15u))
+        return hipErrorNotSupported;
+    const int blk = (in_dim / 4 + 63) / 64 * 64;
+    hipLaunchKernelGGL(qg_norm_image, dim3((unsigned)n_tok), dim3(blk), 0, st, img, x, w, in_dim);
     return hipGetLastError();
 }
 

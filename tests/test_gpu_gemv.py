@@ -357,7 +357,7 @@ def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21)], ids=str)
+@pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21), (12, 12), (14,), (16, 16)], ids=str)
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("in_dim", [4096, 2048, 5120])
 def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
@@ -368,7 +368,9 @@ def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     Q4_K + Q6_K at 5-16 tokens runs the two-format batched launch, whose K
     splits may differ from the per-type calls': there the bar is 1e-5 relative
     against them.  5120 is past the one-workgroup norm; IQ3_S + Q4_K has no
-    two-format kernel."""
+    two-format kernel.  One type at 5-16 tokens (in_dim <= 4096) takes the norm
+    fused into the batched kernel's x images: its images are the per-type
+    call's digitised normalised rows, so it is bit-identical too."""
     import ctypes as C
     outs = [300, 77, 64][:len(types)]
     rng = np.random.default_rng(n + in_dim + sum(types))
