@@ -931,7 +931,7 @@ struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
 
 // K splits per row block: the count s (at least ngroups / gmax) that
 // minimises the rounds of `target` workgroups times (3 + the groups each one
-// walks), the fewest splits on ties.
+// walks), plus the merge's rounds of partial loads, the fewest splits on ties.
 static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
     const int smin = (ngroups + gmax - 1) / gmax;
     const int cap = ngroups > smin ? ngroups : smin;
@@ -943,8 +943,12 @@ static int qg_pick_splits(int blocks, int ngroups, int gmax, int target) {
         // as much as 3 groups of weights (measured: 14336 x 4096 Q4_K at 16
         // tokens 21.7 us with 4 splits of 4 groups, 29.7 with 8 of 2 in two
         // rounds; 1024 x 4096 Q6_K 20.6 us with 4 splits on 16 workgroups)
+        // plus half a group per round of the merging wavefront's partial loads
+        // (4 splits per round; in half-group units: 4096 x 4096 Q4_K at 16
+        // tokens 16.1 us with 16 splits, 13.6 with 8; a full group per round
+        // moved 4096 x 14336 from 14 to 12 splits, 25.5 -> 26.2 us)
         const int gps = (ngroups + s - 1) / s;
-        const int64_t cost = rounds * (3 + gps);
+        const int64_t cost = 2 * rounds * (3 + gps) + (s + 3) / 4;
         if (cost < best_cost) {
             best_cost = cost;
             best = s;
@@ -1202,7 +1206,8 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
             const int64_t wgs = (int64_t)b1 * a + (int64_t)b2 * b;
             const int64_t rounds = (wgs + QG_TARGET_WGS - 1) / QG_TARGET_WGS;
             const int gps = (ngroups + a - 1) / a > (ngroups + b - 1) / b ? (ngroups + a - 1) / a : (ngroups + b - 1) / b;
-            const int64_t cost = rounds * (3 + gps);
+            const int merge = (a > b ? a : b) + 3;
+            const int64_t cost = 2 * rounds * (3 + gps) + merge / 4;
             if (cost < best || (cost == best && wgs < best_wgs)) {
                 best = cost;
                 best_wgs = wgs;
