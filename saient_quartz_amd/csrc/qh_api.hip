@@ -447,9 +447,14 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
             return QH_OK;
         }
     }
-    // 5-16 tokens of one type (a layer's gate and up, the output head): the
-    // norm fused into the images (one launch), then the batched kernel on them
-    if (n >= 5 && n <= 16 && nut == 1 && !qh_force_valu()) {
+    // 5-16 tokens of one type (a layer's gate and up, the output head), or 3-4
+    // tokens over more than 16 MB of weights (which the per-type call also
+    // takes to the batched kernel): the norm fused into the images (one
+    // launch), then the batched kernel on them
+    int64_t wb1 = 0;
+    for (int k = 0; k < count; k++)
+        wb1 += (int64_t)qh_type_size(types[k], (size_t)in_dim) * (out_dims[k] > 0 ? out_dims[k] : 0);
+    if (n >= 3 && n <= 16 && (n >= 5 || wb1 > ((int64_t)16 << 20)) && nut == 1 && !qh_force_valu()) {
         bool ok = true;
         for (int k = 0; k < count; k++)
             ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];

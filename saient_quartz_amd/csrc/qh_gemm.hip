@@ -1137,7 +1137,7 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 
 hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W, float* const* Y, const int* out_dims,
                               const float* x, const float* nw, int n, int in_dim, hipStream_t st) {
-    if (n < 5 || n > 16 || count < 1 || count > QG_MAXG || in_dim % 256 || in_dim > 4096 || !nw)
+    if (n < 2 || n > 16 || count < 1 || count > QG_MAXG || in_dim % 256 || in_dim > 4096 || !nw)
         return hipErrorNotSupported;
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;

@@ -49,7 +49,7 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
                                uint32_t t2, int c2, const uint8_t* const* W2, float* const* Y2, const int* o2,
                                const float* x, int n, int in_dim, hipStream_t st, const float* nw = nullptr);
-// n (5..16) tokens of x, RMS-normalised with nw, through count matrices of one
+// n (2..16) tokens of x, RMS-normalised with nw, through count matrices of one
 // type: the norm and the digitisation in one launch, then the batched kernel
 // on those images.  hipErrorNotSupported when the shapes do not fit.
 hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W, float* const* Y, const int* out_dims,

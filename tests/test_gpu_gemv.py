@@ -409,6 +409,43 @@ def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
             assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [3, 4])
+def test_gemm_group_norm_fused_images_few_tokens(qh, oracle, n):
+    """3-4 tokens over more than 16 MB of one type (a batch of 3-4 sequences'
+    gate and up) take the norm fused into the batched kernel's x images:
+    bit-identical to the per-type normalise-then-GEMM call, and within the bar
+    of the oracle on the float64-normalised rows."""
+    import ctypes as C
+    t, in_dim, outs = 12, 4096, [4096, 4096]
+    rng = np.random.default_rng(7 + n)
+    x = (rng.standard_normal((n, in_dim)) * rng.uniform(0.1, 10, (n, 1))).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    datas = [synth.weights(t, o, in_dim, seed=o + n + k) for k, o in enumerate(outs)]
+    dw = [GpuBuf.upload(d) for d in datas]
+    dx, dn = GpuBuf.upload_f32(x.reshape(-1)), GpuBuf.upload_f32(w)
+    dy = [GpuBuf.alloc_f32(n * o) for o in outs]
+    ey = [GpuBuf.alloc_f32(n * o) for o in outs]
+    scratch = GpuBuf.alloc_f32(n * in_dim)
+    k = len(outs)
+    check("hip_gemm_group_norm_async", qh.hip_gemm_group_norm_async(
+        k, (C.c_uint32 * k)(*([t] * k)), (C.c_void_p * k)(*[b.ptr for b in dw]), dx.ptr, dn.ptr,
+        (C.c_void_p * k)(*[b.ptr for b in dy]), n, (C.c_int * k)(*outs), in_dim, scratch.ptr, None))
+    check("hip_gemm_grouped_norm_async", qh.hip_gemm_grouped_norm_async(
+        t, k, (C.c_void_p * k)(*[b.ptr for b in dw]), dx.ptr, dn.ptr, (C.c_void_p * k)(*[b.ptr for b in ey]),
+        n, (C.c_int * k)(*outs), in_dim, scratch.ptr, None))
+    check("hip_sync", qh.hip_sync())
+    xd = x.astype(np.float64)
+    xn = (xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5) * w).astype(np.float32)
+    for b, e, d, o in zip(dy, ey, datas, outs):
+        got = b.download(np.float32)[:n * o].reshape(n, o)
+        exp = e.download(np.float32)[:n * o].reshape(n, o)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), o
+        ref = oracle.gemm(t, xn, d, in_dim, o, n)
+        for r in range(n):
+            assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
+
+
 @pytest.mark.parametrize("t", [12, 14, 8, 21])
 @pytest.mark.parametrize("n", [1, 3, 16])
 def test_non_finite_x_flags_rows(qh, oracle, t, n):
