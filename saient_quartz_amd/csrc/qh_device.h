@@ -121,22 +121,22 @@ QH_DEV float qh_dot4u(const float* xv, uint32_t w, float s) {
 // (t < 16 and 0x204081 < 2^24: the full-rate 24-bit multiply is exact here.)
 QH_DEV uint32_t qh_spread4(uint32_t t) { return __umul24(t, 0x00204081u) & 0x01010101u; }
 
-// Byte-wise conditional negation: bytes whose mask byte is 0xFF are negated
-// (g must have no zero bytes where negated, true for every IQ codebook entry).
-QH_DEV uint32_t qh_negbytes(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+// Signed codebook bytes: byte j of g negated where bit j of s4 (s4 < 16) is
+// set.  0x01010100 - g negates every byte at once (exact for g with no zero
+// byte, true for every IQ codebook entry: the per-byte terms 256 - b are then
+// all in 1..255), and one v_perm picks g's byte j (selector j) or its negation
+// (j + 4).  The selector's bit 2 of byte j is bit j of s4: s4 * 0x00810204
+// puts bit j at bits j + 2, j + 9, j + 16, j + 23, disjoint ranges with no
+// carries, of which bit 8j + 2 is the one kept.  Five VALU operations per four
+// weights with the extraction of s4 (a mask built from the bits and applied by
+// xor and add took eight).
+QH_DEV uint32_t qh_signbytes(uint32_t g, uint32_t s4) {
+    const uint32_t sel = ((uint32_t)__umul24(s4, 0x00810204u) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(0x01010100u - g, g, sel);
+}
 
 // ksigns_iq2xs[i] = i | parity(i) << 7  (the closed form of KSIGNS_IQ2XS).
 QH_DEV uint32_t qh_ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
-
-// 0xFF in byte j of the result for every set bit j (j < 4) of s.
-QH_DEV uint32_t qh_signmask4(uint32_t s4) {
-    const uint32_t s = qh_spread4(s4 & 0xFu);
-    // s * 0xFF (bytes 0 or 0xFF) as a shift and a subtraction: left alone, the
-    // compiler folds them into v_mul_lo_u32, a quarter-rate instruction
-    uint32_t sh = s << 8;
-    asm volatile("" : "+v"(sh));
-    return sh - s;
-}
 
 // IQ pieces for the int8 matrix-core kernels: 16 consecutive weights of one
 // row (half hh of 32-weight sub-block K) as signed codebook bytes b[0..3], and
@@ -160,7 +160,7 @@ QH_DEV void qh_iq3s_piece(const unsigned char* r, int K, int hh, const uint32_t*
 #pragma unroll
     for (int m = 0; m < 4; m++) {
         const uint32_t idx = ((q >> (8 * m)) & 0xFFu) | (((qh >> m) & 1u) << 8);
-        b[m] = qh_negbytes(g32[idx], qh_signmask4(sg >> (4 * m)));
+        b[m] = qh_signbytes(g32[idx], (sg >> (4 * m)) & 0xFu);
     }
     sc = 1 + 2 * (int)((r[qh_iq3s_at(106 + K / 2)] >> (4 * (K & 1))) & 0xFu);
 }
@@ -177,8 +177,8 @@ QH_DEV void qh_iq2xxs_piece(const unsigned char* r, int K, int hh, const uint64_
     for (int l = 0; l < 2; l++) {
         const uint64_t g = g64[(a0 >> (8 * l)) & 0xFFu];
         const uint32_t s8 = qh_ksigns((a1 >> (7 * (2 * hh + l))) & 127u);
-        b[2 * l] = qh_negbytes((uint32_t)g, qh_signmask4(s8));
-        b[2 * l + 1] = qh_negbytes((uint32_t)(g >> 32), qh_signmask4(s8 >> 4));
+        b[2 * l] = qh_signbytes((uint32_t)g, s8 & 0xFu);
+        b[2 * l + 1] = qh_signbytes((uint32_t)(g >> 32), (s8 >> 4) & 0xFu);
     }
     sc = 2 * (int)(a1 >> 28) + 1;
 }

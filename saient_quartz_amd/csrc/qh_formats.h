@@ -357,8 +357,8 @@ struct FmtIQ4NL {
 // 8 signed codebook values (grid entry g, 8 sign bits) dotted with 8 activations.
 // Values are made unsigned by +128 (byte xor 0x80); the caller subtracts 128*sum(x).
 QH_DEV float qh_grid8(uint64_t g, uint32_t signs, const float* xv, float s) {
-    const uint32_t lo = qh_negbytes((uint32_t)g, qh_signmask4(signs)) ^ 0x80808080u;
-    const uint32_t hi = qh_negbytes((uint32_t)(g >> 32), qh_signmask4(signs >> 4)) ^ 0x80808080u;
+    const uint32_t lo = qh_signbytes((uint32_t)g, signs & 0xFu) ^ 0x80808080u;
+    const uint32_t hi = qh_signbytes((uint32_t)(g >> 32), (signs >> 4) & 0xFu) ^ 0x80808080u;
     s = qh_dot4u(xv, lo, s);
     return qh_dot4u(xv + 4, hi, s);
 }
