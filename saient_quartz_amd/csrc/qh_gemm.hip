@@ -319,7 +319,8 @@ QH_DEV QgTok qg_tokens(const QgXs& xs, int slot, int in_dim) {
     const int a = qg_uni(xs.tok_off[e]) + 16 * c;
     int n = qg_uni(xs.tok_off[e + 1]) - a;
     n = n < 0 ? 0 : (n > 16 ? 16 : n);
-    return QgTok{xs.x[0] + (size_t)a * (size_t)in_dim, xs.x2[0] ? xs.x2[0] + (size_t)a * (size_t)in_dim : nullptr, n, a};
+    const size_t off = (size_t)a * (size_t)in_dim;
+    return QgTok{xs.x[0] + off, xs.x2[0] ? xs.x2[0] + off : nullptr, n, a};
 }
 struct QgGroups {    // the matrices of one grouped launch
     const uint8_t* w[QG_MAXG];
