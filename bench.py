@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the 8B-shape decode-step leg")
     ap.add_argument("--decode-reps", type=int, default=20)
+    ap.add_argument("--only-moe", action="store_true",
+                    help="only the configs[4] MoE leg (grouped, per-expert and routed), one JSON line")
     ap.add_argument("--only-forward", action="store_true",
                     help="only run the end-to-end decode-step leg (for profiling its kernels)")
     ap.add_argument("--batched-suite", action="store_true",
@@ -66,6 +68,10 @@ def main():
 
     if args.batched_suite:
         print(json.dumps({"batched": batched_suite(torch)}), flush=True)
+        return
+
+    if args.only_moe:
+        print(json.dumps({"moe": moe_leg(torch, args.decode_reps)}), flush=True)
         return
 
     if args.only_forward:
