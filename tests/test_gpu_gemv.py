@@ -446,6 +446,52 @@ def test_gemm_group_norm_fused_images_few_tokens(qh, oracle, n):
             assert cf.rel_l2(got[r], ref[r]) < TOL, (r, cf.rel_l2(got[r], ref[r]))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("types", [(12, 12), (12, 12, 14)], ids=str)
+def test_gemm_group_norm_non_finite_token(qh, types):
+    """A token whose row holds an Inf through the fused norm images (5-16
+    tokens): every output of that token is NaN (its norm is NaN), the other
+    tokens equal the per-type call bit for bit."""
+    import ctypes as C
+    n, in_dim, outs = 8, 2048, [300, 77, 64][:len(types)]
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((n, in_dim)).astype(np.float32)
+    x[5, 700] = np.inf
+    w = (1 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    datas = [synth.weights(t, o, in_dim, seed=o + t) for t, o in zip(types, outs)]
+    dw = [GpuBuf.upload(d) for d in datas]
+    dx, dn = GpuBuf.upload_f32(x.reshape(-1)), GpuBuf.upload_f32(w)
+    dy = [GpuBuf.alloc_f32(n * o) for o in outs]
+    scratch = GpuBuf.alloc_f32(n * in_dim)
+    k = len(outs)
+    check("hip_gemm_group_norm_async", qh.hip_gemm_group_norm_async(
+        k, (C.c_uint32 * k)(*types), (C.c_void_p * k)(*[b.ptr for b in dw]), dx.ptr, dn.ptr,
+        (C.c_void_p * k)(*[b.ptr for b in dy]), n, (C.c_int * k)(*outs), in_dim, scratch.ptr, None))
+    x2 = x.copy()
+    x2[5] = 1.0  # the clean rows alone, through the per-type calls
+    dx2 = GpuBuf.upload_f32(x2.reshape(-1))
+    ey = [GpuBuf.alloc_f32(n * o) for o in outs]
+    for t in sorted(set(types)):
+        ks = [i for i, tt in enumerate(types) if tt == t]
+        m = len(ks)
+        check("hip_gemm_grouped_norm_async", qh.hip_gemm_grouped_norm_async(
+            t, m, (C.c_void_p * m)(*[dw[i].ptr for i in ks]), dx2.ptr, dn.ptr,
+            (C.c_void_p * m)(*[ey[i].ptr for i in ks]), n, (C.c_int * m)(*[outs[i] for i in ks]), in_dim,
+            scratch.ptr, None))
+    check("hip_sync", qh.hip_sync())
+    for b, e, o, t in zip(dy, ey, outs, types):
+        got = b.download(np.float32)[:n * o].reshape(n, o)
+        exp = e.download(np.float32)[:n * o].reshape(n, o)
+        assert np.isnan(got[5]).all(), (t, o)
+        for r in range(n):
+            if r == 5:
+                continue
+            if set(types) == {12, 14}:
+                assert cf.rel_l2(got[r], exp[r]) < 1e-5, (t, o, r)
+            else:
+                assert np.array_equal(got[r].view(np.uint32), exp[r].view(np.uint32)), (t, o, r)
+
+
 @pytest.mark.parametrize("t", [12, 14, 8, 21])
 @pytest.mark.parametrize("n", [1, 3, 16])
 def test_non_finite_x_flags_rows(qh, oracle, t, n):

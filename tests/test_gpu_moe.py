@@ -288,3 +288,34 @@ def test_gemm_moe_dev_rejects_other_types(qh):
     with pytest.raises(QuartzError):
         gemm_moe_dev_async(qh, 8, [w.data_ptr()], [y.data_ptr()], 1, off.data_ptr(), 1, x.data_ptr(), 256, 32,
                            torch.cuda.current_stream().cuda_stream)
+
+
+def test_moe_step_graph_replays(qh, oracle):
+    """The device-range MoE step captured once in a HIP graph: replayed three
+    times with new activations copied in between (eager work and syncs around
+    each replay), every replay equals an eager step on the same input bit for
+    bit (routing, token ranges and expert GEMMs all read on the device)."""
+    types, E, k, n, d, f = (12, 12, 14), 8, 2, 24, 512, 768
+    host, deq, rw = moe_case(oracle, types, E, d, f, seed=5)
+    step = MoeStep(types, dev(host["g"]), dev(host["u"]), dev(host["d"]), dev(rw), E, k, d, f, n_max=n)
+    assert step.device_driven
+    rng = np.random.default_rng(11)
+    X = torch.empty(n, d, device="cuda")
+    out = torch.empty(n, d, device="cuda")
+    X.copy_(dev(rng.standard_normal((n, d)).astype(np.float32)))
+    step.issue(X, out, n)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step.issue(X, out, n)
+    for rep in range(3):
+        xs = dev((rng.standard_normal((n, d)) * (1 + rep)).astype(np.float32))
+        X.copy_(xs)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = torch.full((n, d), np.nan, device="cuda")
+        step.issue(X, ref, n)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), rep
