@@ -286,7 +286,7 @@ struct XImg {
 struct QgXs {        // the distinct token blocks of one grouped launch
     const float* x[QG_MAXG];
     const float* x2[QG_MAXG];  // SwiGLU: x is silu(x) * x2 (gate, up) when non-null
-    int n[QG_MAXG];  // tokens (<= 16)
+    int n[QG_MAXG];  // tokens (<= 16 halves)
     const unsigned char* img;  // their x images: slot s, group g at (s ngroups + g) XImg::BYTES
     uint32_t img_bytes;
     // Token ranges on the device (expert layers): when tok_off is set, slot s is
@@ -294,8 +294,12 @@ struct QgXs {        // the distinct token blocks of one grouped launch
     // min(+16, tok_off[e + 1]) of the gathered x[0] (and x2[0]); n[] is unused.
     const int* tok_off;
     int moe_c;
+    // 16-token halves per token block (2: 32-token launches); a device-range
+    // chunk then holds 32 tokens, and qg_ximage writes both halves' images
+    // next to each other ((slot ngroups + g) halves + h)
+    int halves;
 };
-// The tokens of slot s: x (and x2) of its first token, their count (<= 16)
+// The tokens of slot s: x (and x2) of its first token, their count (<= 16 halves)
 // and the index a of the first one in the gathered rows (0 for host slots).
 struct QgTok {
     const float* x;
@@ -316,9 +320,10 @@ QH_DEV int qg_uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 QH_DEV QgTok qg_tokens(const QgXs& xs, int slot, int in_dim) {
     if (!xs.tok_off) return QgTok{qg_uni(xs.x[slot]), qg_uni(xs.x2[slot]), qg_uni(xs.n[slot]), 0};
     const int e = slot / xs.moe_c, c = slot - e * xs.moe_c;
-    const int a = qg_uni(xs.tok_off[e]) + 16 * c;
+    const int ct = 16 * xs.halves;  // tokens per chunk
+    const int a = qg_uni(xs.tok_off[e]) + ct * c;
     int n = qg_uni(xs.tok_off[e + 1]) - a;
-    n = n < 0 ? 0 : (n > 16 ? 16 : n);
+    n = n < 0 ? 0 : (n > ct ? ct : n);
     const size_t off = (size_t)a * (size_t)in_dim;
     return QgTok{xs.x[0] + off, xs.x2[0] ? xs.x2[0] + off : nullptr, n, a};
 }
@@ -449,22 +454,26 @@ QH_DEV void qg_chunk(const qh_u32x4* xr, const qh_u32x4* ur, bool swiglu, float*
 }
 
 __global__ __launch_bounds__(512) void qg_ximage(const QgXs xs, unsigned char* __restrict__ img, int in_dim) {
-    const int g = blockIdx.x, slot = blockIdx.y, ngroups = in_dim >> 8;
+    // blockIdx.y = slot * halves + half h: tokens 16 h .. of the slot
+    const int g = blockIdx.x, half = (int)blockIdx.y % xs.halves, slot = (int)blockIdx.y / xs.halves;
+    const int ngroups = in_dim >> 8;
     const int lane = threadIdx.x & 63, xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
     const QgTok tk = qg_tokens(xs, slot, in_dim);
-    const int n = tk.n;
+    int n = tk.n - 16 * half;
+    n = n > 16 ? 16 : n;
     if (xt >= n) return;  // whole half-wavefronts: the reductions stay within live lanes
+    const size_t t0 = (size_t)(16 * half) * (size_t)in_dim;
     const uint32_t off = 4u * ((uint32_t)xt * (uint32_t)in_dim + 256u * (uint32_t)g + 8u * (uint32_t)xc);
-    const QhBuf xb = qh_buf(tk.x, 4u * (uint32_t)n * (uint32_t)in_dim);
+    const QhBuf xb = qh_buf(tk.x + t0, 4u * (uint32_t)n * (uint32_t)in_dim);
     qh_u32x4 xr[2] = {qh_ld128(xb, off), qh_ld128(xb, off + 16u)}, ur[2] = {};
     if (tk.x2) {
-        const QhBuf ub = qh_buf(tk.x2, 4u * (uint32_t)n * (uint32_t)in_dim);
+        const QhBuf ub = qh_buf(tk.x2 + t0, 4u * (uint32_t)n * (uint32_t)in_dim);
         ur[0] = qh_ld128(ub, off);
         ur[1] = qh_ld128(ub, off + 16u);
     }
     float v[8];
     qg_chunk(xr, ur, tk.x2 != nullptr, v);
-    qg_digitise(v, true, lane, xt, xc, img + ((size_t)slot * ngroups + g) * XImg::BYTES);
+    qg_digitise(v, true, lane, xt, xc, img + (((size_t)slot * ngroups + g) * xs.halves + half) * XImg::BYTES);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -484,7 +493,8 @@ QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<con
 // the end).
 template <class F, int NT, int W, int MODE>
 constexpr int qh_mmq_lds() {
-    return (MODE != 0 ? QG_GMAX : 2) * XImg::BYTES + W * (32 * F::RS + 16) + (F::GRID ? IQT_BYTES : 0);
+    return (MODE != 0 ? QG_GMAX : 2) * (NT > 16 ? 2 : 1) * XImg::BYTES + W * (32 * F::RS + 16) +
+           (F::GRID ? IQT_BYTES : 0);
 }
 
 // The kernel body for workgroup lb of matrix gi (a launch may run two formats'
@@ -499,12 +509,16 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     constexpr int CH = F::CH, RS = F::RS;
     constexpr int NH = (32 * CH + 63) / 64;  // 16-byte weight loads per lane per group
     constexpr int TILE = 32 * RS + 16;
-    static_assert(NT == 4 || NT == 8 || NT == 16, "NT");
+    static_assert(NT == 4 || NT == 8 || NT == 16 || NT == 32, "NT");
     using XI = XImg;
-    constexpr int NQ = NT / 4;                 // slot quads (tokens 4q .. 4q + 3)
+    // 32 tokens: two 16-token halves, each its own image and MFMA accumulator
+    // against the same converted weights (streamed images only)
+    constexpr int NTH = NT > 16 ? 2 : 1;
+    static_assert(NTH == 1 || MODE == 0, "32-token launches stream their images");
+    constexpr int NQ = (NT > 16 ? 16 : NT) / 4;  // slot quads per half (tokens 16h + 4q .. + 3)
     constexpr int TPW = 1;                     // 32-row tiles per wavefront
     constexpr int GRIDB = F::GRID ? IQT_BYTES : 0;  // IQ codebook and sign tables
-    constexpr int IMB = XI::BYTES;
+    constexpr int IMB = NTH * XI::BYTES;  // a group's images (both halves, adjacent)
     constexpr bool RES = MODE != 0;
     constexpr int NSLOT = RES ? QG_GMAX : 2;  // image slots in LDS
     static_assert(qh_mmq_lds<F, NT, W, MODE>() == NSLOT * IMB + W * TILE + GRIDB, "LDS layout");
@@ -584,15 +598,15 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     //   MODE 0: one group at a time through a slot pair, loaded with the
     //     weights one iteration ahead; one workgroup barrier per group orders
     //     the pair.
-    constexpr int NCH = XI::BYTES / 16;
+    constexpr int NCH = IMB / 16;
     constexpr int XP = (NCH + 64 * W - 1) / (64 * W);
     const QhBuf xb = qh_buf(xs.img, xs.img_bytes);
-    const uint32_t ibase = (uint32_t)slot * (uint32_t)ngroups * (uint32_t)XI::BYTES + 16u * threadIdx.x;
+    const uint32_t ibase = (uint32_t)slot * (uint32_t)ngroups * (uint32_t)IMB + 16u * threadIdx.x;
     auto load_x = [&](int i, qh_u32x4* xr) {  // item i: group grp(i)
 #pragma unroll
         for (int p = 0; p < XP; p++) {
             const int id = threadIdx.x + 64 * W * p;
-            xr[p] = qh_ld128(xb, (id < NCH && i < nk) ? ibase + (uint32_t)XI::BYTES * (uint32_t)grp(i) + 1024u * W * p
+            xr[p] = qh_ld128(xb, (id < NCH && i < nk) ? ibase + (uint32_t)IMB * (uint32_t)grp(i) + 1024u * W * p
                                                        : 0x80000000u);
         }
     };
@@ -660,24 +674,32 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 
     // Result slots of this lane: slot (q, r) of tile tt is token t = 4q + 2hh + r
     // of the tile's row R.
-    float tot[TPW][2 * NQ];
+    // Result slot h 2NQ + 2q + r of tile tt is token 16h + 4q + 2hh + r.
+    float tot[TPW][NTH * 2 * NQ];
 #pragma unroll
     for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-        for (int i = 0; i < 2 * NQ; i++) tot[tt][i] = 0.f;
+        for (int i = 0; i < NTH * 2 * NQ; i++) tot[tt][i] = 0.f;
     const unsigned char* wrow = wl + R * RS;
     // compact index of this lane's row in the sums (rows rho(t))
     const int cidx = 4 * (R >> 3) + 2 * ((R >> 2) & 1) + (R & 1) + 16 * hh;
 
     auto compute = [&](const unsigned char* im, float* tot) {
         const typename F::H hd = F::hdr(wrow);
-        qh_f32x16 c0 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        qh_f32x16 dm = c0;
+        qh_f32x16 c[NTH], dm[NTH];
+#pragma unroll
+        for (int h = 0; h < NTH; h++) {
+            c[h] = qh_f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            dm[h] = c[h];
+        }
         auto kb = [&](auto JC) {
             constexpr int J = decltype(JC)::value;
             const qh_f16x8 b = F::template bop<J>(wrow, hh, hd, gridl);
-            const qh_f16x8 a = __builtin_bit_cast(qh_f16x8, qh_lds128(im + 1024 * J + 16 * lane));
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+#pragma unroll
+            for (int h = 0; h < NTH; h++) {
+                const qh_f16x8 a = __builtin_bit_cast(qh_f16x8, qh_lds128(im + h * XI::BYTES + 1024 * J + 16 * lane));
+                c[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[h], 0, 0, 0);
+            }
         };
         kb(std::integral_constant<int, 0>{});
         kb(std::integral_constant<int, 1>{});
@@ -696,24 +718,33 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
         kb(std::integral_constant<int, 14>{});
         kb(std::integral_constant<int, 15>{});
         if constexpr (F::SUMS) {
-            const qh_f16x8 sv = __builtin_bit_cast(qh_f16x8, qh_lds128(im + XI::SUM + 16 * cidx));
-            dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, F::minh(hd, hh), dm, 0, 0, 0);
-        }
-        // finish: slot (q, r) = token 4q + 2hh + r (rows 2t, 2t + 1: registers
-        // 4q + 2r, 4q + 2r + 1), its 2^-s at float 8 hh + 2q + r of the image
-        const qh_u32x4 rs0 = qh_lds128(im + XI::RSF + 32 * hh), rs1 = qh_lds128(im + XI::RSF + 32 * hh + 16);
-        const uint32_t rsw[8] = {rs0.x, rs0.y, rs0.z, rs0.w, rs1.x, rs1.y, rs1.z, rs1.w};
+            const qh_f16x8 mb = F::minh(hd, hh);
 #pragma unroll
-        for (int q = 0; q < NQ; q++)
-#pragma unroll
-            for (int r = 0; r < 2; r++) {
-                const float rs = __uint_as_float(rsw[2 * q + r]);
-                const float P = c0[4 * q + 2 * r] + c0[4 * q + 2 * r + 1];
-                if constexpr (F::SUMS)
-                    tot[2 * q + r] += (hd.d * P - hd.dm * 32.0f * dm[4 * q + r]) * rs;
-                else
-                    tot[2 * q + r] += hd.d * P * rs;
+            for (int h = 0; h < NTH; h++) {
+                const qh_f16x8 sv = __builtin_bit_cast(qh_f16x8, qh_lds128(im + h * XI::BYTES + XI::SUM + 16 * cidx));
+                dm[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, mb, dm[h], 0, 0, 0);
             }
+        }
+        // finish: slot (q, r) = token 4q + 2hh + r of the half (rows 2t, 2t + 1:
+        // registers 4q + 2r, 4q + 2r + 1), its 2^-s at float 8 hh + 2q + r of
+        // the half's image
+#pragma unroll
+        for (int h = 0; h < NTH; h++) {
+            const unsigned char* ih = im + h * XI::BYTES;
+            const qh_u32x4 rs0 = qh_lds128(ih + XI::RSF + 32 * hh), rs1 = qh_lds128(ih + XI::RSF + 32 * hh + 16);
+            const uint32_t rsw[8] = {rs0.x, rs0.y, rs0.z, rs0.w, rs1.x, rs1.y, rs1.z, rs1.w};
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const float rs = __uint_as_float(rsw[2 * q + r]);
+                    const float P = c[h][4 * q + 2 * r] + c[h][4 * q + 2 * r + 1];
+                    if constexpr (F::SUMS)
+                        tot[h * 2 * NQ + 2 * q + r] += (hd.d * P - hd.dm * 32.0f * dm[h][4 * q + r]) * rs;
+                    else
+                        tot[h * 2 * NQ + 2 * q + r] += hd.d * P * rs;
+                }
+        }
     };
 
     // Item i in register set i % QG_NBUF, refilled with item i + QG_NBUF as
@@ -747,7 +778,10 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
         item(1, i0 + 1);
     }
     if (i0 < nk) item(0, i0);
-    // Results: this wavefront's 32 rows x NT tokens.
+    // Results: this wavefront's 32 rows x NT tokens; slot i of a tile holds
+    // token stok(i) (half i / 2NQ, quad (i % 2NQ) / 2, r = i % 2).
+    constexpr int NSL = NTH * 2 * NQ;  // result slots per lane and tile
+    auto stok = [&](int i) { return 16 * (i / (2 * NQ)) + 4 * ((i % (2 * NQ)) >> 1) + 2 * hh + (i & 1); };
     auto put = [&](int t, int row, float a) {
         if (t < n && row < out_dim) {
             float* yp = y + (size_t)t * ldy + row;
@@ -758,9 +792,7 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 #pragma unroll
         for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-            for (int q = 0; q < NQ; q++)
-#pragma unroll
-                for (int r = 0; r < 2; r++) put(4 * q + 2 * hh + r, (tile0 + tt) * 32 + R, tot[tt][2 * q + r]);
+            for (int i = 0; i < NSL; i++) put(stok(i), (tile0 + tt) * 32 + R, tot[tt][i]);
         return;
     }
     // Split K: each wavefront stores its partial (NT tokens x 32 rows), and the
@@ -774,13 +806,9 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 #pragma unroll
     for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-        for (int q = 0; q < NQ; q++)
-#pragma unroll
-            for (int r = 0; r < 2; r++) {
-                const int t = 4 * q + 2 * hh + r;
-                __hip_atomic_store(mine + (tt * NT + t) * 32 + R, tot[tt][2 * q + r], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
+        for (int i = 0; i < NSL; i++)
+            __hip_atomic_store(mine + (tt * NT + stok(i)) * 32 + R, tot[tt][i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     // Agent-scope stores and loads of the partials reach the device's point of
     // coherence without writing back or invalidating whole L2s (which a
     // release/acquire fence would, at a cost measured in tens of microseconds
@@ -797,7 +825,7 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     // flight at once, summed in split order.
     const QhBuf pbuf = qh_buf(part, 4u * QG_PART_FLOATS);
     const uint32_t bbase = 4u * (uint32_t)(wslot * splits * PW);
-    constexpr int NS = TPW * 2 * NQ;  // result slots per lane
+    constexpr int NS = TPW * NSL;  // result slots per lane
     float a[NS];
 #pragma unroll
     for (int i = 0; i < NS; i++) a[i] = 0.f;
@@ -806,17 +834,14 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 #pragma unroll
         for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-            for (int q = 0; q < NQ; q++)
+            for (int i = 0; i < NSL; i++)
 #pragma unroll
-                for (int r = 0; r < 2; r++)
-#pragma unroll
-                    for (int uu = 0; uu < 4; uu++) {
-                        const int t = 4 * q + 2 * hh + r;
-                        const uint32_t off = k0 + uu < splits
-                                                 ? bbase + 4u * (uint32_t)((k0 + uu) * PW + (tt * NT + t) * 32 + R)
-                                                 : 0x80000000u;
-                        v[(tt * NQ + q) * 2 + r][uu] = __builtin_amdgcn_raw_buffer_load_b32(pbuf.rs, (int)off, 0, 16);
-                    }
+                for (int uu = 0; uu < 4; uu++) {
+                    const uint32_t off = k0 + uu < splits
+                                             ? bbase + 4u * (uint32_t)((k0 + uu) * PW + (tt * NT + stok(i)) * 32 + R)
+                                             : 0x80000000u;
+                    v[tt * NSL + i][uu] = __builtin_amdgcn_raw_buffer_load_b32(pbuf.rs, (int)off, 0, 16);
+                }
 #pragma unroll
         for (int i = 0; i < NS; i++)
 #pragma unroll
@@ -826,10 +851,7 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 #pragma unroll
     for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-        for (int q = 0; q < NQ; q++)
-#pragma unroll
-            for (int r = 0; r < 2; r++)
-                put(4 * q + 2 * hh + r, (tile0 + tt) * 32 + R, a[(tt * NQ + q) * 2 + r]);
+        for (int i = 0; i < NSL; i++) put(stok(i), (tile0 + tt) * 32 + R, a[tt * NSL + i]);
     if (lane == 0) __hip_atomic_store(&cnt[wslot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
@@ -919,10 +941,13 @@ static void launch_mmq_nt(int nt, int mode, const QgGroups& gs, const QgXs& xs, 
                           const QgScratch& sc, uint32_t row_bytes, int in_dim, hipStream_t st) {
     if (nt <= 4) launch_mmq_t<F, 4>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
     else if (nt <= 8) launch_mmq_t<F, 8>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
-    else launch_mmq_t<F, 16>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
+    else if (nt <= 16) launch_mmq_t<F, 16>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
+    else  // 17-32 tokens: streamed images only (the caller forces mode 0)
+        hipLaunchKernelGGL((qh_mmq<F, 32, QG_WAVES, 0>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
+                           splits, sc.part, sc.cnt);
 }
 
-struct QgEntry {  // one matrix (or row chunk of one) and its <= 16 tokens
+struct QgEntry {  // one matrix (or row chunk of one) and its <= 32 tokens
     const uint8_t* w;
     const float* x;
     const float* x2;  // SwiGLU up (x is the gate), or null
@@ -966,6 +991,7 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
                          const QgScratch& sc, hipStream_t st, int accum, bool img_ready = false) {
     const int ngroups = in_dim / 256;
     QgXs xs = {};
+    xs.halves = 1;
     QgGroups gs = {};
     int nslots = 0, ntmax = 0;
     for (int i = 0; i < cnt; i++) {
@@ -1011,10 +1037,17 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         if (nslots != 1) return hipErrorNotSupported;
         mode = res ? 1 : 0;
     }
-    const int64_t pb = (int64_t)(brows / 32) * 16 * 32;  // floats of one partial block (16-token bound)
+    // 17-32 tokens per block: two image halves per group, streamed (the
+    // resident modes would need twice the LDS)
+    const int halves = ntmax > 16 ? 2 : 1;
+    if (halves == 2) {
+        if (img_ready) return hipErrorNotSupported;
+        mode = 0;
+    }
+    const int64_t pb = (int64_t)(brows / 32) * 16 * halves * 32;  // floats of one partial block (token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
-    const bool img_fits = (int64_t)nslots * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES;
+    const bool img_fits = (int64_t)nslots * halves * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES;
     if (!img_fits || (splits > 1 && ((int64_t)blocks * splits * pb > QG_PART_FLOATS || blocks > QG_PART_TILES))) {
         if (cnt > 1) {
             hipError_t e = qg_run(type, en, cnt / 2, in_dim, row_bytes, sc, st, accum, img_ready);
@@ -1043,9 +1076,11 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     const dim3 grid((unsigned)maxw, (unsigned)cnt);
     // the token blocks' x images, once per launch
     xs.img = sc.img;
-    xs.img_bytes = (uint32_t)(nslots * ngroups * XImg::BYTES);
+    xs.halves = halves;
+    xs.img_bytes = (uint32_t)(nslots * halves * ngroups * XImg::BYTES);
     if (mode != 2 && !img_ready)
-        hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)nslots), dim3(512), 0, st, xs, sc.img, in_dim);
+        hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)(nslots * halves)), dim3(512), 0, st, xs, sc.img,
+                           in_dim);
     switch (type) {
         case QT_Q4_K: launch_mmq_nt<GQ4K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
         case QT_Q5_K: launch_mmq_nt<GQ5K>(ntmax, mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st); break;
@@ -1102,8 +1137,9 @@ hipError_t qh_launch_mmq_grouped(uint32_t type, int count, const uint8_t* const*
     const float* last_x = nullptr;
     for (int i = 0; i < count; i++) {
         if (out_dims[i] <= 0) continue;
-        for (int t0 = 0; t0 < n[i]; t0 += 16) {
-            const int nt = n[i] - t0 < 16 ? n[i] - t0 : 16;
+        for (int t0 = 0; t0 < n[i]; t0 += 32) {
+            // blocks of up to 32 tokens (17-32: one weight pass on two halves)
+            const int nt = n[i] - t0 < 32 ? n[i] - t0 : 32;
             const float* xs = X[i] + (size_t)t0 * in_dim;
             const float* xs2 = X2 && X2[i] ? X2[i] + (size_t)t0 * in_dim : nullptr;
             for (int64_t r0 = 0; r0 < out_dims[i]; r0 += max_rows) {
@@ -1220,6 +1256,7 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     const int64_t pw = (int64_t)QG_WAVES * 16 * 32;  // floats of one workgroup's partials (16-token bound)
     if ((int64_t)wgs * pw > QG_PART_FLOATS || b1 + b2 > QG_PART_TILES) return hipErrorNotSupported;
     QgXs xs = {};
+    xs.halves = 1;
     xs.x[0] = x;
     xs.n[0] = n;
     // nw: x's rows RMS-normalised with nw and digitised by qg_norm_image into
@@ -1288,8 +1325,11 @@ hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* 
     if ((int64_t)out_dim * row_bytes >= ((int64_t)1 << 31) - 4096) return hipErrorNotSupported;
     const size_t slice = (size_t)row_bytes * (size_t)out_dim;
     const int ngroups = in_dim / 256, brows = 32 * QG_WAVES, blocks = (out_dim + brows - 1) / brows;
-    const int C = (max_tokens + 15) / 16;
-    const int pw = QG_WAVES * 16 * 32;  // floats of one workgroup's partials (16-token bound)
+    // experts of more than 16 tokens: 32-token chunks on two image halves (one
+    // weight pass for up to 32 tokens), streamed images
+    const int halves = max_tokens > 16 ? 2 : 1;
+    const int C = (max_tokens + 16 * halves - 1) / (16 * halves);
+    const int pw = QG_WAVES * 16 * halves * 32;  // floats of one workgroup's partials (token bound)
     for (int e0 = 0; e0 < n_exp;) {
         // experts of this launch: bounded by the entries, the partials and the images
         int ne = n_exp - e0 < QG_MAXG / sets ? n_exp - e0 : QG_MAXG / sets;
@@ -1302,18 +1342,20 @@ hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* 
             splits = splits < ngroups ? splits : ngroups;
             const bool res = (ngroups + splits - 1) / splits <= QG_GMAX;
             mode = res ? (bl <= QG_DIG_BLOCKS * ne ? 2 : 1) : 0;
+            if (halves == 2) mode = 0;
             const int64_t wgs = (int64_t)sets * ne * C * blocks * splits;
             const bool fits = wgs * pw <= QG_PART_FLOATS && (int64_t)sets * ne * C * blocks <= QG_PART_TILES &&
-                              (mode == 2 || (int64_t)ne * C * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES);
+                              (mode == 2 || (int64_t)ne * C * halves * ngroups * XImg::BYTES <= (int64_t)QG_IMG_BYTES);
             if (fits) break;
         }
         QgXs xs = {};
+        xs.halves = halves;
         xs.x[0] = X;
         xs.x2[0] = X2;
         xs.tok_off = tok_off + e0;
         xs.moe_c = C;
         xs.img = sc->img;
-        xs.img_bytes = (uint32_t)((int64_t)ne * C * ngroups * XImg::BYTES);
+        xs.img_bytes = (uint32_t)((int64_t)ne * C * halves * ngroups * XImg::BYTES);
         QgGroups gs = {};
         int wgs = 0;
         const int per = C * blocks * splits;  // workgroups of each (set, expert)
@@ -1332,14 +1374,14 @@ hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* 
         gs.accum = accum;
         const dim3 grid((unsigned)per, (unsigned)(sets * ne));
         if (mode != 2)
-            hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)(ne * C)), dim3(512), 0, st, xs, sc->img,
-                               in_dim);
+            hipLaunchKernelGGL(qg_ximage, dim3((unsigned)ngroups, (unsigned)(ne * C * halves)), dim3(512), 0, st, xs,
+                               sc->img, in_dim);
         switch (type) {
-            case QT_Q4_K: launch_mmq_nt<GQ4K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_Q5_K: launch_mmq_nt<GQ5K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_IQ3_S: launch_mmq_nt<GIQ3S>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
-            case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
-            default: launch_mmq_nt<GQ6K>(16, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_Q4_K: launch_mmq_nt<GQ4K>(16 * halves, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_Q5_K: launch_mmq_nt<GQ5K>(16 * halves, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ3_S: launch_mmq_nt<GIQ3S>(16 * halves, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            case QT_IQ2_XXS: launch_mmq_nt<GIQ2XXS>(16 * halves, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
+            default: launch_mmq_nt<GQ6K>(16 * halves, mode, gs, xs, grid, splits, *sc, row_bytes, in_dim, st); break;
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

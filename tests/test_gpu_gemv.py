@@ -177,7 +177,8 @@ def test_gemm_vs_oracle(qh, oracle, t, n):
 # blocks sharing x, one split of 4 groups: images from the prologue launch,
 # resident) and 9000 x 16384 (7 splits of 9-10 groups: images streamed).
 MMQ_CASES = [(40, 4096, 2), (40, 4096, 3), (77, 4096, 5), (300, 14336, 8), (100, 4096, 11), (130, 2048, 16),
-             (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4), (40000, 1024, 16), (9000, 16384, 16)]
+             (64, 4096, 17), (33, 1024, 33), (9000, 256, 16), (4100, 512, 4), (40000, 1024, 16), (9000, 16384, 16),
+             (300, 4096, 24), (9000, 1024, 32), (130, 2048, 40), (64, 14336, 20)]
 
 
 @pytest.mark.parametrize("t", [12, 13, 14, 21, 16])
@@ -252,7 +253,7 @@ def test_mem_info(qh):
 
 
 @pytest.mark.parametrize("t", [12, 14, 13, 8])
-@pytest.mark.parametrize("n", [1, 4, 16])
+@pytest.mark.parametrize("n", [1, 4, 16, 27])
 @pytest.mark.parametrize("swiglu, acc", [(True, True), (True, False), (False, True)])
 def test_gemm_grouped_ex(qh, oracle, t, n, swiglu, acc):
     """hip_gemm_grouped_ex: y (+)= W (silu(gate) * up) or W x for n tokens, two

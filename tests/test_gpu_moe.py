@@ -237,13 +237,15 @@ def test_moe_step_vs_oracle(qh, oracle, types, E, k, n, renorm, extras, driven):
 
 @pytest.mark.parametrize("t", [12, 13, 14, 21, 16])
 @pytest.mark.parametrize("sets, swiglu, acc", [(1, False, False), (2, False, True), (1, True, False)])
-def test_gemm_moe_dev_vs_oracle(qh, oracle, t, sets, swiglu, acc):
-    """Device-held token ranges: empty experts, one token, and more than 16 tokens
-    (several 16-token chunks of one expert) against the oracle per expert."""
+@pytest.mark.parametrize("counts", [[0, 1, 37, 0, 16, 5], [3, 0, 16, 9, 0, 2], [20, 0, 18, 1, 32, 0]],
+                         ids=["upto37", "upto16", "upto32"])
+def test_gemm_moe_dev_vs_oracle(qh, oracle, t, sets, swiglu, acc, counts):
+    """Device-held token ranges: empty experts, one token, 16 tokens, 17-32
+    tokens (one chunk over two 16-token image halves) and 37 (two 32-token
+    chunks) against the oracle per expert."""
     from saient_quartz_amd import type_size
     from saient_quartz_amd.host import gemm_moe_dev_async
     E, in_dim, out_dim = 6, 512, 320
-    counts = [0, 1, 37, 0, 16, 5]
     off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     S = int(off[-1])
     rng = np.random.default_rng(t + 10 * sets)
