@@ -1,4 +1,4 @@
-// qh_gemm.hip -- batched dequant-GEMM for n = 2..16 tokens on the f16 matrix
+// qh_gemm.hip -- batched dequant-GEMM for n = 2..32 tokens per weight pass on the f16 matrix
 // cores (v_mfma_f32_32x32x16_f16), Q4_K / Q5_K / Q6_K / IQ3_S / IQ2_XXS.
 //
 // Y[t][j] = sum_k W[j,k] X[t][k], X and Y token-major.  One pass over the weights

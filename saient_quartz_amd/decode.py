@@ -425,7 +425,7 @@ class BatchStep:
     """forward_gpu_step for n sequences decoding in lockstep (token batch N of
     BatchConfig configs[3]): every sequence has its own token, hidden state and
     K/V cache, all at the same position.  The weight products are batched GEMMs
-    (hip_gemm_grouped: one weight pass per 16 tokens on the matrix cores; q/k
+    (hip_gemm_grouped: one weight pass per 32 tokens on the matrix cores; q/k
     share one launch, v another, since they differ in type); the residual adds
     and the SwiGLU before the down projection are fused into the GEMMs
     (hip_gemm_grouped_ex); the norms and the attention are one launch each for
