@@ -173,7 +173,8 @@ BATCH_CASES = {
 
 @pytest.mark.parametrize("n, case", [(3, "llama_q4km_1layer"), (16, "llama_q4km_1layer"), (16, "llama_q4km_2layers"),
                                      (8, "llama_q4km_2layers"), (4, "sym_2layers"),
-                                     (16, "sym_2layers"), (2, "q5_0"),
+                                     (16, "sym_2layers"), (24, "llama_q4km_2layers"), (32, "sym_2layers"),
+                                     (2, "q5_0"),
                                      (2, "q2_k_fallback")])
 def test_batch_step_matches_oracle(qh, oracle, n, case):
     """BatchStep (n sequences in lockstep: batched GEMMs, batched norm and
