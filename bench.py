@@ -269,15 +269,15 @@ def forward_leg(torch, reps, wbytes):
       N = 1: ForwardStep (embedding lookup, 32 x [fused norm + q/k/v, RoPE + KV
              append + attention, o + residual, fused norm + gate/up + SwiGLU,
              down + residual], fused final norm + head; 5 launches per layer);
-      N = 4, 16: BatchStep, N sequences in lockstep with their own K/V caches
-             (batched matrix-core GEMMs, one weight pass per 16 tokens, and
-             batched glue)."""
+      N = 4, 16, 32: BatchStep, N sequences in lockstep with their own K/V
+             caches (batched matrix-core GEMMs, one weight pass per 16 tokens,
+             or per 32 on two image halves, and batched glue)."""
     from saient_quartz_amd.decode import BatchStep, ForwardStep, ModelConfig
 
     cfg = ModelConfig(max_seq=1024)
     weights = ForwardStep.random_weights(cfg)
     out = {}
-    for n in (1, 4, 16):
+    for n in (1, 4, 16, 32):
         step = ForwardStep(cfg, weights) if n == 1 else BatchStep(cfg, weights, n)
         tokens = [(7 * i + 3) % 1000 for i in range(n)]
         issue = (lambda pos: step.issue(tokens[0], pos)) if n == 1 else (lambda pos: step.issue(tokens, pos))

@@ -454,17 +454,23 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
     int64_t wb1 = 0;
     for (int k = 0; k < count; k++)
         wb1 += (int64_t)qh_type_size(types[k], (size_t)in_dim) * (out_dims[k] > 0 ? out_dims[k] : 0);
-    if (n >= 3 && n <= 16 && (n >= 5 || wb1 > ((int64_t)16 << 20)) && nut == 1 && !qh_force_valu()) {
+    // 17-32 tokens (one 32-token pass, two image halves) of any number of
+    // types: the norm fused into the images once, then one launch per type
+    // on them
+    int u0 = 0;
+    if (n >= 3 && n <= 32 && (n >= 5 || wb1 > ((int64_t)16 << 20)) && (nut == 1 || n > 16) && !qh_force_valu()) {
         bool ok = true;
         for (int k = 0; k < count; k++)
             ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
-        if (ok) {
-            hipError_t e = qh_launch_mmq_norm(ut[0], cnt[0], wu[0], yu[0], ou[0], x, norm_w, n, in_dim, st);
-            if (e == hipSuccess) return QH_OK;
-            if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
+        for (; ok && u0 < nut; u0++) {
+            hipError_t e =
+                qh_launch_mmq_norm(ut[u0], cnt[u0], wu[u0], yu[u0], ou[u0], x, norm_w, n, in_dim, st, u0 > 0);
+            if (e == hipErrorNotSupported) break;  // this type and the rest: the per-type calls
+            if (e != hipSuccess) return qh_fail(e, "hip_gemm_group_norm");
         }
+        if (u0 == nut) return QH_OK;
     }
-    for (int u = 0; u < nut; u++) {
+    for (int u = u0; u < nut; u++) {
         int rc = hip_gemm_grouped_norm_async(ut[u], cnt[u], wu[u], x, norm_w, yu[u], n, ou[u], in_dim, scratch, stream);
         if (rc) return rc;
     }

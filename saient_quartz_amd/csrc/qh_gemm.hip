@@ -1038,12 +1038,10 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         mode = res ? 1 : 0;
     }
     // 17-32 tokens per block: two image halves per group, streamed (the
-    // resident modes would need twice the LDS)
+    // resident modes would need twice the LDS); ready images are then the
+    // two-half layout qg_norm_image writes past 16 tokens
     const int halves = ntmax > 16 ? 2 : 1;
-    if (halves == 2) {
-        if (img_ready) return hipErrorNotSupported;
-        mode = 0;
-    }
+    if (halves == 2) mode = 0;
     const int64_t pb = (int64_t)(brows / 32) * 16 * halves * 32;  // floats of one partial block (token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
@@ -1173,8 +1171,8 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 }
 
 hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W, float* const* Y, const int* out_dims,
-                              const float* x, const float* nw, int n, int in_dim, hipStream_t st) {
-    if (n < 2 || n > 16 || count < 1 || count > QG_MAXG || in_dim % 256 || in_dim > 4096 || !nw)
+                              const float* x, const float* nw, int n, int in_dim, hipStream_t st, bool img_done) {
+    if (n < 2 || n > 32 || count < 1 || count > QG_MAXG || in_dim % 256 || in_dim > 4096 || !nw)
         return hipErrorNotSupported;
     if (type != QT_Q4_K && type != QT_Q5_K && type != QT_Q6_K && type != QT_IQ3_S && type != QT_IQ2_XXS)
         return hipErrorNotSupported;
@@ -1189,8 +1187,10 @@ hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W,
         en[cnt++] = QgEntry{W[i], x, nullptr, Y[i], n, out_dims[i], out_dims[i]};
     }
     if (cnt == 0) return hipSuccess;
-    hipError_t e = qh_glue_norm_image(sc->img, x, nw, n, in_dim, st);
-    if (e != hipSuccess) return e;
+    if (!img_done) {
+        hipError_t e = qh_glue_norm_image(sc->img, x, nw, n, in_dim, st);
+        if (e != hipSuccess) return e;
+    }
     return qg_run(type, en, cnt, in_dim, row_bytes, *sc, st, 0, true);
 }
 

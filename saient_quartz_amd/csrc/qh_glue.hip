@@ -93,14 +93,15 @@ __global__ __launch_bounds__(1024) void qg_rms_norm(float* out, const float* x, 
 }
 
 // RMS norm of each token's row fused with the batched GEMM's x images: token
-// t = blockIdx.x of a token-major batch (<= 16 tokens) is normalised exactly as
+// t = blockIdx.x of a token-major batch (<= 32 tokens; 17-32 on two image
+// halves, token t in half t / 16) is normalised exactly as
 // qg_rms_norm's one-float4-per-thread path computes it (the same per-thread
 // sums, block sum and products), and digitised straight into image slot 0
 // (qg_digitise: one half-wavefront per 256-element group), so the GEMM reads
 // the images (no normalised rows in memory, no image launch of its own).
 // n % 256 == 0, n <= 4 blockDim.x, 16-byte aligned x and w.
 __global__ __launch_bounds__(1024) void qg_norm_image(unsigned char* __restrict__ img, const float* x,
-                                                      const float* w, int n) {
+                                                      const float* w, int n, int halves) {
     __shared__ float sm[16];
     const int t = blockIdx.x;
     x += (size_t)t * n;
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(1024) void qg_norm_image(unsigned char* __restrict_
             v[6] = b.z * r * wb.z;
             v[7] = b.w * r * wb.w;
         }
-        qg_digitise(v, on, lane, t, xc, img + (size_t)(on ? g : 0) * XImg::BYTES);
+        qg_digitise(v, on, lane, t & 15, xc, img + ((size_t)(on ? g : 0) * halves + (t >> 4)) * XImg::BYTES);
     }
 }
 
@@ -613,10 +614,10 @@ hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, h
 hipError_t qh_glue_norm_image(unsigned char* img, const float* x, const float* w, int n_tok, int in_dim,
                               hipStream_t st) {
     // the launch shape of qh_glue_rms_norm's register path, so the norm is its
-    if (n_tok < 1 || n_tok > 16 || in_dim % 256 || in_dim > 4096 || (((uintptr_t)x | (uintptr_t)w) & 15u))
+    if (n_tok < 1 || n_tok > 32 || in_dim % 256 || in_dim > 4096 || (((uintptr_t)x | (uintptr_t)w) & 15u))
         return hipErrorNotSupported;
     const int blk = (in_dim / 4 + 63) / 64 * 64;
-    hipLaunchKernelGGL(qg_norm_image, dim3((unsigned)n_tok), dim3(blk), 0, st, img, x, w, in_dim);
+    hipLaunchKernelGGL(qg_norm_image, dim3((unsigned)n_tok), dim3(blk), 0, st, img, x, w, in_dim, n_tok > 16 ? 2 : 1);
     return hipGetLastError();
 }
 

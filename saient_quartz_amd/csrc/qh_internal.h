@@ -49,11 +49,14 @@ hipError_t qh_launch_mmq(uint32_t type, const uint8_t* W, const float* x, float*
 hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, float* const* Y1, const int* o1,
                                uint32_t t2, int c2, const uint8_t* const* W2, float* const* Y2, const int* o2,
                                const float* x, int n, int in_dim, hipStream_t st, const float* nw = nullptr);
-// n (2..16) tokens of x, RMS-normalised with nw, through count matrices of one
+// n (2..32) tokens of x, RMS-normalised with nw, through count matrices of one
 // type: the norm and the digitisation in one launch, then the batched kernel
-// on those images.  hipErrorNotSupported when the shapes do not fit.
+// on those images.  img_done: the images already hold this x and nw (an
+// earlier call of the same n, x and nw, on the same stream): no norm launch.
+// hipErrorNotSupported when the shapes do not fit.
 hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W, float* const* Y, const int* out_dims,
-                              const float* x, const float* nw, int n, int in_dim, hipStream_t st);
+                              const float* x, const float* nw, int n, int in_dim, hipStream_t st,
+                              bool img_done = false);
 hipError_t qh_launch_mmq_moe_dev(uint32_t type, int sets, const uint8_t* const* E, float* const* Y, int n_exp,
                                  const int* tok_off, int max_tokens, const float* X, const float* X2, int in_dim,
                                  int out_dim, int accum, hipStream_t st);
@@ -88,8 +91,8 @@ void qh_set_error(const char* msg);
 // Decode-step glue kernels (qh_glue.hip).
 hipError_t qh_glue_vec(int op, float* dst, const float* src, float scale, int n, hipStream_t st);
 hipError_t qh_glue_rms_norm(float* out, const float* x, const float* w, int n, hipStream_t st, int rows = 1);
-// RMS norm of n_tok <= 16 token rows fused with the batched GEMM's x images
-// (slot 0 of img); in_dim % 256 == 0, in_dim <= 4096.
+// RMS norm of n_tok <= 32 token rows fused with the batched GEMM's x images
+// (slot 0 of img; two halves past 16 tokens); in_dim % 256 == 0, in_dim <= 4096.
 hipError_t qh_glue_norm_image(unsigned char* img, const float* x, const float* w, int n_tok, int in_dim,
                               hipStream_t st);
 hipError_t qh_glue_rope(float* x, int n_heads, int head_dim, int pos, float theta, float yarn_scale, int orig_ctx,

@@ -474,9 +474,10 @@ class BatchStep:
         hip_gemm_group_norm call.  Up to 4 tokens: the norm fused into the GEMMs
         (q/k (Q4_K) and v (Q6_K) in one launch); 5-16: the norm fused into the
         batched kernel's x images (one launch), then the GEMMs on those images
-        (both types in one launch).  More than 16 tokens of one type: one
+        (both types in one launch); 17-32: the same images in two halves, then
+        one launch per type.  More than 32 tokens of one type: one
         hip_rms_norm_rows, then the type's grouped GEMMs."""
-        if self.n > 16 and len({self.cfg.type_of(nm) for nm in names}) == 1:
+        if self.n > 32 and len({self.cfg.type_of(nm) for nm in names}) == 1:
             check("hip_rms_norm_rows_async", self.L.hip_rms_norm_rows_async(
                 self.xn.data_ptr(), self.hidden.data_ptr(), norm.data_ptr(), self.n, self.cfg.hidden, sp))
             self._gemm(names, layer, self.xn, ys, self.cfg.hidden, sp)

@@ -359,7 +359,7 @@ def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21), (12, 12), (14,), (16, 16)], ids=str)
-@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16, 20, 32])
 @pytest.mark.parametrize("in_dim", [4096, 2048, 5120])
 def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     """hip_gemm_group_norm_async (mixed types: a Q4_K_M layer's q, k (Q4_K) and v
@@ -369,9 +369,10 @@ def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     Q4_K + Q6_K at 5-16 tokens runs the two-format batched launch, whose K
     splits may differ from the per-type calls': there the bar is 1e-5 relative
     against them.  5120 is past the one-workgroup norm; IQ3_S + Q4_K has no
-    two-format kernel.  One type at 5-16 tokens (in_dim <= 4096) takes the norm
-    fused into the batched kernel's x images: its images are the per-type
-    call's digitised normalised rows, so it is bit-identical too."""
+    two-format kernel.  One type at 5-16 tokens, and any types at 17-32 tokens
+    (in_dim <= 4096), take the norm fused into the batched kernel's x images
+    (two image halves past 16 tokens): its images are the per-type call's
+    digitised normalised rows, so it is bit-identical too."""
     import ctypes as C
     outs = [300, 77, 64][:len(types)]
     rng = np.random.default_rng(n + in_dim + sum(types))
@@ -448,13 +449,14 @@ def test_gemm_group_norm_fused_images_few_tokens(qh, oracle, n):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n", [8, 27])
 @pytest.mark.parametrize("types", [(12, 12), (12, 12, 14)], ids=str)
-def test_gemm_group_norm_non_finite_token(qh, types):
-    """A token whose row holds an Inf through the fused norm images (5-16
+def test_gemm_group_norm_non_finite_token(qh, types, n):
+    """A token whose row holds an Inf through the fused norm images (5-32
     tokens): every output of that token is NaN (its norm is NaN), the other
     tokens equal the per-type call bit for bit."""
     import ctypes as C
-    n, in_dim, outs = 8, 2048, [300, 77, 64][:len(types)]
+    in_dim, outs = 2048, [300, 77, 64][:len(types)]
     rng = np.random.default_rng(3)
     x = rng.standard_normal((n, in_dim)).astype(np.float32)
     x[5, 700] = np.inf
