@@ -416,9 +416,10 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
             if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
         }
     }
-    // 5-16 tokens of two types (a layer's q/k in Q4_K and v in Q6_K): the rows
-    // normalised once into scratch, then both types in one batched launch.
-    if (n >= 5 && n <= 16 && nut == 2 && scratch && !qh_force_valu()) {
+    // 5-32 tokens of two types (a layer's q/k in Q4_K and v in Q6_K): the rows
+    // normalised once (into the x images; for 5-16 tokens into scratch when
+    // that does not fit), then both types in one batched launch.
+    if (n >= 5 && n <= 32 && nut == 2 && scratch && !qh_force_valu()) {
         bool ok = true;
         for (int k = 0; k < count; k++)
             ok = ok && qh_check_dims(types[k], in_dim, out_dims[k]) == QH_OK && out_dims[k] > 0 && W[k] && y[k];
@@ -428,7 +429,11 @@ int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* c
                                                x, n, in_dim, st, norm_w);
             if (e == hipSuccess) return QH_OK;
             if (e != hipErrorNotSupported) return qh_fail(e, "hip_gemm_group_norm");
+            ok = n <= 16;  // 17-32 tokens: the per-type fused images below
+        }
+        if (ok) {
             QH_CHECK(qh_glue_rms_norm(scratch, x, norm_w, in_dim, st, n), "hip_gemm_group_norm");
+            hipError_t e;
             e = qh_launch_mmq_mixed(ut[0], cnt[0], wu[0], yu[0], ou[0], ut[1], cnt[1], wu[1], yu[1], ou[1], scratch, n,
                                     in_dim, st);
             if (e == hipSuccess) return QH_OK;

@@ -1195,7 +1195,8 @@ hipError_t qh_launch_mmq_norm(uint32_t type, int count, const uint8_t* const* W,
 }
 
 // Two weight types sharing one x of n <= 16 tokens (a layer's q, k in Q4_K and
-// v in Q6_K) in one launch, images digitised in the kernel: Y1[i] = W1[i] X,
+// v in Q6_K; n <= 32 with nw, 17-32 on two streamed image halves) in one
+// launch, images digitised in the kernel or by qg_norm_image: Y1[i] = W1[i] X,
 // Y2[i] = W2[i] X (token-major, token stride out_dims).  Splits are chosen
 // jointly: the pair (s1, s2) minimising the rounds of 256 workgroups over both
 // formats times (3 + the longer split), the fewest workgroups on ties.
@@ -1205,7 +1206,10 @@ template <class F1, class F2, int NT>
 static void launch_mmq_mix(const QgGroups& g1s, const QgGroups& g2s, const QgXs& xs, uint32_t rb1, uint32_t rb2,
                            int in_dim, int s1, int s2, int c1, dim3 grid, const QgScratch& sc, size_t poff, int coff,
                            hipStream_t st, bool img_ready) {
-    if (img_ready)
+    if constexpr (NT > 16)  // two image halves, streamed from qg_norm_image's images
+        hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES, 0>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1,
+                           rb2, in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
+    else if (img_ready)
         hipLaunchKernelGGL((qh_mmq_mix<F1, F2, NT, QG_WAVES, 1>), grid, dim3(64 * QG_WAVES), 0, st, g1s, g2s, xs, rb1,
                            rb2, in_dim, s1, s2, c1, sc.part, sc.cnt, sc.part + poff, sc.cnt + coff);
     else
@@ -1219,9 +1223,11 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
     if (t1 == QT_Q6_K && t2 == QT_Q4_K)
         return qh_launch_mmq_mixed(t2, c2, W2, Y2, o2, t1, c1, W1, Y1, o1, x, n, in_dim, st, nw);
     if (t1 != QT_Q4_K || t2 != QT_Q6_K) return hipErrorNotSupported;
-    if (n < 2 || n > 16 || c1 < 1 || c2 < 1 || c1 > QG_MAXG || c2 > QG_MAXG || in_dim % 256 ||
+    // 17-32 tokens only from images qg_norm_image writes (two halves, streamed)
+    if (n < 2 || n > (nw ? 32 : 16) || c1 < 1 || c2 < 1 || c1 > QG_MAXG || c2 > QG_MAXG || in_dim % 256 ||
         in_dim / 256 > QG_MAX_GROUPS || ((uintptr_t)x & 15u))
         return hipErrorNotSupported;
+    const int halves = n > 16 ? 2 : 1;
     const QgScratch* sc = qh_mmq_scratch_ptrs();
     if (!sc) return hipErrorNotSupported;
     const int ngroups = in_dim / 256, brows = 32 * QG_WAVES;
@@ -1253,10 +1259,10 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
             }
         }
     const int wgs1 = b1 * s1, wgs = wgs1 + b2 * s2;
-    const int64_t pw = (int64_t)QG_WAVES * 16 * 32;  // floats of one workgroup's partials (16-token bound)
+    const int64_t pw = (int64_t)QG_WAVES * 16 * halves * 32;  // floats of one workgroup's partials (token bound)
     if ((int64_t)wgs * pw > QG_PART_FLOATS || b1 + b2 > QG_PART_TILES) return hipErrorNotSupported;
     QgXs xs = {};
-    xs.halves = 1;
+    xs.halves = halves;
     xs.x[0] = x;
     xs.n[0] = n;
     // nw: x's rows RMS-normalised with nw and digitised by qg_norm_image into
@@ -1266,7 +1272,7 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
         hipError_t e = qh_glue_norm_image(sc->img, x, nw, n, in_dim, st);
         if (e != hipSuccess) return e;
         xs.img = sc->img;
-        xs.img_bytes = (uint32_t)(ngroups * XImg::BYTES);
+        xs.img_bytes = (uint32_t)(halves * ngroups * XImg::BYTES);
     }
     int maxw = 0;
     auto fill = [&](QgGroups& g, int c, const uint8_t* const* Wt, float* const* Y, const int* o, uint32_t rb, int s) {
@@ -1299,8 +1305,10 @@ hipError_t qh_launch_mmq_mixed(uint32_t t1, int c1, const uint8_t* const* W1, fl
                                               img_ready);
     else if (n <= 8) launch_mmq_mix<GQ4K, GQ6K, 8>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
                                               img_ready);
-    else launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
-                                              img_ready);
+    else if (n <= 16) launch_mmq_mix<GQ4K, GQ6K, 16>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff,
+                                                     st, img_ready);
+    else launch_mmq_mix<GQ4K, GQ6K, 32>(g1s, g2s, xs, rb1, rb2, in_dim, s1, s2, c1, grid, *sc, poff, coff, st,
+                                        img_ready);
     return hipGetLastError();
 }
 
