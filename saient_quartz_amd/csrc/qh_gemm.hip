@@ -50,6 +50,7 @@ typedef _Float16 qh_f16x2 __attribute__((ext_vector_type(2)));
 #ifndef QG_GMAX
 #define QG_GMAX 5           // groups per K split (their x images stay in LDS)
 #endif
+#define QG_GMAX2 3          // the same for 32-token launches (two image halves per group)
 #define QG_DIG_BLOCKS 128   // row blocks per token block up to which a launch digitises x in the kernel
 #define QG_MAX_GROUPS 256   // in_dim <= 65536 on the matrix-core path
 
@@ -493,7 +494,7 @@ QH_DEV qh_u32x4 qh_lds128(const unsigned char* p) { return *reinterpret_cast<con
 // the end).
 template <class F, int NT, int W, int MODE>
 constexpr int qh_mmq_lds() {
-    return (MODE != 0 ? QG_GMAX : 2) * (NT > 16 ? 2 : 1) * XImg::BYTES + W * (32 * F::RS + 16) +
+    return (MODE != 0 ? (NT > 16 ? QG_GMAX2 : QG_GMAX) : 2) * (NT > 16 ? 2 : 1) * XImg::BYTES + W * (32 * F::RS + 16) +
            (F::GRID ? IQT_BYTES : 0);
 }
 
@@ -512,15 +513,16 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     static_assert(NT == 4 || NT == 8 || NT == 16 || NT == 32, "NT");
     using XI = XImg;
     // 32 tokens: two 16-token halves, each its own image and MFMA accumulator
-    // against the same converted weights (streamed images only)
+    // against the same converted weights (streamed images, or digitised in the
+    // kernel)
     constexpr int NTH = NT > 16 ? 2 : 1;
-    static_assert(NTH == 1 || MODE == 0, "32-token launches stream their images");
+    static_assert(NTH == 1 || MODE != 1, "32-token launches: streamed or digitised images");
     constexpr int NQ = (NT > 16 ? 16 : NT) / 4;  // slot quads per half (tokens 16h + 4q .. + 3)
     constexpr int TPW = 1;                     // 32-row tiles per wavefront
     constexpr int GRIDB = F::GRID ? IQT_BYTES : 0;  // IQ codebook and sign tables
     constexpr int IMB = NTH * XI::BYTES;  // a group's images (both halves, adjacent)
     constexpr bool RES = MODE != 0;
-    constexpr int NSLOT = RES ? QG_GMAX : 2;  // image slots in LDS
+    constexpr int NSLOT = RES ? (NTH == 2 ? QG_GMAX2 : QG_GMAX) : 2;  // image slots in LDS
     static_assert(qh_mmq_lds<F, NT, W, MODE>() == NSLOT * IMB + W * TILE + GRIDB, "LDS layout");
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int R = lane & 31, hh = lane >> 5;
@@ -594,7 +596,8 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     //     runs without workgroup barriers.
     //   MODE 2: as MODE 1, but the workgroup digitises the split's x (and
     //     SwiGLU operand) itself: no qg_ximage launch; thread tid < 32 NT
-    //     takes token tid / 32, elements 8 (tid % 32) .. + 7 of each group.
+    //     takes token tid / 32, elements 8 (tid % 32) .. + 7 of each group
+    //     (32 tokens: tokens tid / 32 and 16 + tid / 32, one per half).
     //   MODE 0: one group at a time through a slot pair, loaded with the
     //     weights one iteration ahead; one workgroup barrier per group orders
     //     the pair.
@@ -620,44 +623,54 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     qh_u32x4 wr[QG_NBUF][NH];
     qh_u32x4 xq[RES ? 1 : XP];  // streamed: the next group's image
     if constexpr (MODE == 2) {
-        static_assert(32 * NT <= 64 * W, "one chunk per thread");
+        constexpr int TH = NT > 16 ? 16 : NT;  // tokens per half
+        static_assert(32 * TH <= 64 * W, "one chunk per thread and half");
         const int xt = threadIdx.x >> 5, xc = threadIdx.x & 31;
-        const bool xon = (int)threadIdx.x < 32 * NT && xt < n;
         const QhBuf fb = qh_buf(tk.x, 4u * (uint32_t)n * (uint32_t)in_dim);
         const QhBuf ub = qh_buf(tk.x2, 4u * (uint32_t)n * (uint32_t)in_dim);
         const bool swiglu = tk.x2 != nullptr;
         const uint32_t xo = 4u * ((uint32_t)xt * (uint32_t)in_dim + 8u * (uint32_t)xc);
-        qh_u32x4 xd[QG_GMAX][2], ud[QG_GMAX][2];
+        bool xon[NTH];
 #pragma unroll
-        for (int k = 0; k < QG_GMAX; k++) {
-            const uint32_t off = (xon && k < nk) ? xo + 1024u * (uint32_t)grp(k) : 0x80000000u;
-            xd[k][0] = qh_ld128(fb, off);
-            xd[k][1] = qh_ld128(fb, off + 16u);
-            const uint32_t uoff = swiglu ? off : 0x80000000u;
-            ud[k][0] = qh_ld128(ub, uoff);
-            ud[k][1] = qh_ld128(ub, uoff + 16u);
-        }
+        for (int p = 0; p < NTH; p++) xon[p] = (int)threadIdx.x < 32 * TH && xt + 16 * p < n;
+        qh_u32x4 xd[NSLOT][NTH][2], ud[NSLOT][NTH][2];
+#pragma unroll
+        for (int k = 0; k < NSLOT; k++)
+#pragma unroll
+            for (int p = 0; p < NTH; p++) {
+                const uint32_t off = (xon[p] && k < nk)
+                                         ? xo + 64u * (uint32_t)p * (uint32_t)in_dim + 1024u * (uint32_t)grp(k)
+                                         : 0x80000000u;
+                xd[k][p][0] = qh_ld128(fb, off);
+                xd[k][p][1] = qh_ld128(fb, off + 16u);
+                const uint32_t uoff = swiglu ? off : 0x80000000u;
+                ud[k][p][0] = qh_ld128(ub, uoff);
+                ud[k][p][1] = qh_ld128(ub, uoff + 16u);
+            }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < QG_GMAX; k++)
+        for (int k = 0; k < NSLOT; k++)
             if (k < nk) {
-                float v[8];
-                qg_chunk(xd[k], ud[k], swiglu, v);
-                qg_digitise(v, xon, lane, xt, xc, lds + k * IMB);
+#pragma unroll
+                for (int p = 0; p < NTH; p++) {
+                    float v[8];
+                    qg_chunk(xd[k][p], ud[k][p], swiglu, v);
+                    qg_digitise(v, xon[p], lane, xt, xc, lds + k * IMB + p * XI::BYTES);
+                }
             }
     } else if constexpr (RES) {
-        qh_u32x4 xr[QG_GMAX][XP];
+        qh_u32x4 xr[NSLOT][XP];
 #pragma unroll
-        for (int k = 0; k < QG_GMAX; k++) load_x(k < nk ? k : nk, xr[k]);
+        for (int k = 0; k < NSLOT; k++) load_x(k < nk ? k : nk, xr[k]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 0; b < QG_NBUF; b++) load_w(b, wr[b]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < QG_GMAX; k++)
+        for (int k = 0; k < NSLOT; k++)
             if (k < nk) store_x(lds + k * IMB, xr[k]);
     } else {
         // group 0's image, the first QG_NBUF groups' weights, group 0's image
@@ -942,7 +955,10 @@ static void launch_mmq_nt(int nt, int mode, const QgGroups& gs, const QgXs& xs, 
     if (nt <= 4) launch_mmq_t<F, 4>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
     else if (nt <= 8) launch_mmq_t<F, 8>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
     else if (nt <= 16) launch_mmq_t<F, 16>(mode, gs, xs, grid, splits, sc, row_bytes, in_dim, st);
-    else  // 17-32 tokens: streamed images only (the caller forces mode 0)
+    else if (mode == 2)  // 17-32 tokens: digitised in the kernel, or streamed
+        hipLaunchKernelGGL((qh_mmq<F, 32, QG_WAVES, 2>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
+                           splits, sc.part, sc.cnt);
+    else
         hipLaunchKernelGGL((qh_mmq<F, 32, QG_WAVES, 0>), grid, dim3(64 * QG_WAVES), 0, st, gs, xs, row_bytes, in_dim,
                            splits, sc.part, sc.cnt);
 }
@@ -1025,7 +1041,10 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
     int splits = qh_mmq_splits_env();
     if (splits <= 0) splits = qg_pick_splits(blocks, ngroups, ngroups, QG_TARGET_WGS);
     splits = splits < ngroups ? splits : ngroups;
-    const bool res = (ngroups + splits - 1) / splits <= QG_GMAX;
+    // 17-32 tokens per block: two image halves per group, QG_GMAX2 groups of
+    // them resident in LDS
+    const int halves = ntmax > 16 ? 2 : 1;
+    const bool res = (ngroups + splits - 1) / splits <= (halves == 2 ? QG_GMAX2 : QG_GMAX);
     // Resident images are digitised in the kernel (no image launch) when few
     // row blocks share each token block's x; otherwise qg_ximage digitises
     // each block's x once.
@@ -1037,11 +1056,9 @@ static hipError_t qg_run(uint32_t type, const QgEntry* en, int cnt, int in_dim, 
         if (nslots != 1) return hipErrorNotSupported;
         mode = res ? 1 : 0;
     }
-    // 17-32 tokens per block: two image halves per group, streamed (the
-    // resident modes would need twice the LDS); ready images are then the
-    // two-half layout qg_norm_image writes past 16 tokens
-    const int halves = ntmax > 16 ? 2 : 1;
-    if (halves == 2) mode = 0;
+    // two halves: no resident copy of ready images (MODE 1); ready images are
+    // the two-half layout qg_norm_image writes past 16 tokens
+    if (halves == 2 && mode == 1) mode = 0;
     const int64_t pb = (int64_t)(brows / 32) * 16 * halves * 32;  // floats of one partial block (token bound)
     // The partials and the per-block counters must hold the launch: otherwise
     // halve the batch (or, for one entry, its rows) and run the halves in turn.
