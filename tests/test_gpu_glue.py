@@ -218,10 +218,12 @@ def test_attention_step_repeat(qh):
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("n_seq, pos", [(1, 40), (4, 0), (4, 77), (16, 300)])
+@pytest.mark.parametrize("n_seq, pos", [(1, 40), (4, 0), (4, 77), (16, 300), (32, 511), (3, 2100)])
 def test_attention_step_batched(qh, n_seq, pos):
     """hip_attention_step_batched: each sequence against its own single-sequence
-    oracle (own q/k/v rows and own cache), 1e-5 relative L2."""
+    oracle (own q/k/v rows and own cache), 1e-5 relative L2 (2e-4 past 1000
+    cached rows, as the single-sequence test: the output is a near-cancelling
+    f32 sum over that many value rows)."""
     nh, nkv, hd = 8, 2, 128
     kvd = nkv * hd
     max_seq = pos + 2
@@ -244,7 +246,7 @@ def test_attention_step_batched(qh, n_seq, pos):
         kc64, vc64 = kc[z].astype(np.float64), vc[z].astype(np.float64)
         kc64[pos], vc64[pos] = kr, v[z]
         _, ref = g.attention(qr, kc64, vc64, nh, nkv, pos + 1, hd, kvd, 0.09)
-        assert cf.rel_l2(got[z], ref) < 1e-5, z
+        assert cf.rel_l2(got[z], ref) < (1e-5 if pos < 1000 else 2e-4), z
 
 
 def test_rms_norm_rows(qh):
