@@ -86,7 +86,7 @@ int hip_gemv_fused_async(uint32_t ggml_type, int count, const uint8_t* const* W,
 
 /* Y[t][j] = sum_k W[j,k] X[t][k] for t < n (token-major).  GPU counterpart of
  * dequant::gemm (src/dequant.rs:143-200); n == 1 is hip_gemv.  For n >= 2 the
- * matrix-core path reads the weights once per 16 tokens (see the note above on
+ * matrix-core path reads the weights once per 32 tokens (see the note above on
  * its device scratch); x is kept to 23 bits below each token's largest |x| per
  * 256 elements, so results stay within 1e-3 relative L2 per token (observed
  * ~1e-6) with activation outliers up to thousands of times the RMS. */
@@ -150,15 +150,16 @@ int hip_gemm_grouped_norm_static_async(uint32_t ggml_type, int count, const uint
  * (types[k] for W[k]): a batch's norm + q/k/v when v has its own type, as
  * Q4_K_M models have (src/cuda.rs:549-562).  For 2..4 tokens, two types among
  * Q4_K/Q5_K + Q6_K and in_dim <= 4096, one launch computes every matrix; each
- * token's result then equals the per-type call's bit for bit.  For 5..16
+ * token's result then equals the per-type call's bit for bit.  For 5..32
  * tokens of Q4_K + Q6_K, one launch normalises the rows straight into the
- * batched kernel's x images (in_dim <= 4096; otherwise into d_scratch, n *
- * in_dim floats) and both types run in one batched matrix-core launch; each
- * token's result equals the per-type batched call's within rounding (the split
- * of K may differ).  For 5..16 tokens of one matrix-core type and in_dim <=
- * 4096, the same fused norm feeds that type's batched launch, bit-identical to
- * the per-type call.  Otherwise one hip_gemm_grouped_norm_async per type, with
- * its scratch rule. */
+ * batched kernel's x images (in_dim <= 4096; otherwise, up to 16 tokens, into
+ * d_scratch, n * in_dim floats) and both types run in one batched matrix-core
+ * launch; each token's result equals the per-type batched call's within
+ * rounding (the split of K may differ).  For 5..16 tokens of one matrix-core
+ * type, and 17..32 tokens of any matrix-core types, with in_dim <= 4096, the
+ * same fused norm feeds each type's batched launch, bit-identical to the
+ * per-type call.  Otherwise one hip_gemm_grouped_norm_async per type, with its
+ * scratch rule. */
 int hip_gemm_group_norm_async(int count, const uint32_t* types, const uint8_t* const* d_data, const float* d_x,
                               const float* d_norm_w, float* const* d_y, int n, const int* out_dims, int in_dim,
                               float* d_scratch, void* stream);

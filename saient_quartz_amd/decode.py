@@ -475,7 +475,8 @@ class BatchStep:
         (q/k (Q4_K) and v (Q6_K) in one launch); 5-16: the norm fused into the
         batched kernel's x images (one launch), then the GEMMs on those images
         (both types in one launch); 17-32: the same images in two halves, then
-        one launch per type.  More than 32 tokens of one type: one
+        one launch for Q4_K + Q6_K or one per type.  More than 32 tokens of one
+        type: one
         hip_rms_norm_rows, then the type's grouped GEMMs."""
         if self.n > 32 and len({self.cfg.type_of(nm) for nm in names}) == 1:
             check("hip_rms_norm_rows_async", self.L.hip_rms_norm_rows_async(
