@@ -359,7 +359,7 @@ def test_gemm_grouped_norm(qh, oracle, t, n, in_dim):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("types", [(12, 12, 14), (13, 14, 13), (12, 21), (12, 12), (14,), (16, 16)], ids=str)
-@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16, 20, 32])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 16, 17, 20, 32])
 @pytest.mark.parametrize("in_dim", [4096, 2048, 5120])
 def test_gemm_group_norm_mixed(qh, oracle, types, n, in_dim):
     """hip_gemm_group_norm_async (mixed types: a Q4_K_M layer's q, k (Q4_K) and v
