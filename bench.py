@@ -193,7 +193,8 @@ def main():
 
 
 def batched_suite(torch, reps=50):
-    """hip_gemm with 16 tokens (and 4 for the 4-sequence step's big matrices) at
+    """hip_gemm with 16 tokens (4 for the 4-sequence step's big matrices, 32 for
+    the 17-32-token tile) at
     the batched shapes of BASELINE.json configs[3] (Q4_K gate/up, Q6_K down)
     and configs[4] (IQ3_S / IQ2_XXS expert gate/up and down): each shape's
     `reps` calls over rotated weights captured in one HIP graph, events around
@@ -204,7 +205,8 @@ def batched_suite(torch, reps=50):
     L = lib()
     out = {}
     for t, o, i, n in ((12, 14336, 4096, 16), (14, 4096, 14336, 16), (12, 14336, 4096, 4), (14, 4096, 14336, 4),
-                       (21, 14336, 4096, 16), (21, 4096, 14336, 16), (16, 14336, 4096, 16), (16, 4096, 14336, 16)):
+                       (21, 14336, 4096, 16), (21, 4096, 14336, 16), (16, 14336, 4096, 16), (16, 4096, 14336, 16),
+                       (12, 14336, 4096, 32), (14, 4096, 14336, 32), (21, 14336, 4096, 32), (16, 14336, 4096, 32)):
         wb = type_size(t, o * i)
         rot = max(3, -(-768 * 2**20 // wb))
         Ws = [synth_device.weights(t, o, i, seed=40 + k) for k in range(rot)]
