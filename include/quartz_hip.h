@@ -392,6 +392,13 @@ int hip_attention_step_batched_async(float* out, const float* q, const float* k,
 int hip_embed_lookup(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim);
 int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim,
                            void* stream);
+/* n_tok rows at once (a batch's tokens, host array): row i = tokens[i] into
+ * out + i * out_stride floats (out_stride >= embed_dim when n_tok > 1), each
+ * bit-identical to hip_embed_lookup; up to 64 rows per launch.  No counterpart
+ * in the reference (one embed_lookup per token); for callers that step several
+ * sequences together. */
+int hip_embed_lookup_batched_async(float* out, size_t out_stride, const uint8_t* d_data, uint32_t ggml_type,
+                                   const int* tokens, int n_tok, int embed_dim, void* stream);
 
 /* ---------------------------------------------------------------- GGUF
  * Reader for the weight container either side of the GEMV path: GgufFile

@@ -140,6 +140,8 @@ _SIGS = {
     "hip_swiglu_oai_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
     "hip_embed_lookup": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int]),
     "hip_embed_lookup_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_void_p]),
+    "hip_embed_lookup_batched_async": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int,
+                                                 C.c_int, C.c_void_p]),
     "hip_attn_score": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     "hip_softmax_sink": (C.c_int, [C.c_void_p, C.c_int, C.c_float]),
     "hip_attn_values": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int]),

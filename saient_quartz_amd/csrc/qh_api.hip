@@ -887,7 +887,20 @@ int hip_embed_lookup_async(float* out, const uint8_t* data, uint32_t ggml_type, 
     if (qk == 0) return QH_ERR_TYPE;
     if (token < 0 || embed_dim <= 0 || embed_dim % qk) return QH_ERR_DIMS;
     if (!out || !data) return QH_ERR_NULL;
-    QH_GLUE(qh_glue_embed(out, data, ggml_type, token, embed_dim, (hipStream_t)s), "hip_embed_lookup");
+    QH_GLUE(qh_glue_embed(out, 0, data, ggml_type, &token, 1, embed_dim, (hipStream_t)s), "hip_embed_lookup");
+}
+int hip_embed_lookup_batched_async(float* out, size_t out_stride, const uint8_t* data, uint32_t ggml_type,
+                                   const int* tokens, int n_tok, int embed_dim, void* s) {
+    const int qk = qh_block_elems(ggml_type);
+    if (qk == 0) return QH_ERR_TYPE;
+    if (n_tok < 0 || embed_dim <= 0 || embed_dim % qk || (n_tok > 1 && out_stride < (size_t)embed_dim))
+        return QH_ERR_DIMS;
+    if (n_tok == 0) return QH_OK;
+    if (!out || !data || !tokens) return QH_ERR_NULL;
+    for (int i = 0; i < n_tok; i++)
+        if (tokens[i] < 0) return QH_ERR_DIMS;
+    QH_GLUE(qh_glue_embed(out, out_stride, data, ggml_type, tokens, n_tok, embed_dim, (hipStream_t)s),
+            "hip_embed_lookup_batched");
 }
 int hip_embed_lookup(float* out, const uint8_t* data, uint32_t ggml_type, int token, int embed_dim) {
     return hip_embed_lookup_async(out, data, ggml_type, token, embed_dim, nullptr);

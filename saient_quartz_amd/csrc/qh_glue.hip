@@ -575,13 +575,20 @@ __global__ __launch_bounds__(256) void qg_swiglu_oai(float* out, const float* ga
 // (embed_lookup_*, :678-731 handle Q5_1, IQ4_NL and BF16).  A workgroup takes
 // up to 4096 output values: it stages their blocks' bytes in LDS with coalesced
 // loads, one thread per block decodes from LDS into LDS (qh_decode_block), and
-// the values leave in coalesced stores.
+// the values leave in coalesced stores.  Several rows (a batch's tokens) go in
+// one launch, row blockIdx.y = toks.t[blockIdx.y] into out + blockIdx.y *
+// out_stride, so the rows decode side by side.
 #define QG_EMB_OUT 4096
 #define QG_EMB_RAW 4608
-__global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t* data, uint32_t type, int token,
-                                                       int embed_dim, int qk, uint32_t bb, int bpw) {
+#define QG_EMB_TOKS 64  // rows per launch
+struct QgToks { int t[QG_EMB_TOKS]; };
+__global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t* data, uint32_t type,
+                                                       const QgToks toks, size_t out_stride, int embed_dim, int qk,
+                                                       uint32_t bb, int bpw) {
     __shared__ __align__(16) uint8_t raw[QG_EMB_RAW];
     __shared__ __align__(16) float dec[QG_EMB_OUT];
+    const int token = toks.t[blockIdx.y];
+    out += (size_t)blockIdx.y * out_stride;
     const int nb = embed_dim / qk, b0 = blockIdx.x * bpw;
     const int nbw = min(bpw, nb - b0);
     const uint8_t* src = data + ((size_t)token * nb + b0) * bb;
@@ -742,14 +749,22 @@ hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* u
     return hipGetLastError();
 }
 
-hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st) {
+hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uint32_t type, const int* tokens,
+                         int n_tok, int embed_dim, hipStream_t st) {
     const int qk = qh_block_elems(type);
     const uint32_t bb = qh_block_bytes(type);
     const int nb = embed_dim / qk;
     int bpw = QG_EMB_OUT / qk;
     if (bpw > 256) bpw = 256;
     if ((uint32_t)bpw * bb > QG_EMB_RAW) bpw = QG_EMB_RAW / bb;
-    hipLaunchKernelGGL(qg_embed_lookup, dim3((unsigned)((nb + bpw - 1) / bpw)), dim3(256), 0, st, out, data, type,
-                       token, embed_dim, qk, bb, bpw);
-    return hipGetLastError();
+    for (int t0 = 0; t0 < n_tok; t0 += QG_EMB_TOKS) {
+        const int c = n_tok - t0 < QG_EMB_TOKS ? n_tok - t0 : QG_EMB_TOKS;
+        QgToks toks = {};
+        for (int i = 0; i < c; i++) toks.t[i] = tokens[t0 + i];
+        hipLaunchKernelGGL(qg_embed_lookup, dim3((unsigned)((nb + bpw - 1) / bpw), (unsigned)c), dim3(256), 0, st,
+                           out + (size_t)t0 * out_stride, data, type, toks, out_stride, embed_dim, qk, bb, bpw);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }

@@ -119,5 +119,6 @@ hipError_t qh_moe_swiglu(float* act, const float* g, const float* u, const float
 hipError_t qh_moe_combine(float* out, const float* yg, const int* slot_of, const float* wts, const int* ids,
                           const float* db, int n_tok, int k, int d, int accumulate, hipStream_t st);
 hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* up, int n, hipStream_t st);
-hipError_t qh_glue_embed(float* out, const uint8_t* data, uint32_t type, int token, int embed_dim, hipStream_t st);  // hip_last_error() text
+hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uint32_t type, const int* tokens,
+                         int n_tok, int embed_dim, hipStream_t st);  // hip_last_error() text
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

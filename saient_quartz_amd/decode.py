@@ -17,6 +17,7 @@ Layer shapes (forward_gpu_step's order, src/cuda.rs:556-562, :647, :773-788):
   gate 14336x4096 Q4_K, up 14336x4096 Q4_K, down 4096x14336 Q6_K;
 then the output head 128256x4096 Q6_K.  32 layers: 4,875,853,824 weight bytes.
 """
+import ctypes as C
 from dataclasses import dataclass
 
 import torch
@@ -495,10 +496,9 @@ class BatchStep:
         sp = (stream or torch.cuda.current_stream()).cuda_stream
         kvd = c.n_kv * c.head_dim
         row = self.hidden.stride(0)
-        for i, t in enumerate(tokens):
-            check("hip_embed_lookup_async", L.hip_embed_lookup_async(
-                self.hidden.data_ptr() + 4 * i * row, self.w["embed"].data_ptr(), c.type_of("embed"), int(t),
-                c.hidden, sp))
+        toks = (C.c_int * n)(*[int(t) for t in tokens])
+        check("hip_embed_lookup_batched_async", L.hip_embed_lookup_batched_async(
+            self.hidden.data_ptr(), row, self.w["embed"].data_ptr(), c.type_of("embed"), toks, n, c.hidden, sp))
         for l in range(c.layers):
             self._gemm_norm(("q", "k", "v"), l, self.w["attn_norm"][l], (self.q, self.k, self.v), sp)
             check("hip_attention_step_batched_async", L.hip_attention_step_batched_async(

@@ -157,6 +157,39 @@ def test_embed_lookup_bit_exact(qh, oracle, t):
     assert np.array_equal(out.download(np.uint32)[:dim], ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [1, 5, 70])
+@pytest.mark.parametrize("t", [12, 14, 8, 21])
+def test_embed_lookup_batched_bit_exact(qh, oracle, t, n):
+    """hip_embed_lookup_batched_async: n rows (repeats included; 70 takes two
+    launches of at most 64) at a row stride past embed_dim, each bit-exact to
+    the oracle's dequantised row; the gap between rows is left untouched."""
+    qk = GGML_TYPES[t][1]
+    vocab, dim, stride = 40, 4096 if qk > 1 else 100, 4096 + 64 if qk > 1 else 128
+    data = synth.weights(t, vocab, dim, seed=57 + t)
+    dd = GpuBuf.upload(data)
+    rng = np.random.default_rng(n + t)
+    toks = rng.integers(0, vocab, n).astype(np.int32)
+    out = GpuBuf.upload_f32(np.full(n * stride, 7.0, np.float32))
+    check("embed_batched", qh.hip_embed_lookup_batched_async(out.ptr, stride, dd.ptr, t, (C.c_int * n)(*toks.tolist()),
+                                                             n, dim, None))
+    sync(qh)
+    ref = oracle.dequant(t, data, vocab * dim).reshape(vocab, dim)
+    got = out.download(np.uint32)[:n * stride].reshape(n, stride)
+    for i in range(n):
+        assert np.array_equal(got[i, :dim], ref[toks[i]].view(np.uint32)), i
+        assert np.all(got[i, dim:].view(np.float32) == 7.0), i
+
+
+def test_embed_lookup_batched_rejects(qh):
+    """Negative tokens and a row stride below embed_dim are rejected before any
+    launch."""
+    out = GpuBuf.alloc_f32(2 * 256)
+    dd = GpuBuf.upload(synth.weights(12, 4, 256, seed=1))
+    assert qh.hip_embed_lookup_batched_async(out.ptr, 256, dd.ptr, 12, (C.c_int * 2)(1, -1), 2, 256, None) != 0
+    assert qh.hip_embed_lookup_batched_async(out.ptr, 128, dd.ptr, 12, (C.c_int * 2)(1, 2), 2, 256, None) != 0
+    assert qh.hip_embed_lookup_batched_async(out.ptr, 256, dd.ptr, 12, (C.c_int * 2)(1, 2), 0, 256, None) == 0
+
+
 @pytest.mark.parametrize("heads", [(32, 8), (4, 2), (8, 8), (6, 4), (16, 1), (8, 2, 64), (4, 4, 96)], ids=str)
 @pytest.mark.parametrize("pos", [0, 5, 31, 32, 33, 100, 1000, 2047, 5000])
 def test_attention_step(qh, heads, pos):
