@@ -208,3 +208,36 @@ def test_batch_step_matches_oracle(qh, oracle, n, case):
                                                     ocfg)
             assert cf.rel_l2(got_h[i], ref_hidden) < 1e-3, (pos, i)
             assert cf.rel_l2(got_l[i], ref_logits) < 1e-3, (pos, i, cf.rel_l2(got_l[i], ref_logits))
+
+
+@pytest.mark.parametrize("n, case", [(16, "llama_q4km_2layers"), (32, "llama_q4km_2layers"), (24, "sym_2layers")])
+def test_batch_step_graph_replays(qh, n, case):
+    """BatchStep captured into a HIP graph (the tokens baked into its batched
+    embedding launch) and replayed three times, each after an eager step on
+    other tokens at the same position (which rewrites the scratch images,
+    split-K partials and counters and the cache row): every replay's logits
+    equal the eager step's bit for bit."""
+    from saient_quartz_amd.decode import BatchStep
+    kw = dict(hidden=512, n_heads=4, n_kv=2, head_dim=128, ffn=1024, vocab=300, layers=2, max_seq=8)
+    kw.update(BATCH_CASES[case])
+    cfg = ModelConfig(**kw)
+    raw, norms = host_model(cfg, seed=13, realistic=True)
+    step = BatchStep(cfg, device_weights(raw, norms), n)
+    rng = np.random.default_rng(n)
+    for pos in range(3):
+        step.issue(rng.integers(0, cfg.vocab, n), pos)
+    tokens = rng.integers(0, cfg.vocab, n)
+    step.issue(tokens, 3)
+    torch.cuda.synchronize()
+    eager = step.logits.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.issue(tokens, 3)
+    for r in range(3):
+        print(f"batch graph n={n} case {case} replay {r}", flush=True)
+        step.issue(rng.integers(0, cfg.vocab, n), 3)
+        torch.cuda.synchronize()
+        assert not torch.equal(step.logits, eager)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(step.logits, eager), r
