@@ -266,14 +266,23 @@ def decode_leg(torch, reps):
 
 
 def forward_leg(torch, reps, wbytes):
-    """End-to-end Llama-3-8B-shaped decode steps, one HIP graph per (N, position),
-    timed over `reps` replays at KV position 0 and 511:
+    """End-to-end Llama-3-8B-shaped decode steps generating tokens: one HIP
+    graph per N, captured once with the tokens and the position read on the
+    device (issue(dev=True, greedy=True): the step ends with the greedy pick,
+    which writes the next tokens and advances the position), then `reps`
+    consecutive replays from KV position 0 and from 511, i.e. positions
+    p0 .. p0 + reps - 1, each step feeding the next:
       N = 1: ForwardStep (embedding lookup, 32 x [fused norm + q/k/v, RoPE + KV
              append + attention, o + residual, fused norm + gate/up + SwiGLU,
-             down + residual], fused final norm + head; 5 launches per layer);
+             down + residual], fused final norm + head, greedy pick; 5
+             launches per layer);
       N = 4, 16, 32: BatchStep, N sequences in lockstep with their own K/V
              caches (batched matrix-core GEMMs, one weight pass per 16 tokens,
-             or per 32 on two image halves, and batched glue)."""
+             or per 32 on two image halves, and batched glue).
+    n1_eager_pos0: the same N = 1 steps issued eagerly (host token and position
+    arguments, one C-ABI call per launch from Python, as a host without graphs
+    would), events around `reps` steps; issue_ms_per_step is the host's own
+    time to issue one step."""
     from saient_quartz_amd.decode import BatchStep, ForwardStep, ModelConfig
 
     cfg = ModelConfig(max_seq=1024)
@@ -282,30 +291,60 @@ def forward_leg(torch, reps, wbytes):
     for n in (1, 4, 16, 32):
         step = ForwardStep(cfg, weights) if n == 1 else BatchStep(cfg, weights, n)
         tokens = [(7 * i + 3) % 1000 for i in range(n)]
-        issue = (lambda pos: step.issue(tokens[0], pos)) if n == 1 else (lambda pos: step.issue(tokens, pos))
+        set_state = (lambda pos: step.set_state(tokens[0], pos)) if n == 1 else (lambda pos: step.set_state(tokens, pos))
+        set_state(0)
+        step.issue(dev=True, greedy=True)  # eager warm-up (first-call device queries happen outside capture)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step.issue(dev=True, greedy=True)
         for pos in (0, 511):
-            issue(pos)
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                issue(pos)
+            set_state(pos)
             g.replay()
+            set_state(pos)
             torch.cuda.synchronize()
+            ms = timed_replay(torch, g, reps) / reps
+            st = step.state.cpu().tolist()
+            if st[-1] != pos + reps:
+                raise SystemExit(f"decode state did not advance: {st[-1]} != {pos + reps}")
             if not torch.isfinite(step.logits).all():
                 raise SystemExit("decode step produced non-finite logits")
-            ms = timed_replay(torch, g, reps) / reps
             rec = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
                    "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
-                   "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+                   "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+                   "positions": [pos, pos + reps - 1]}
             if n == 1:
-                rec["launches"] = 1 + 5 * cfg.layers + 1
+                rec["launches"] = 1 + 5 * cfg.layers + 2
             out[f"n{n}_full_pos{pos}"] = rec
-            del g
+        del g
+        if n == 1:
+            out["n1_eager_pos0"] = eager_steps(torch, step, reps)
         del step
         torch.cuda.empty_cache()
     del weights
     torch.cuda.empty_cache()
     return out
+
+
+def eager_steps(torch, step, reps):
+    """`reps` ForwardStep steps at positions 0 .. reps-1 issued eagerly with
+    host arguments: GPU time between events, and the host's issue time."""
+    for pos in range(3):
+        step.issue(11, pos)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1_000_000)
+    t0.record()
+    h0 = time.perf_counter()
+    for pos in range(reps):
+        step.issue(11 + pos, pos)
+    h1 = time.perf_counter()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    return {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+            "issue_ms_per_step": round((h1 - h0) * 1e3 / reps, 4), "positions": [0, reps - 1]}
 
 
 def moe_leg(torch, reps):
@@ -425,6 +464,27 @@ def measured_traffic(path):
     return None
 
 
+def host_llc_bytes():
+    """Total last-level (L3) cache of the host: the sizes of the distinct L3
+    instances sysfs lists (0 if unknown)."""
+    seen, total = set(), 0
+    base = Path("/sys/devices/system/cpu")
+    for idx in base.glob("cpu[0-9]*/cache/index[0-9]*"):
+        try:
+            if (idx / "level").read_text().strip() != "3":
+                continue
+            key = (idx / "shared_cpu_list").read_text().strip()
+            if key in seen:
+                continue
+            seen.add(key)
+            size = (idx / "size").read_text().strip()
+            mult = {"K": 2**10, "M": 2**20, "G": 2**30}.get(size[-1], 1)
+            total += int(size.rstrip("KMG")) * mult
+        except (OSError, ValueError):
+            continue
+    return total
+
+
 def cpu_threads():
     """Threads for the CPU baseline: the host's CPUs available to this process,
     capped at the GPU box's CPU share for one GPU (16; OMP_NUM_THREADS is set to
@@ -462,16 +522,29 @@ def cpu_baseline(out_dim, in_dim, seconds):
     share = seconds / 5.0
     o.set_threads(cores)
     data = synth.weights(Q4K, out_dim, in_dim, seed=20261202)
+    # Copies of the weights at distinct addresses, rotated call by call, twice
+    # the host's last-level cache in all, so no call reads weights the cache
+    # kept from an earlier one.
+    llc = host_llc_bytes()
+    n_copies = max(2, -(-2 * max(llc, 1) // data.nbytes))
+    copies = [data] + [data.copy() for _ in range(n_copies - 1)]
     x = synth.activations(1, in_dim, seed=3)[0]
     alg = data.nbytes + 4 * in_dim + 4 * out_dim
-    dt, reps = _time_calls(lambda: o.gemv(Q4K, x, data, in_dim, out_dim), share)
+    rot = [0]
+
+    def gemv_rot():
+        o.gemv(Q4K, x, copies[rot[0] % n_copies], in_dim, out_dim)
+        rot[0] += 1
+
+    dt, reps = _time_calls(gemv_rot, share)
     rec = {"value": round(alg / dt / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
            "sample": f"{reps} x Q4_K 14336x4096 GEMV (C restatement of q4k_row, OpenMP over rows), "
-                     f"{dt * 1e3:.2f} ms each",
-           "host_cpus": os.cpu_count(), "cpus_available": avail}
+                     f"{dt * 1e3:.2f} ms each, weights rotated over {n_copies} copies "
+                     f"({n_copies * data.nbytes / 2**20:.0f} MiB, 2x the host LLC)",
+           "host_cpus": os.cpu_count(), "cpus_available": avail, "host_llc_bytes": llc}
     legs = {}
     o.set_threads(1)
-    dt1, reps = _time_calls(lambda: o.gemv(Q4K, x, data, in_dim, out_dim), share)
+    dt1, reps = _time_calls(gemv_rot, share)
     legs["q4_k_14336x4096_1core"] = {"GB_s": round(alg / dt1 / 1e9, 2), "ms": round(dt1 * 1e3, 2), "cores": 1,
                                      "reps": reps}
     o.set_threads(cores)
@@ -483,21 +556,31 @@ def cpu_baseline(out_dim, in_dim, seconds):
     a8 = q8.nbytes + 4 * 4096 * 2
     legs["q8_0_4096x4096_dequant_matmul"] = {"GB_s": round(a8 / dt8 / 1e9, 2), "ms": round(dt8 * 1e3, 2),
                                              "cores": cores, "reps": reps}
-    # batched gemm, 16 tokens, Q4_K 14336x4096
+    # batched gemm, 16 tokens, Q4_K 14336x4096 (rotated copies as above)
     x16 = synth.activations(16, in_dim, seed=6)
-    dtg, reps = _time_calls(lambda: o.gemm(Q4K, x16, data, in_dim, out_dim, 16), share)
+
+    def gemm_rot():
+        o.gemm(Q4K, x16, copies[rot[0] % n_copies], in_dim, out_dim, 16)
+        rot[0] += 1
+
+    dtg, reps = _time_calls(gemm_rot, share)
     legs["q4_k_14336x4096_gemm_n16"] = {"GB_s": round(data.nbytes / dtg / 1e9, 2), "ms": round(dtg * 1e3, 2),
                                         "tokens_per_s": round(16 / dtg, 1), "cores": cores, "reps": reps}
-    del x16, wbuf
-    # the 8B decode step's GEMVs: one layer's 7 matrices (x 32 layers) + the head
+    del x16, wbuf, copies
+    # the 8B decode step's GEMVs: one layer's 7 matrices (x 32 layers) + the
+    # head; layers alternate between weight sets covering twice the LLC
     cfg = ModelConfig()
     mats = [(cfg.type_of(n), oo, ii, synth.weights(cfg.type_of(n), oo, ii, seed=20261300 + k))
             for k, (n, oo, ii) in enumerate(cfg.mats())]
+    layer_bytes = sum(d.nbytes for _, _, _, d in mats)
+    n_sets = max(2, -(-2 * max(llc, 1) // layer_bytes))
+    sets = [mats] + [[(t, oo, ii, d.copy()) for t, oo, ii, d in mats] for _ in range(n_sets - 1)]
     xs = {ii: synth.activations(1, ii, seed=ii)[0] for _, _, ii, _ in mats}
 
     def layer():
-        for t, oo, ii, d in mats:
+        for t, oo, ii, d in sets[rot[0] % n_sets]:
             o.gemv(t, xs[ii], d, ii, oo)
+        rot[0] += 1
 
     dtl, reps = _time_calls(layer, share * 0.6)
     head = synth.weights(cfg.type_of("head"), cfg.vocab, cfg.hidden, seed=20261399)

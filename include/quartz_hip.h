@@ -234,6 +234,32 @@ int hip_h2d(void* dst, const void* src, size_t bytes);
 int hip_d2h(void* dst, const void* src, size_t bytes);
 int hip_sync(void);
 int hip_mem_info(size_t* free_b, size_t* total_b);
+/* Copies ordered on a stream (no counterpart in the reference, whose copies are
+ * blocking); with pageable host memory they return once the source is read. */
+int hip_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int hip_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
+
+/* Streams and HIP graphs through the C ABI (no counterpart in the reference,
+ * which launches every kernel eagerly): a host that reaches HIP only through
+ * this library records a decode step once and replays it per token.
+ *   hip_stream_create: a new non-blocking stream at the default priority;
+ *   hip_graph_begin: start capturing `stream` (not the null stream; thread-local
+ *     capture mode); every _async call on it is recorded, not run;
+ *   hip_graph_end: stop, instantiate, and return the executable graph in *exec;
+ *   hip_graph_launch: replay it on a stream; hip_graph_destroy frees it.
+ * A captured call keeps the argument values it was given.  To replay one step
+ * at consecutive positions, capture the _dev entries (hip_attention_step_dev_async,
+ * hip_embed_lookup_dev_async), which read the position and the token ids from
+ * device memory at run time: write them (hip_h2d_async) before each replay, or
+ * end the step with hip_greedy_next_async, which writes the next token and
+ * advances the position on the device. */
+int hip_stream_create(void** stream);
+int hip_stream_sync(void* stream);
+void hip_stream_destroy(void* stream);
+int hip_graph_begin(void* stream);
+int hip_graph_end(void* stream, void** exec);
+int hip_graph_launch(void* exec, void* stream);
+void hip_graph_destroy(void* exec);
 
 /* IQ codebooks.  Replace cuda_set_iq3s_grid / _iq2s_grid / _iq2xxs_grid /
  * _iq2xs_grid / cuda_set_ksigns (src/cuda_kernels.cu:1027-1041).  The library is
@@ -389,6 +415,17 @@ int hip_attention_step_batched_async(float* out, const float* q, const float* k,
                                      float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
                                      int n_kv_heads, int head_dim, int kv_dim, int pos, float theta, float yarn_scale,
                                      int yarn_orig_ctx, int neox, float scale, void* stream);
+/* hip_attention_step_batched_async with the position read from device memory
+ * when the kernel runs (*d_pos, clamped to [0, max_pos] as forward_gpu_step
+ * clamps pos to max_seq - 1, src/cuda.rs:517-520), so one captured launch serves
+ * every position.  The launch is sized for max_pos (cache_stride >= (max_pos+1)
+ * * kv_dim when n_seq > 1); workgroups beyond the split of the actual position
+ * exit at once, and the arithmetic equals the host-position call's bit for bit.
+ * No counterpart in the reference (pos is a host argument there). */
+int hip_attention_step_dev_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                                 float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                                 int n_kv_heads, int head_dim, int kv_dim, const int* d_pos, int max_pos, float theta,
+                                 float yarn_scale, int yarn_orig_ctx, int neox, float scale, void* stream);
 int hip_embed_lookup(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim);
 int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type, int token, int embed_dim,
                            void* stream);
@@ -399,6 +436,18 @@ int hip_embed_lookup_async(float* out, const uint8_t* d_data, uint32_t ggml_type
  * sequences together. */
 int hip_embed_lookup_batched_async(float* out, size_t out_stride, const uint8_t* d_data, uint32_t ggml_type,
                                    const int* tokens, int n_tok, int embed_dim, void* stream);
+/* hip_embed_lookup_batched_async with the n_tok token ids read from device
+ * memory (d_tokens) when the kernel runs; an id outside [0, n_vocab) gives a row
+ * of zeros.  No counterpart in the reference (the token is a host argument). */
+int hip_embed_lookup_dev_async(float* out, size_t out_stride, const uint8_t* d_data, uint32_t ggml_type,
+                               const int* d_tokens, int n_tok, int n_vocab, int embed_dim, void* stream);
+/* Greedy sampling on the device: d_tokens[r] = the index of the largest of the
+ * n logits of row r (rows at logits + r * row_stride) in f32::total_cmp order,
+ * the last one among equal maxima -- the reference's temperature <= 0 arm
+ * (src/main.rs:1684-1692, max_by over total_cmp).  If d_pos is non-null,
+ * *d_pos += 1 after the rows are read, so a captured step feeds itself. */
+int hip_greedy_next_async(const float* logits, size_t row_stride, int rows, int n, int* d_tokens, int* d_pos,
+                          void* stream);
 
 /* ---------------------------------------------------------------- GGUF
  * Reader for the weight container either side of the GEMV path: GgufFile

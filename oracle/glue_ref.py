@@ -20,6 +20,8 @@ the step built on it; only tests/ import it.
                                        top k, softmax over the k (renorm) or over
                                        all experts (OLMoE); weights in f32 as
                                        the reference computes them.
+  greedy_next     src/main.rs:1684-1692: the temperature <= 0 arm, max_by over
+                                       total_cmp (the last of equal maxima).
   moe_ffn         src/main.rs:995-1040: per chosen expert gate/up (+ biases),
                                        SwiGLU (plain or OAI), down (+ bias),
                                        output += w * down, in float64.
@@ -31,7 +33,8 @@ and to 1 - p_sink with one; attention over one cached token returns that
 token's value; swiglu(0, .) = 0 and swiglu(g, 1) = silu(g); the OAI form
 clamps at 7; moe_route's order against numpy's stable argsort on distinct
 values, -0 < +0 and NaN placement by sign, k = n_exp weights summing to 1, and
-the OLMoE weights against a float64 softmax; moe_ffn with one expert of weight
+the OLMoE weights against a float64 softmax; greedy_next against numpy's
+argmax on distinct finite values, with ties, +-0, +-inf and NaNs by hand; moe_ffn with one expert of weight
 1 against the dense FFN.  forward_step as a composition is pinned by
 tests/test_forward_step_ref.py: at pos 0 the output ignores q/k and attention
 returns each group's v; zero o/down weights keep the hidden state and leave
@@ -137,6 +140,18 @@ def total_order_key(v):
     magnitude bits of negative values, then compare as signed 32-bit)."""
     b = struct.unpack("<i", struct.pack("<f", float(np.float32(v))))[0]
     return b ^ ((b >> 31) & 0x7FFFFFFF)
+
+
+def greedy_next(logits):
+    """Greedy token (src/main.rs:1684-1692): Iterator::max_by with total_cmp,
+    which keeps the later element when two compare equal, so among equal
+    maxima the last index wins; NaN with the sign bit clear orders above +inf."""
+    best, best_key = 0, None
+    for i, v in enumerate(np.asarray(logits, np.float32)):
+        k = total_order_key(v)
+        if best_key is None or k >= best_key:
+            best, best_key = i, k
+    return best
 
 
 def moe_route(logits, k, renorm=True, bias=None):

@@ -142,6 +142,22 @@ _SIGS = {
     "hip_embed_lookup_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_void_p]),
     "hip_embed_lookup_batched_async": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int,
                                                  C.c_int, C.c_void_p]),
+    "hip_embed_lookup_dev_async": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int,
+                                             C.c_int, C.c_int, C.c_void_p]),
+    "hip_attention_step_dev_async": (C.c_int, [C.c_void_p] * 7 + [C.c_int, C.c_size_t] + [C.c_int] * 4 +
+                                     [C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int, C.c_float,
+                                      C.c_void_p]),
+    "hip_greedy_next_async": (C.c_int, [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                        C.c_void_p]),
+    "hip_h2d_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "hip_d2h_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "hip_stream_create": (C.c_int, [C.c_void_p]),
+    "hip_stream_sync": (C.c_int, [C.c_void_p]),
+    "hip_stream_destroy": (None, [C.c_void_p]),
+    "hip_graph_begin": (C.c_int, [C.c_void_p]),
+    "hip_graph_end": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "hip_graph_launch": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "hip_graph_destroy": (None, [C.c_void_p]),
     "hip_attn_score": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     "hip_softmax_sink": (C.c_int, [C.c_void_p, C.c_int, C.c_float]),
     "hip_attn_values": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int]),

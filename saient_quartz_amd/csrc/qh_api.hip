@@ -806,10 +806,10 @@ int hip_attention_decode(float* out, const float* q, const float* k_cache, const
                                       scale, nullptr);
 }
 
-int hip_attention_step_batched_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
-                                     float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
-                                     int n_kv_heads, int head_dim, int kv_dim, int pos, float theta, float yarn_scale,
-                                     int yarn_orig_ctx, int neox, float scale, void* s) {
+static int qh_attention_step(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                             float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                             int n_kv_heads, int head_dim, int kv_dim, int pos, const int* d_pos, float theta,
+                             float yarn_scale, int yarn_orig_ctx, int neox, float scale, void* s) {
     if (pos < 0 || n_seq < 0) return QH_ERR_DIMS;
     int rc = qh_attn_dims(n_heads, n_kv_heads, pos + 1, head_dim, kv_dim, pos + 1);
     if (rc) return rc;
@@ -819,10 +819,27 @@ int hip_attention_step_batched_async(float* out, const float* q, const float* k,
     if (!out || !q || !k || !v || !k_cache || !v_cache) return QH_ERR_NULL;
     hipError_t e = qh_glue_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_heads, n_kv_heads, head_dim,
                                           kv_dim, pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, (hipStream_t)s,
-                                          n_seq, cache_stride);
+                                          n_seq, cache_stride, d_pos);
     if (e == hipErrorNotSupported) return QH_ERR_RANGE;
     if (e != hipSuccess) return qh_fail(e, "hip_attention_step");
     return QH_OK;
+}
+
+int hip_attention_step_batched_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                                     float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                                     int n_kv_heads, int head_dim, int kv_dim, int pos, float theta, float yarn_scale,
+                                     int yarn_orig_ctx, int neox, float scale, void* s) {
+    return qh_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_seq, cache_stride, n_heads, n_kv_heads,
+                             head_dim, kv_dim, pos, nullptr, theta, yarn_scale, yarn_orig_ctx, neox, scale, s);
+}
+
+int hip_attention_step_dev_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
+                                 float* v_cache, const float* sinks, int n_seq, size_t cache_stride, int n_heads,
+                                 int n_kv_heads, int head_dim, int kv_dim, const int* d_pos, int max_pos, float theta,
+                                 float yarn_scale, int yarn_orig_ctx, int neox, float scale, void* s) {
+    if (!d_pos && n_heads > 0 && n_seq > 0) return QH_ERR_NULL;
+    return qh_attention_step(out, q, k, v, k_cache, v_cache, sinks, n_seq, cache_stride, n_heads, n_kv_heads,
+                             head_dim, kv_dim, max_pos, d_pos, theta, yarn_scale, yarn_orig_ctx, neox, scale, s);
 }
 
 int hip_attention_step_async(float* out, const float* q, const float* k, const float* v, float* k_cache,
@@ -902,6 +919,26 @@ int hip_embed_lookup_batched_async(float* out, size_t out_stride, const uint8_t*
     QH_GLUE(qh_glue_embed(out, out_stride, data, ggml_type, tokens, n_tok, embed_dim, (hipStream_t)s),
             "hip_embed_lookup_batched");
 }
+int hip_embed_lookup_dev_async(float* out, size_t out_stride, const uint8_t* data, uint32_t ggml_type,
+                               const int* d_tokens, int n_tok, int n_vocab, int embed_dim, void* s) {
+    const int qk = qh_block_elems(ggml_type);
+    if (qk == 0) return QH_ERR_TYPE;
+    if (n_tok < 0 || n_vocab < 0 || embed_dim <= 0 || embed_dim % qk ||
+        (n_tok > 1 && out_stride < (size_t)embed_dim))
+        return QH_ERR_DIMS;
+    if (n_tok == 0) return QH_OK;
+    if (!out || !data || !d_tokens) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_embed(out, out_stride, data, ggml_type, nullptr, n_tok, embed_dim, (hipStream_t)s, d_tokens,
+                          n_vocab),
+            "hip_embed_lookup_dev");
+}
+int hip_greedy_next_async(const float* logits, size_t row_stride, int rows, int n, int* d_tokens, int* d_pos,
+                          void* s) {
+    if (rows < 0 || n < 0 || (rows > 1 && row_stride < (size_t)n)) return QH_ERR_DIMS;
+    if (rows == 0 || n == 0) return QH_OK;
+    if (!logits || !d_tokens) return QH_ERR_NULL;
+    QH_GLUE(qh_glue_greedy(logits, row_stride, rows, n, d_tokens, d_pos, (hipStream_t)s), "hip_greedy_next");
+}
 int hip_embed_lookup(float* out, const uint8_t* data, uint32_t ggml_type, int token, int embed_dim) {
     return hip_embed_lookup_async(out, data, ggml_type, token, embed_dim, nullptr);
 }
@@ -935,6 +972,17 @@ int hip_h2d(void* dst, const void* src, size_t bytes) {
     return QH_OK;
 }
 
+int hip_h2d_async(void* dst, const void* src, size_t bytes, void* s) {
+    if (bytes && (!dst || !src)) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)s), "hip_h2d_async");
+    return QH_OK;
+}
+int hip_d2h_async(void* dst, const void* src, size_t bytes, void* s) {
+    if (bytes && (!dst || !src)) return QH_ERR_NULL;
+    QH_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)s), "hip_d2h_async");
+    return QH_OK;
+}
+
 int hip_d2h(void* dst, const void* src, size_t bytes) {
     QH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hip_d2h");
     return QH_OK;
@@ -947,6 +995,49 @@ int hip_timestamp_async(uint64_t* dst, void* stream) {
     hipLaunchKernelGGL(qh_timestamp_k, dim3(1), dim3(1), 0, (hipStream_t)stream, dst);
     QH_CHECK(hipGetLastError(), "hip_timestamp_async");
     return QH_OK;
+}
+
+// Stream capture into a HIP graph for hosts that drive the library through
+// the C ABI only (hipStreamBeginCapture / hipStreamEndCapture /
+// hipGraphInstantiate / hipGraphLaunch).
+int hip_graph_begin(void* stream) {
+    if (!stream) return QH_ERR_NULL;  // the null stream cannot be captured
+    QH_CHECK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal), "hip_graph_begin");
+    return QH_OK;
+}
+int hip_graph_end(void* stream, void** exec) {
+    if (!stream || !exec) return QH_ERR_NULL;
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    QH_CHECK(hipStreamEndCapture((hipStream_t)stream, &g), "hip_graph_end");
+    hipGraphExec_t x = nullptr;
+    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    QH_CHECK(e, "hip_graph_end");
+    *exec = (void*)x;
+    return QH_OK;
+}
+int hip_graph_launch(void* exec, void* stream) {
+    if (!exec) return QH_ERR_NULL;
+    QH_CHECK(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream), "hip_graph_launch");
+    return QH_OK;
+}
+void hip_graph_destroy(void* exec) {
+    if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+int hip_stream_create(void** stream) {
+    if (!stream) return QH_ERR_NULL;
+    hipStream_t st = nullptr;
+    QH_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hip_stream_create");
+    *stream = (void*)st;
+    return QH_OK;
+}
+int hip_stream_sync(void* stream) {
+    QH_CHECK(hipStreamSynchronize((hipStream_t)stream), "hip_stream_sync");
+    return QH_OK;
+}
+void hip_stream_destroy(void* stream) {
+    if (stream) (void)hipStreamDestroy((hipStream_t)stream);
 }
 
 int hip_wallclock_khz(void) {

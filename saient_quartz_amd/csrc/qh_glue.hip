@@ -11,6 +11,7 @@
 // results differ from the reference's only by summation order.
 // hip_attention_decode fuses the three attention kernels into one launch per
 // step (scores and probabilities stay in LDS).
+#include <climits>
 #include "qh_internal.h"
 
 // Sum / max over the 64 lanes of a wavefront (every lane gets the result).
@@ -145,16 +146,18 @@ struct QgRot {
 };
 QH_DEV QgRot qg_rope_rot(int i, int head_dim, int pos, float theta, float yarn_scale, int yarn_orig_ctx, int neox) {
     const int half = head_dim >> 1;
-    const float std_inv = 1.f / powf(theta, 2.f * (float)i / (float)head_dim);
-    float eff_inv = std_inv;
+    // base angular rate of pair i; with YaRN, pairs whose period lies between
+    // orig_ctx / 32 and orig_ctx blend linearly towards rate / yarn_scale
+    const float base_rate = 1.f / powf(theta, 2.f * (float)i / (float)head_dim);
+    float rate = base_rate;
     if (yarn_scale > 1.f && yarn_orig_ctx > 0) {
-        const float hfw = (float)yarn_orig_ctx / 32.f, lfw = (float)yarn_orig_ctx / 1.f;
-        const float wavelen = 2.f * 3.14159265358979f / std_inv;
-        const float ramp = fmaxf(0.f, fminf(1.f, (lfw - wavelen) / (lfw - hfw)));
-        eff_inv = ramp * std_inv + (1.f - ramp) * (std_inv / yarn_scale);
+        const float short_ctx = (float)yarn_orig_ctx / 32.f, long_ctx = (float)yarn_orig_ctx / 1.f;
+        const float period = 2.f * 3.14159265358979f / base_rate;
+        const float keep = fmaxf(0.f, fminf(1.f, (long_ctx - period) / (long_ctx - short_ctx)));
+        rate = keep * base_rate + (1.f - keep) * (base_rate / yarn_scale);
     }
     QgRot r;
-    sincosf((float)pos * eff_inv, &r.s, &r.c);
+    sincosf((float)pos * rate, &r.s, &r.c);
     r.i0 = neox ? i : 2 * i;
     r.i1 = neox ? i + half : 2 * i + 1;
     return r;
@@ -308,6 +311,27 @@ __global__ __launch_bounds__(256) void qg_attention_decode(float* out, const flo
 static __device__ __align__(256) float qa_part[QA_PART];
 static __device__ __align__(256) unsigned int qa_cnt[QA_MAXKV];
 
+// Workgroups per kv head (slices of 32 rows shared out) for a step at row pos:
+// more workgroups until the merge of their partials costs more than the slices
+// they take over (measured on MI355X: 1 slice each up to 16 slices, 2 up to 64,
+// then 4).  Several sequences: at least two slices per workgroup and at most
+// 512 workgroups in all (position 511: 16 sequences 4.73 -> 4.48 ms per step
+// with 4 slices per workgroup, 4 sequences 2.98 -> 2.90 with 2).  per_force > 0
+// fixes the slices per workgroup.  The host sizes a launch with it, and a launch
+// that reads pos on the device recomputes it there, so both split alike.
+__host__ __device__ inline int qa_nch(int pos, int n_seq, int n_kv, int n_heads, int hd, int per_force) {
+    const int slices = (pos + QA_ROWS) / QA_ROWS;
+    int per = per_force ? per_force : (slices <= 16 ? 1 : (slices <= 64 ? 2 : 4));
+    if (!per_force && n_seq > 1) {
+        if (per < 2 && slices > 1) per = 2;
+        while (per < slices && (int64_t)n_kv * n_seq * ((slices + per - 1) / per) > 512) per *= 2;
+    }
+    int nch = (slices + per - 1) / per;
+    nch = nch < QA_MAXCH ? nch : QA_MAXCH;
+    const int cap = QA_PART / (n_seq * n_heads * (hd + 2));
+    return nch < cap ? nch : cap;
+}
+
 // HD: head_dim capacity, 128 or QA_MAXHD (LDS, so occupancy, scales with it);
 // GW: q heads per wavefront (1, 2 or 4: groups of up to 4, 8 or QA_MAXG heads).
 template <int HD, int GW>
@@ -315,14 +339,25 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
                                                          float* kc, float* vc, const float* sinks, int n_heads,
                                                          int n_kv, int hd, int kv_dim, int pos, float theta,
                                                          float yarn_scale, int orig_ctx, int neox, float scale,
-                                                         float* part, unsigned int* cnt, size_t cache_stride) {
+                                                         float* part, unsigned int* cnt, size_t cache_stride,
+                                                         const int* pos_dev, int per_force) {
     __shared__ __align__(16) float kl[QA_ROWS * (HD + 4)];
     __shared__ __align__(16) float vl[QA_ROWS * HD];
     __shared__ __align__(16) float qr[QA_MAXG * HD];
     __shared__ __align__(16) float kr[HD];
     __shared__ __align__(16) float vr[HD];
     __shared__ int last_flag;
-    const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    const int g = blockIdx.x, c = blockIdx.y;
+    int nch = gridDim.y;
+    if (pos_dev) {
+        // the position comes from device memory (a step replayed from one graph
+        // at consecutive positions): `pos` is the launch's bound, and the
+        // reference clamps to the cache (src/cuda.rs:517-520); workgroups past
+        // this position's split exit at once
+        pos = min(max(*pos_dev, 0), pos);
+        nch = qa_nch(pos, gridDim.z, n_kv, n_heads, hd, per_force);
+        if (c >= nch) return;
+    }
     // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
     {
         const size_t z = blockIdx.z;
@@ -584,13 +619,22 @@ __global__ __launch_bounds__(256) void qg_swiglu_oai(float* out, const float* ga
 struct QgToks { int t[QG_EMB_TOKS]; };
 __global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t* data, uint32_t type,
                                                        const QgToks toks, size_t out_stride, int embed_dim, int qk,
-                                                       uint32_t bb, int bpw) {
+                                                       uint32_t bb, int bpw, const int* tok_dev, int vocab) {
     __shared__ __align__(16) uint8_t raw[QG_EMB_RAW];
     __shared__ __align__(16) float dec[QG_EMB_OUT];
-    const int token = toks.t[blockIdx.y];
     out += (size_t)blockIdx.y * out_stride;
     const int nb = embed_dim / qk, b0 = blockIdx.x * bpw;
     const int nbw = min(bpw, nb - b0);
+    int token = toks.t[blockIdx.y];
+    if (tok_dev) {
+        // token ids from device memory (a step replayed from one graph): an id
+        // outside the table gives a zero row instead of a read past it
+        token = tok_dev[blockIdx.y];
+        if (token < 0 || token >= vocab) {
+            for (int i = threadIdx.x; i < nbw * qk; i += 256) out[(size_t)b0 * qk + i] = 0.f;
+            return;
+        }
+    }
     const uint8_t* src = data + ((size_t)token * nb + b0) * bb;
     for (int i = threadIdx.x; i < nbw * (int)bb; i += 256) raw[i] = src[i];
     __syncthreads();
@@ -598,6 +642,53 @@ __global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t
     __syncthreads();
     float* o = out + (size_t)b0 * qk;
     for (int i = threadIdx.x; i < nbw * qk; i += 256) o[i] = dec[i];
+}
+
+// Greedy next token of each of `rows` logit rows: the reference's temperature
+// <= 0 arm (src/main.rs:1684-1692), max_by(total_cmp), which returns the last
+// of equal maxima.  Key of a value: its bits with the magnitude flipped when
+// negative (f32::total_cmp's order as a signed compare), joined with the index
+// so one signed 64-bit max picks the largest key and, among equal keys, the
+// largest index.  One workgroup per row; tokens[r] = the index, and pos (if
+// non-null) advances by one, so a captured step can feed the next one.
+__device__ __forceinline__ long long qg_greedy_key(float v, int i) {
+    const int b = __float_as_int(v);
+    const int key = b ^ ((b >> 31) & 0x7FFFFFFF);
+    return ((long long)key << 32) | (unsigned)i;
+}
+__global__ __launch_bounds__(1024) void qg_greedy(const float* logits, size_t stride, int n, int* tokens, int* pos) {
+    __shared__ long long best_w[16];
+    const float* x = logits + (size_t)blockIdx.x * stride;
+    long long best = LLONG_MIN;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = x[min(i0 + u * 1024, n - 1)];  // all eight loads in flight
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(i0 + u * 1024, n - 1);  // a clamped repeat of the last value changes nothing
+            const long long kk = qg_greedy_key(v[u], i);
+            best = kk > best ? kk : best;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) best_w[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = best_w[w] > best ? best_w[w] : best;
+        tokens[blockIdx.x] = (int)(unsigned)(best & 0xFFFFFFFFll);
+        if (pos && blockIdx.x == 0) pos[0] += 1;
+    }
+}
+
+hipError_t qh_glue_greedy(const float* logits, size_t stride, int rows, int n, int* tokens, int* pos, hipStream_t st) {
+    if (rows <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(qg_greedy, dim3((unsigned)rows), dim3(1024), 0, st, logits, stride, n, tokens, pos);
+    return hipGetLastError();
 }
 
 static unsigned qg_blocks(int n) { return (unsigned)((n + 255) / 256); }
@@ -688,7 +779,7 @@ static const QaScratch* qa_scratch_ptrs() {
 hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
                                   const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
                                   float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st, int n_seq,
-                                  size_t cache_stride) {
+                                  size_t cache_stride, const int* pos_dev) {
     if (pos < 0 || hd <= 0 || (hd & 3) || hd > QA_MAXHD || n_seq < 1 || n_kv * n_seq > QA_MAXKV || (kv_dim & 3) ||
         (cache_stride & 3) || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15))
         return hipErrorNotSupported;
@@ -697,33 +788,28 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
     if ((n_heads + n_kv - 1) / n_kv > QA_MAXG) return hipErrorNotSupported;
     const QaScratch* sc = qa_scratch_ptrs();
     if (!sc) return hipErrorInvalidDevice;
-    const int slices = (pos + QA_ROWS) / QA_ROWS;
-    // 32-row slices per workgroup: more workgroups until the merge of their
-    // partials costs more than the slices they take over (measured on MI355X:
-    // 1 up to 16 slices, 2 up to 64, then 4).  QUARTZ_HIP_ATTN_SLICES=k forces k.
+    // QUARTZ_HIP_ATTN_SLICES=k forces k slices per workgroup
     static const int env_per = [] {
         const char* e = getenv("QUARTZ_HIP_ATTN_SLICES");
         return e && atoi(e) > 0 ? atoi(e) : 0;
     }();
-    int per = env_per ? env_per : (slices <= 16 ? 1 : (slices <= 64 ? 2 : 4));
-    if (!env_per && n_seq > 1) {
-        // several sequences: fatter workgroups, at most 512 in all and at least
-        // two slices each (measured at position 511: 16 sequences 4.73 -> 4.48 ms
-        // per step with 4 slices per workgroup, 4 sequences 2.98 -> 2.90 with 2)
-        if (per < 2 && slices > 1) per = 2;
-        while (per < slices && (int64_t)n_kv * n_seq * ((slices + per - 1) / per) > 512) per *= 2;
+    // pos_dev: the grid covers the largest split of any position up to pos
+    int nch = 0;
+    if (pos_dev) {
+        for (int sl = 1; sl <= pos / QA_ROWS + 1; sl++) {
+            const int c = qa_nch(sl * QA_ROWS - 1, n_seq, n_kv, n_heads, hd, env_per);
+            nch = c > nch ? c : nch;
+        }
+    } else {
+        nch = qa_nch(pos, n_seq, n_kv, n_heads, hd, env_per);
     }
-    int nch = (slices + per - 1) / per;
-    nch = nch < QA_MAXCH ? nch : QA_MAXCH;
-    const int cap = QA_PART / (n_seq * n_heads * (hd + 2));
-    if (nch > cap) nch = cap;
     if (nch < 1) return hipErrorNotSupported;
     const int gmax = (n_heads + n_kv - 1) / n_kv;
     auto launch = [&](auto HDC, auto GWC) {
         constexpr int H = decltype(HDC)::value, G = decltype(GWC)::value;
         hipLaunchKernelGGL((qg_attention_step<H, G>), dim3(n_kv, nch, n_seq), dim3(256), 0, st, out, q, k, v, kc, vc,
                            sinks, n_heads, n_kv, hd, kv_dim, pos, theta, yarn_scale, orig_ctx, neox, scale, sc->part,
-                           sc->cnt, cache_stride);
+                           sc->cnt, cache_stride, pos_dev, env_per);
     };
     using I128 = std::integral_constant<int, 128>;
     using IMAX = std::integral_constant<int, QA_MAXHD>;
@@ -750,7 +836,7 @@ hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* u
 }
 
 hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uint32_t type, const int* tokens,
-                         int n_tok, int embed_dim, hipStream_t st) {
+                         int n_tok, int embed_dim, hipStream_t st, const int* tok_dev, int vocab) {
     const int qk = qh_block_elems(type);
     const uint32_t bb = qh_block_bytes(type);
     const int nb = embed_dim / qk;
@@ -760,9 +846,11 @@ hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uin
     for (int t0 = 0; t0 < n_tok; t0 += QG_EMB_TOKS) {
         const int c = n_tok - t0 < QG_EMB_TOKS ? n_tok - t0 : QG_EMB_TOKS;
         QgToks toks = {};
-        for (int i = 0; i < c; i++) toks.t[i] = tokens[t0 + i];
+        if (!tok_dev)
+            for (int i = 0; i < c; i++) toks.t[i] = tokens[t0 + i];
         hipLaunchKernelGGL(qg_embed_lookup, dim3((unsigned)((nb + bpw - 1) / bpw), (unsigned)c), dim3(256), 0, st,
-                           out + (size_t)t0 * out_stride, data, type, toks, out_stride, embed_dim, qk, bb, bpw);
+                           out + (size_t)t0 * out_stride, data, type, toks, out_stride, embed_dim, qk, bb, bpw,
+                           tok_dev ? tok_dev + t0 : nullptr, vocab);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -106,7 +106,8 @@ hipError_t qh_glue_attention_decode(float* out, const float* q, const float* kc,
 hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
                                   const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
                                   float yarn_scale, int orig_ctx, int neox, float scale, hipStream_t st, int n_seq = 1,
-                                  size_t cache_stride = 0);
+                                  size_t cache_stride = 0, const int* pos_dev = nullptr);
+hipError_t qh_glue_greedy(const float* logits, size_t stride, int rows, int n, int* tokens, int* pos, hipStream_t st);
 hipError_t qh_launch_gemm_f32(const float* W, const float* x, float* y, int in_dim, int out_dim, int n,
                               hipStream_t st);
 hipError_t qh_moe_route(const float* logits, const float* bias, int n_tok, int ne, int k, int renorm, int* ids,
@@ -120,5 +121,6 @@ hipError_t qh_moe_combine(float* out, const float* yg, const int* slot_of, const
                           const float* db, int n_tok, int k, int d, int accumulate, hipStream_t st);
 hipError_t qh_glue_swiglu(int oai, float* out, const float* gate, const float* up, int n, hipStream_t st);
 hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uint32_t type, const int* tokens,
-                         int n_tok, int embed_dim, hipStream_t st);  // hip_last_error() text
+                         int n_tok, int embed_dim, hipStream_t st, const int* tok_dev = nullptr,
+                         int vocab = 0);
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);

@@ -30,6 +30,22 @@ from .host import (gemm_group_norm_async, gemm_grouped_async, gemm_grouped_ex_as
 Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_S = 12, 13, 14, 16, 21
 
 
+def _write_state(L, state, values, stream):
+    """hip_h2d_async of int32 values into a step's device state, ordered on the
+    stream (a pageable source: the call returns once it is read)."""
+    buf = (C.c_int * len(values))(*[int(v) for v in values])
+    check("hip_h2d_async", L.hip_h2d_async(state.data_ptr(), buf, 4 * len(values), _stream_ptr(stream)))
+    return buf
+
+
+def _stream_ptr(stream):
+    """A torch stream, a raw hipStream_t (int, e.g. from hip_stream_create) or
+    None (torch's current stream) -> the raw handle the C ABI takes."""
+    if isinstance(stream, int):
+        return stream
+    return (stream or torch.cuda.current_stream()).cuda_stream
+
+
 @dataclass(frozen=True)
 class Shape:
     hidden: int = 4096
@@ -86,7 +102,7 @@ class DecodeStep:
         each: q+k (Q4_K) and gate+up (Q4_K), through hip_gemv_multi at n = 1 and
         hip_gemm_grouped (one x digitisation, one weight launch) at n > 1."""
         assert 1 <= n <= self.n_max
-        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        sp = _stream_ptr(stream)
         names = [m[0] for m in self.shape.layer_mats()]
         for mats in self.layers:
             by = dict(zip(names, mats))
@@ -149,7 +165,7 @@ class MoeLayer:
         return w.data_ptr() + e * self.slice
 
     def issue(self, stream=None, grouped: bool = True):
-        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        sp = _stream_ptr(stream)
         t, n, h, f, E = self.t, self.n, self.h, self.f, self.E
         if grouped:
             xs = [self.x[e].data_ptr() for e in range(E)]
@@ -364,6 +380,16 @@ class ForwardStep:
         self.kc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
         self.vc = [torch.zeros(c.max_seq * kvd, **f32) for _ in range(c.layers)]
         self.scale = 1.0 / math.sqrt(c.head_dim)
+        # device-side step state [token, pos] read by issue(dev=True)
+        self.state = torch.zeros(2, dtype=torch.int32, device="cuda")
+
+    def set_state(self, token: int, pos: int, stream=None):
+        """Write the token and position a dev=True step reads (outside any graph)."""
+        self._state_src = _write_state(self.L, self.state, [token, pos], stream)  # kept alive until the next write
+
+    def embed_rows(self) -> int:
+        from . import type_size
+        return self.w["embed"].numel() // type_size(self.cfg.type_of("embed"), self.cfg.hidden)
 
     @staticmethod
     def random_weights(cfg: ModelConfig, seed: int = 20261204) -> dict:
@@ -375,8 +401,7 @@ class ForwardStep:
             for j, (n, o, i) in enumerate(cfg.mats()):
                 w[n].append(synth_device.weights(cfg.type_of(n), o, i, seed + 16 * l + j))
         w["head"] = synth_device.weights(cfg.type_of("head"), cfg.vocab, cfg.hidden, seed - 1)
-        # the lookup touches one row; a small table keeps the bench's memory down
-        w["embed"] = synth_device.weights(cfg.type_of("embed"), min(cfg.vocab, 1024), cfg.hidden, seed - 2)
+        w["embed"] = synth_device.weights(cfg.type_of("embed"), cfg.vocab, cfg.hidden, seed - 2)
         norm = lambda: (1.0 + 0.1 * torch.randn(cfg.hidden, device="cuda", generator=g))
         w["attn_norm"] = [norm() for _ in range(cfg.layers)]
         w["ffn_norm"] = [norm() for _ in range(cfg.layers)]
@@ -391,21 +416,40 @@ class ForwardStep:
                          norm_ptr=None if norm is None else norm.data_ptr(), accumulate=accumulate,
                          scratch_ptr=self.scratch.data_ptr())
 
-    def issue(self, token: int, pos: int, stream=None, logits: bool = True):
-        """Enqueue one decode step (token at position pos) on `stream`."""
+    def issue(self, token: int = 0, pos: int = 0, stream=None, logits: bool = True, dev: bool = False,
+              greedy: bool = False):
+        """Enqueue one decode step (token at position pos) on `stream`.
+        dev: read the token and position from self.state when the kernels run
+        (set_state, or the previous step's greedy pick), so a captured step
+        replays at consecutive positions.  greedy (with logits): end with
+        hip_greedy_next, which writes the argmax token to state[0] and
+        advances state[1]."""
         c, L = self.cfg, self.L
-        assert 0 <= pos < c.max_seq
-        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        assert dev or 0 <= pos < c.max_seq
+        assert logits or not greedy
+        sp = _stream_ptr(stream)
         kvd = c.n_kv * c.head_dim
-        check("hip_embed_lookup_async", L.hip_embed_lookup_async(self.hidden.data_ptr(), self.w["embed"].data_ptr(),
-                                                                 c.type_of("embed"), token, c.hidden, sp))
+        tok_p, pos_p = self.state.data_ptr(), self.state.data_ptr() + 4
+        if dev:
+            check("hip_embed_lookup_dev_async", L.hip_embed_lookup_dev_async(
+                self.hidden.data_ptr(), c.hidden, self.w["embed"].data_ptr(), c.type_of("embed"), tok_p, 1,
+                self.embed_rows(), c.hidden, sp))
+        else:
+            check("hip_embed_lookup_async", L.hip_embed_lookup_async(
+                self.hidden.data_ptr(), self.w["embed"].data_ptr(), c.type_of("embed"), token, c.hidden, sp))
         for l in range(c.layers):
             self._fused(("q", "k", "v"), l, self.hidden, (self.q, self.k, self.v), c.hidden,
                         self.w["attn_norm"][l], False, sp)
-            check("hip_attention_step_async", L.hip_attention_step_async(
-                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
-                self.vc[l].data_ptr(), None, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta, 1.0, 0, c.neox,
-                self.scale, sp))
+            if dev:
+                check("hip_attention_step_dev_async", L.hip_attention_step_dev_async(
+                    self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                    self.kc[l].data_ptr(), self.vc[l].data_ptr(), None, 1, 0, c.n_heads, c.n_kv, c.head_dim, kvd,
+                    pos_p, c.max_seq - 1, c.theta, 1.0, 0, c.neox, self.scale, sp))
+            else:
+                check("hip_attention_step_async", L.hip_attention_step_async(
+                    self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                    self.kc[l].data_ptr(), self.vc[l].data_ptr(), None, c.n_heads, c.n_kv, c.head_dim, kvd, pos,
+                    c.theta, 1.0, 0, c.neox, self.scale, sp))
             self._fused(("o",), l, self.att, (self.hidden,), c.n_heads * c.head_dim, None, True, sp)
             if c.type_of("gate") == c.type_of("up"):
                 check("hip_gemv_swiglu_async", L.hip_gemv_swiglu_async(
@@ -420,6 +464,9 @@ class ForwardStep:
             self._fused(("down",), l, self.act, (self.hidden,), c.ffn, None, True, sp)
         if logits:
             self._fused(("head",), None, self.hidden, (self.logits,), c.hidden, self.w["out_norm"], False, sp)
+        if greedy:
+            check("hip_greedy_next_async", L.hip_greedy_next_async(self.logits.data_ptr(), c.vocab, 1, c.vocab, tok_p,
+                                                                   pos_p, sp))
 
 
 class BatchStep:
@@ -451,6 +498,12 @@ class BatchStep:
         self.scale = 1.0 / math.sqrt(c.head_dim)
         big = max(c.hidden, c.ffn, qd)
         self.scratch = torch.zeros(2 * n * big, **f32)  # fallback of hip_gemm_grouped_ex
+        # device-side step state [tokens[0..n), pos] read by issue(dev=True)
+        self.state = torch.zeros(n + 1, dtype=torch.int32, device="cuda")
+
+    def set_state(self, tokens, pos: int, stream=None):
+        """Write the tokens and position a dev=True step reads (outside any graph)."""
+        self._state_src = _write_state(self.L, self.state, list(tokens) + [pos], stream)
 
     def _gemm_res(self, name, layer, x, in_dim, sp, up=None):
         """hidden += W x (or W (silu(x) * up)) in one hip_gemm_grouped_ex call."""
@@ -489,24 +542,45 @@ class BatchStep:
                               norm.data_ptr(), [y.data_ptr() for y in ys], self.n, [y.shape[1] for y in ys],
                               self.cfg.hidden, sp, self.scratch.data_ptr())
 
-    def issue(self, tokens, pos: int, stream=None, logits: bool = True):
-        """Enqueue one lockstep decode step: sequence i takes tokens[i] at `pos`."""
+    def issue(self, tokens=None, pos: int = 0, stream=None, logits: bool = True, dev: bool = False,
+              greedy: bool = False):
+        """Enqueue one lockstep decode step: sequence i takes tokens[i] at `pos`.
+        dev / greedy: as ForwardStep.issue, with the n tokens and the shared
+        position in self.state."""
         c, L, n = self.cfg, self.L, self.n
-        assert len(tokens) == n and 0 <= pos < c.max_seq
-        sp = (stream or torch.cuda.current_stream()).cuda_stream
+        assert dev or (len(tokens) == n and 0 <= pos < c.max_seq)
+        assert logits or not greedy
+        sp = _stream_ptr(stream)
         kvd = c.n_kv * c.head_dim
         row = self.hidden.stride(0)
-        toks = (C.c_int * n)(*[int(t) for t in tokens])
-        check("hip_embed_lookup_batched_async", L.hip_embed_lookup_batched_async(
-            self.hidden.data_ptr(), row, self.w["embed"].data_ptr(), c.type_of("embed"), toks, n, c.hidden, sp))
+        tok_p, pos_p = self.state.data_ptr(), self.state.data_ptr() + 4 * n
+        if dev:
+            from . import type_size
+            rows = self.w["embed"].numel() // type_size(c.type_of("embed"), c.hidden)
+            check("hip_embed_lookup_dev_async", L.hip_embed_lookup_dev_async(
+                self.hidden.data_ptr(), row, self.w["embed"].data_ptr(), c.type_of("embed"), tok_p, n, rows,
+                c.hidden, sp))
+        else:
+            toks = (C.c_int * n)(*[int(t) for t in tokens])
+            check("hip_embed_lookup_batched_async", L.hip_embed_lookup_batched_async(
+                self.hidden.data_ptr(), row, self.w["embed"].data_ptr(), c.type_of("embed"), toks, n, c.hidden, sp))
         for l in range(c.layers):
             self._gemm_norm(("q", "k", "v"), l, self.w["attn_norm"][l], (self.q, self.k, self.v), sp)
-            check("hip_attention_step_batched_async", L.hip_attention_step_batched_async(
-                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.kc[l].data_ptr(),
-                self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv, c.head_dim, kvd, pos, c.theta,
-                1.0, 0, c.neox, self.scale, sp))
+            if dev:
+                check("hip_attention_step_dev_async", L.hip_attention_step_dev_async(
+                    self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                    self.kc[l].data_ptr(), self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv,
+                    c.head_dim, kvd, pos_p, c.max_seq - 1, c.theta, 1.0, 0, c.neox, self.scale, sp))
+            else:
+                check("hip_attention_step_batched_async", L.hip_attention_step_batched_async(
+                    self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                    self.kc[l].data_ptr(), self.vc[l].data_ptr(), None, n, self.cache_stride, c.n_heads, c.n_kv,
+                    c.head_dim, kvd, pos, c.theta, 1.0, 0, c.neox, self.scale, sp))
             self._gemm_res("o", l, self.att, c.n_heads * c.head_dim, sp)
             self._gemm_norm(("gate", "up"), l, self.w["ffn_norm"][l], (self.gate, self.up), sp)
             self._gemm_res("down", l, self.gate, c.ffn, sp, up=self.up)
         if logits:
             self._gemm_norm(("head",), None, self.w["out_norm"], (self.logits,), sp)
+        if greedy:
+            check("hip_greedy_next_async", L.hip_greedy_next_async(self.logits.data_ptr(), c.vocab, n, c.vocab, tok_p,
+                                                                   pos_p, sp))

@@ -107,6 +107,23 @@ def test_moe_route_order():
     assert list(ids) == [0]
 
 
+def test_greedy_next():
+    rng = np.random.default_rng(6)
+    for n in (1, 7, 1000):
+        v = rng.standard_normal(n).astype(np.float32)
+        assert g.greedy_next(v) == int(np.argmax(v))  # distinct values: the one maximum
+    # equal maxima: the last one (max_by keeps the later of equal elements)
+    assert g.greedy_next(np.array([1, 3, 2, 3, 0], np.float32)) == 3
+    assert g.greedy_next(np.zeros(9, np.float32)) == 8
+    # +0 above -0; +inf above every finite value; +NaN above +inf; -NaN below -inf
+    nan = np.float32(np.nan)
+    assert g.greedy_next(np.array([0.0, -0.0], np.float32)) == 0
+    assert g.greedy_next(np.array([5.0, np.inf, 1e38], np.float32)) == 1
+    assert g.greedy_next(np.array([np.inf, nan, 1.0], np.float32)) == 1
+    assert g.greedy_next(np.array([-np.inf, -nan, -1.0], np.float32)) == 2
+    assert g.greedy_next(np.array([-nan, -np.inf], np.float32)) == 1
+
+
 def test_moe_route_weights():
     rng = np.random.default_rng(4)
     v = (rng.standard_normal(16) * 3).astype(np.float32)

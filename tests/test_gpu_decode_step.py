@@ -38,7 +38,10 @@ MIXED_TYPES = (("q", Q5_K), ("k", Q4_K), ("v", Q8_0), ("o", Q6_K), ("gate", Q4_K
 
 
 def host_model(cfg, seed, realistic=False):
-    """Seeded GGUF-layout weights on the host (bytes); realistic: scales / 64."""
+    """Seeded GGUF-layout weights on the host (bytes); every f16 block scale
+    divided by 64 (realistic: a real checkpoint's weight size) or by 16 (four
+    times that: activations grow several-fold per layer, while every gate
+    pre-activation stays below 700, so the float64 oracle's exp stays finite)."""
     rng = np.random.default_rng(seed)
     raw, deq = {}, {}
     k = 0
@@ -46,16 +49,13 @@ def host_model(cfg, seed, realistic=False):
         raw[n], deq[n] = [], []
         for l in range(cfg.layers):
             t = cfg.type_of(n)
-            d = synth.weights(t, o, i, seed=seed + k)
-            if realistic:
-                d = realistic_scale(d, t)
+            d = realistic_scale(synth.weights(t, o, i, seed=seed + k), t, 64.0 if realistic else 16.0)
             k += 1
             raw[n].append(d)
             deq[n].append(d)
     for n, o in (("head", cfg.vocab), ("embed", cfg.vocab)):
-        raw[n] = synth.weights(cfg.type_of(n), o, cfg.hidden, seed=seed + k)
-        if realistic:
-            raw[n] = realistic_scale(raw[n], cfg.type_of(n))
+        raw[n] = realistic_scale(synth.weights(cfg.type_of(n), o, cfg.hidden, seed=seed + k), cfg.type_of(n),
+                                 64.0 if realistic else 16.0)
         k += 1
     norms = {"attn_norm": [1 + 0.1 * rng.standard_normal(cfg.hidden) for _ in range(cfg.layers)],
              "ffn_norm": [1 + 0.1 * rng.standard_normal(cfg.hidden) for _ in range(cfg.layers)],
@@ -73,12 +73,12 @@ _D_FIELDS = {12: (144, (0, 2)), 13: (176, (0, 2)), 14: (210, (208,)), 8: (34, (0
              10: (84, (80, 82))}
 
 
-def realistic_scale(data, t):
+def realistic_scale(data, t, div=64.0):
     bb, offs = _D_FIELDS[t]
     blk = data.reshape(-1, bb).copy()
     for o in offs:
         h = blk[:, o:o + 2].copy().view(np.float16)
-        blk[:, o:o + 2] = (h.astype(np.float32) / 64.0).astype(np.float16).view(np.uint8)
+        blk[:, o:o + 2] = (h.astype(np.float32) / div).astype(np.float16).view(np.uint8)
     return blk.reshape(-1)
 
 

@@ -74,10 +74,16 @@ def test_gemv_swiglu(qh, oracle, t, ffn, in_dim, norm):
     or through the separate kernels (Q8_0, in_dim past one workgroup's chunk)."""
     if ffn * in_dim > 14336 * 4096 and t != 12:
         pytest.skip("large shape only for Q4_K")
+    from test_gpu_decode_step import realistic_scale
     rng = np.random.default_rng(ffn + in_dim + t)
     x = (rng.standard_normal(in_dim) * 1.5).astype(np.float32)
     nw = (1 + 0.2 * rng.standard_normal(in_dim)).astype(np.float32)
     wg, wu = synth.weights(t, ffn, in_dim, seed=11), synth.weights(t, ffn, in_dim, seed=12)
+    if t in (12, 13, 14):
+        # the K-quant blocks' O(1) weights give gate values in the thousands, where
+        # silu is linear or zero and the oracle's exp overflows: a checkpoint's
+        # weight size (scales / 64) keeps |gate| below 40
+        wg, wu = realistic_scale(wg, t), realistic_scale(wu, t)
     dg, du = GpuBuf.upload(wg), GpuBuf.upload(wu)
     dx, dn, act = GpuBuf.upload_f32(x), GpuBuf.upload_f32(nw), GpuBuf.alloc_f32(ffn)
     scratch = GpuBuf.alloc_f32(in_dim + 2 * ffn)
