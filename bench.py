@@ -40,6 +40,8 @@ def parse():
                     help="only the configs[4] MoE leg (grouped, per-expert and routed), one JSON line")
     ap.add_argument("--only-forward", action="store_true",
                     help="only run the end-to-end decode-step leg (for profiling its kernels)")
+    ap.add_argument("--forward-n", type=str, default="1,4,16,32",
+                    help="token batches of the end-to-end decode-step leg (comma separated)")
     ap.add_argument("--batched-suite", action="store_true",
                     help="only time hip_gemm at the batched shapes of configs[3]/[4] (16 tokens; for profiling "
                          "the matrix-core GEMM kernels)")
@@ -77,7 +79,8 @@ def main():
     if args.only_forward:
         from saient_quartz_amd.decode import ModelConfig
         wbytes = ModelConfig().weight_bytes()
-        print(json.dumps({"forward": forward_leg(torch, args.decode_reps, wbytes)}), flush=True)
+        ns = [int(v) for v in args.forward_n.split(",")]
+        print(json.dumps({"forward": forward_leg(torch, args.decode_reps, wbytes, ns)}), flush=True)
         return
 
     from saient_quartz_amd import lib, synth_device, type_size
@@ -265,7 +268,7 @@ def decode_leg(torch, reps):
     return out
 
 
-def forward_leg(torch, reps, wbytes):
+def forward_leg(torch, reps, wbytes, ns=(1, 4, 16, 32)):
     """End-to-end Llama-3-8B-shaped decode steps generating tokens: one HIP
     graph per N, captured once with the tokens and the position read on the
     device (issue(dev=True, greedy=True): the step ends with the greedy pick,
@@ -288,7 +291,7 @@ def forward_leg(torch, reps, wbytes):
     cfg = ModelConfig(max_seq=1024)
     weights = ForwardStep.random_weights(cfg)
     out = {}
-    for n in (1, 4, 16, 32):
+    for n in ns:
         step = ForwardStep(cfg, weights) if n == 1 else BatchStep(cfg, weights, n)
         tokens = [(7 * i + 3) % 1000 for i in range(n)]
         set_state = (lambda pos: step.set_state(tokens[0], pos)) if n == 1 else (lambda pos: step.set_state(tokens, pos))

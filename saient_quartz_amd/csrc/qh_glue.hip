@@ -12,6 +12,7 @@
 // hip_attention_decode fuses the three attention kernels into one launch per
 // step (scores and probabilities stay in LDS).
 #include <climits>
+#include <mutex>
 #include "qh_internal.h"
 
 // Sum / max over the 64 lanes of a wavefront (every lane gets the result).
@@ -334,42 +335,17 @@ __host__ __device__ inline int qa_nch(int pos, int n_seq, int n_kv, int n_heads,
 
 // HD: head_dim capacity, 128 or QA_MAXHD (LDS, so occupancy, scales with it);
 // GW: q heads per wavefront (1, 2 or 4: groups of up to 4, 8 or QA_MAXG heads).
-template <int HD, int GW>
-__global__ __launch_bounds__(256) void qg_attention_step(float* out, const float* q, const float* k, const float* v,
-                                                         float* kc, float* vc, const float* sinks, int n_heads,
-                                                         int n_kv, int hd, int kv_dim, int pos, float theta,
-                                                         float yarn_scale, int orig_ctx, int neox, float scale,
-                                                         float* part, unsigned int* cnt, size_t cache_stride,
-                                                         const int* pos_dev, int per_force) {
-    __shared__ __align__(16) float kl[QA_ROWS * (HD + 4)];
-    __shared__ __align__(16) float vl[QA_ROWS * HD];
-    __shared__ __align__(16) float qr[QA_MAXG * HD];
-    __shared__ __align__(16) float kr[HD];
-    __shared__ __align__(16) float vr[HD];
-    __shared__ int last_flag;
-    const int g = blockIdx.x, c = blockIdx.y;
-    int nch = gridDim.y;
-    if (pos_dev) {
-        // the position comes from device memory (a step replayed from one graph
-        // at consecutive positions): `pos` is the launch's bound, and the
-        // reference clamps to the cache (src/cuda.rs:517-520); workgroups past
-        // this position's split exit at once
-        pos = min(max(*pos_dev, 0), pos);
-        nch = qa_nch(pos, gridDim.z, n_kv, n_heads, hd, per_force);
-        if (c >= nch) return;
-    }
-    // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
-    {
-        const size_t z = blockIdx.z;
-        q += z * (size_t)n_heads * hd;
-        out += z * (size_t)n_heads * hd;
-        k += z * (size_t)kv_dim;
-        v += z * (size_t)kv_dim;
-        kc += z * cache_stride;
-        vc += z * cache_stride;
-        part += z * (size_t)n_heads * nch * (hd + 2);
-        cnt += z * (size_t)n_kv;
-    }
+// The attention of kv head g for one workgroup, slices c, c + nch, ... (the
+// body of qg_attention_step).  Returns true in the workgroup that wrote the
+// group's output rows (the only one when nch == 1, else the last to arrive,
+// which merges the partials).  PUB: those rows are stored for other workgroups
+// of the same launch to read (agent-scope stores).
+template <int HD, int GW, bool PUB>
+QH_DEV bool qg_attn_group(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
+                          const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
+                          float yarn_scale, int orig_ctx, int neox, float scale, float* part, unsigned int* cnt,
+                          const int g, const int c, const int nch, float* kl, float* vl, float* qr, float* kr,
+                          float* vr, int& last_flag) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int h0 = (g * n_heads + n_kv - 1) / n_kv, h1 = ((g + 1) * n_heads + n_kv - 1) / n_kv, ng = h1 - h0;
     const int seq = pos + 1, half = hd >> 1;
@@ -512,7 +488,13 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
 #pragma unroll
         for (int d = 0; d < HD / 64; d++) {
             const int dd = lane + 64 * d;
-            if (dd < hd) out[(size_t)h * hd + dd] = oo[d] * f;
+            if (dd < hd) {
+                if constexpr (PUB)  // read by other workgroups of this launch
+                    __hip_atomic_store(out + (size_t)h * hd + dd, oo[d] * f, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    out[(size_t)h * hd + dd] = oo[d] * f;
+            }
         }
     };
     if (nch == 1) {
@@ -522,7 +504,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
             if (j >= ng) break;
             finish(j, m[a], l[a], o[a], false);
         }
-        return;
+        return true;
     }
     // partial record of (head h, slice c): [m, l, o[0 .. hd)]
     const int rec = hd + 2;
@@ -548,7 +530,7 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         last_flag = __hip_atomic_fetch_add(&cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     (unsigned)(nch - 1);
     __syncthreads();
-    if (!last_flag) return;
+    if (!last_flag) return false;
     // Merge.  The partials are read with SC1 buffer loads (the coherence bit of
     // an agent-scope load, so no stale L2 line of another launch is seen), which
     // unlike atomic loads issue back to back: lane cc holds slice cc's (m, l).
@@ -589,6 +571,48 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
         finish(j, M, L, oo, true);
     }
     if (threadIdx.x == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    return true;
+}
+
+template <int HD, int GW>
+__global__ __launch_bounds__(256) void qg_attention_step(float* out, const float* q, const float* k, const float* v,
+                                                         float* kc, float* vc, const float* sinks, int n_heads,
+                                                         int n_kv, int hd, int kv_dim, int pos, float theta,
+                                                         float yarn_scale, int orig_ctx, int neox, float scale,
+                                                         float* part, unsigned int* cnt, size_t cache_stride,
+                                                         const int* pos_dev, int per_force) {
+    __shared__ __align__(16) float kl[QA_ROWS * (HD + 4)];
+    __shared__ __align__(16) float vl[QA_ROWS * HD];
+    __shared__ __align__(16) float qr[QA_MAXG * HD];
+    __shared__ __align__(16) float kr[HD];
+    __shared__ __align__(16) float vr[HD];
+    __shared__ int last_flag;
+    const int g = blockIdx.x, c = blockIdx.y;
+    int nch = gridDim.y;
+    if (pos_dev) {
+        // the position comes from device memory (a step replayed from one graph
+        // at consecutive positions): `pos` is the launch's bound, and the
+        // reference clamps to the cache (src/cuda.rs:517-520); workgroups past
+        // this position's split exit at once
+        pos = min(max(*pos_dev, 0), pos);
+        nch = qa_nch(pos, gridDim.z, n_kv, n_heads, hd, per_force);
+        if (c >= nch) return;
+    }
+    // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
+    {
+        const size_t z = blockIdx.z;
+        q += z * (size_t)n_heads * hd;
+        out += z * (size_t)n_heads * hd;
+        k += z * (size_t)kv_dim;
+        v += z * (size_t)kv_dim;
+        kc += z * cache_stride;
+        vc += z * cache_stride;
+        part += z * (size_t)n_heads * nch * (hd + 2);
+        cnt += z * (size_t)n_kv;
+    }
+    return (void)qg_attn_group<HD, GW, false>(out, q, k, v, kc, vc, sinks, n_heads, n_kv, hd, kv_dim, pos, theta,
+                                              yarn_scale, orig_ctx, neox, scale, part, cnt, g, c, nch, kl, vl, qr,
+                                              kr, vr, last_flag);
 }
 
 // silu(gate) * up (swiglu_f32, :670-676) and the clamped gpt-oss form
@@ -656,20 +680,44 @@ __device__ __forceinline__ long long qg_greedy_key(float v, int i) {
     const int key = b ^ ((b >> 31) & 0x7FFFFFFF);
     return ((long long)key << 32) | (unsigned)i;
 }
-__global__ __launch_bounds__(1024) void qg_greedy(const float* logits, size_t stride, int n, int* tokens, int* pos) {
-    __shared__ long long best_w[16];
-    const float* x = logits + (size_t)blockIdx.x * stride;
+// A row is split over QG_GP workgroups (a single workgroup reading a 128256-
+// entry row is bound by one CU's bandwidth: 12 us); each writes its best key,
+// and the last of a row's workgroups to arrive reduces them in order and
+// writes the token (row 0's also advances pos).
+#define QG_GP 32
+#define QG_GROWS 256
+static __device__ __align__(256) unsigned long long qg_gpart[QG_GROWS * QG_GP];
+static __device__ __align__(256) unsigned int qg_gcnt[QG_GROWS];
+__global__ __launch_bounds__(256) void qg_greedy(const float* logits, size_t stride, int n, int* tokens, int* pos,
+                                                 unsigned long long* gpart, unsigned int* gcnt) {
+    __shared__ long long best_w[4];
+    __shared__ int last;
+    const int p = blockIdx.x, r = blockIdx.y;
+    const float* x = logits + (size_t)r * stride;
+    // chunk [i0, i1) of the row, 4-element aligned in index
+    const int per = ((n + QG_GP - 1) / QG_GP + 3) & ~3;
+    const int i0 = min(p * per, n), i1 = min(i0 + per, n);
     long long best = LLONG_MIN;
-    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
-        float v[8];
+    if ((((uintptr_t)(x + i0)) & 15u) == 0) {
+        const int n4 = (i1 - i0) >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(x + i0);
+        for (int j0 = threadIdx.x; j0 < n4; j0 += 4 * 256) {
+            float4 v[4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = x[min(i0 + u * 1024, n - 1)];  // all eight loads in flight
+            for (int u = 0; u < 4; u++) v[u] = x4[min(j0 + u * 256, n4 - 1)];  // a repeat changes nothing
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = min(i0 + u * 1024, n - 1);  // a clamped repeat of the last value changes nothing
-            const long long kk = qg_greedy_key(v[u], i);
-            best = kk > best ? kk : best;
+            for (int u = 0; u < 4; u++) {
+                const int i = i0 + 4 * min(j0 + u * 256, n4 - 1);
+                long long kk = qg_greedy_key(v[u].x, i);
+                kk = max(kk, qg_greedy_key(v[u].y, i + 1));
+                kk = max(kk, qg_greedy_key(v[u].z, i + 2));
+                kk = max(kk, qg_greedy_key(v[u].w, i + 3));
+                best = kk > best ? kk : best;
+            }
         }
+        for (int i = i0 + 4 * n4 + (int)threadIdx.x; i < i1; i += 256) best = max(best, qg_greedy_key(x[i], i));
+    } else {
+        for (int i = i0 + (int)threadIdx.x; i < i1; i += 256) best = max(best, qg_greedy_key(x[i], i));
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -679,16 +727,60 @@ __global__ __launch_bounds__(1024) void qg_greedy(const float* logits, size_t st
     if ((threadIdx.x & 63) == 0) best_w[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = best_w[w] > best ? best_w[w] : best;
-        tokens[blockIdx.x] = (int)(unsigned)(best & 0xFFFFFFFFll);
-        if (pos && blockIdx.x == 0) pos[0] += 1;
+        for (int w = 1; w < 4; w++) best = best_w[w] > best ? best_w[w] : best;
+        // stored with the sign flipped: unsigned order = signed order
+        __hip_atomic_store(gpart + (size_t)r * QG_GP + p, (unsigned long long)best ^ 0x8000000000000000ull,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        last = __hip_atomic_fetch_add(gcnt + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == QG_GP - 1;
     }
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x < 64) {
+        unsigned long long v = threadIdx.x < QG_GP
+                                   ? __hip_atomic_load(gpart + (size_t)r * QG_GP + threadIdx.x, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0ull;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const unsigned long long o = __shfl_xor(v, off);
+            v = o > v ? o : v;
+        }
+        if (threadIdx.x == 0) {
+            tokens[r] = (int)(unsigned)(v & 0xFFFFFFFFull);
+            if (pos && r == 0) pos[0] += 1;
+            __hip_atomic_store(gcnt + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+        }
+    }
+}
+
+struct QgGreedyScratch { unsigned long long* part; unsigned int* cnt; };
+static const QgGreedyScratch* qg_greedy_scratch() {
+    static QgGreedyScratch ptrs[64] = {};
+    static std::once_flag once[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::call_once(once[dev], [&] {
+        void *a = nullptr, *b = nullptr;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qg_gpart)) == hipSuccess &&
+            hipGetSymbolAddress(&b, HIP_SYMBOL(qg_gcnt)) == hipSuccess)
+            ptrs[dev] = QgGreedyScratch{static_cast<unsigned long long*>(a), static_cast<unsigned int*>(b)};
+    });
+    return ptrs[dev].part ? &ptrs[dev] : nullptr;
 }
 
 hipError_t qh_glue_greedy(const float* logits, size_t stride, int rows, int n, int* tokens, int* pos, hipStream_t st) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(qg_greedy, dim3((unsigned)rows), dim3(1024), 0, st, logits, stride, n, tokens, pos);
-    return hipGetLastError();
+    const QgGreedyScratch* sc = qg_greedy_scratch();
+    if (!sc) return hipErrorInvalidDevice;
+    for (int r0 = 0; r0 < rows; r0 += QG_GROWS) {
+        const int c = rows - r0 < QG_GROWS ? rows - r0 : QG_GROWS;
+        hipLaunchKernelGGL(qg_greedy, dim3(QG_GP, (unsigned)c), dim3(256), 0, st, logits + (size_t)r0 * stride,
+                           stride, n, tokens + r0, r0 == 0 ? pos : nullptr, sc->part, sc->cnt);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 static unsigned qg_blocks(int n) { return (unsigned)((n + 255) / 256); }

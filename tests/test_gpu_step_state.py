@@ -50,6 +50,14 @@ def test_greedy_next_vs_oracle(qh):
         torch.cuda.synchronize()
         assert int(out[0]) == g.greedy_next(r), r[:8]
         assert int(out[1]) == -7
+    # a row starting off a 16-byte boundary (scalar head, vector body, scalar tail)
+    r = rng.integers(-20, 20, 1003).astype(np.float32)
+    buf = _f32(np.concatenate([[0.0], r]))
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    check("hip_greedy_next_async", L.hip_greedy_next_async(buf.data_ptr() + 4, r.size, 1, r.size, out.data_ptr(),
+                                                           None, None))
+    torch.cuda.synchronize()
+    assert int(out[0]) == g.greedy_next(r)
     # several rows at a stride, and the position advance (once per launch)
     n, stride, rows_n = 1000, 1024, 5
     x = rng.integers(-50, 50, (rows_n, stride)).astype(np.float32)
