@@ -199,8 +199,12 @@ int hip_gemm_moe_async(uint32_t ggml_type, const uint8_t* d_experts, int n_sel, 
  * in_dim*out_dim)) into the same rows of d_y[s] (y += with accumulate).  With
  * d_x_up, x is silu(d_x) * d_x_up (a down projection after SwiGLU).  max_tokens
  * bounds any expert's token count (the launch holds ceil(max_tokens/16) token
- * chunks per expert; the empty ones exit at once), so nothing is read back to
- * the host and the call can be captured in a HIP graph.  Replaces the host
+ * chunks per expert, of 32 tokens when max_tokens > 16; the empty ones exit at
+ * once), so nothing is read back to the host and the call can be captured in a
+ * HIP graph.  An expert with more rows than the chunks cover (a max_tokens
+ * below its count) gets only its first chunks' rows computed; its later rows
+ * of d_y are left as they were (the bound is the caller's: n_tok * k, or the
+ * batch size, always holds).  Replaces the host
  * round trip of the per-expert loop of src/cuda.rs:667-798 (the reference
  * copies the router logits back to build it).  Matrix-core types only (Q4_K,
  * Q5_K, Q6_K, IQ3_S, IQ2_XXS; QH_ERR_TYPE otherwise), in_dim % 256 == 0,

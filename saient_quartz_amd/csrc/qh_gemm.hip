@@ -33,6 +33,7 @@
 // q4k_row_batched / q6k_row_batched (:38-122); the reference has no GPU
 // batched path.
 #include <climits>
+#include <mutex>
 
 #include "qh_formats.h"
 #include "qh_internal.h"
@@ -288,7 +289,7 @@ struct QgXs {        // the distinct token blocks of one grouped launch
     const float* x[QG_MAXG];
     const float* x2[QG_MAXG];  // SwiGLU: x is silu(x) * x2 (gate, up) when non-null
     int n[QG_MAXG];  // tokens (<= 16 halves)
-    const unsigned char* img;  // their x images: slot s, group g at (s ngroups + g) XImg::BYTES
+    const unsigned char* img;  // their x images: slot s, group g, half h at ((s ngroups + g) halves + h) XImg::BYTES
     uint32_t img_bytes;
     // Token ranges on the device (expert layers): when tok_off is set, slot s is
     // chunk c = s % moe_c of expert e = s / moe_c, tokens tok_off[e] + 16 c ..
@@ -350,8 +351,8 @@ QH_DEV QgTok qg_tokens(const QgGroups& gs, int gi, const QgXs& xs, int slot, int
     if (!xs.tok_off) return QgTok{qg_uni(gs.x[gi]), qg_uni(gs.x2[gi]), qg_uni(gs.n[gi]), 0};
     return qg_tokens(xs, slot, in_dim);
 }
-// Split-K partials (per (row block, split): W wavefronts x TPW tiles x 16 tokens
-// x 32 rows)
+// Split-K partials (per (row block, split): W wavefronts x TPW tiles x NT
+// tokens (16 or 32) x 32 rows)
 // and per-(block, wavefront) arrival counters; every counter is back at zero
 // when a launch ends.
 #define QG_PART_FLOATS (16 * 1024 * 1024)
@@ -897,21 +898,20 @@ __global__ __launch_bounds__(64 * W) void qh_mmq_mix(const QgGroups gs1, const Q
 // Device addresses of the library's static scratch, per device (hipGetSymbolAddress once).
 struct QgScratch { float* part; unsigned int* cnt; unsigned char* img; };
 static const QgScratch* qh_mmq_scratch_ptrs() {
+    // filled once per device (std::call_once: host threads may race here)
     static QgScratch ptrs[64] = {};
+    static std::once_flag once[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    QgScratch& p = ptrs[dev];
-    if (!p.part) {
+    std::call_once(once[dev], [&] {
         void *b = nullptr, *c = nullptr, *im = nullptr;
-        if (hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) != hipSuccess ||
-            hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) != hipSuccess ||
-            hipGetSymbolAddress(&im, HIP_SYMBOL(qh_mmq_img)) != hipSuccess)
-            return nullptr;
-        p.cnt = static_cast<unsigned int*>(c);
-        p.img = static_cast<unsigned char*>(im);
-        p.part = static_cast<float*>(b);
-    }
-    return &p;
+        if (hipGetSymbolAddress(&b, HIP_SYMBOL(qh_mmq_part)) == hipSuccess &&
+            hipGetSymbolAddress(&c, HIP_SYMBOL(qh_mmq_cnt)) == hipSuccess &&
+            hipGetSymbolAddress(&im, HIP_SYMBOL(qh_mmq_img)) == hipSuccess)
+            ptrs[dev] = QgScratch{static_cast<float*>(b), static_cast<unsigned int*>(c),
+                                  static_cast<unsigned char*>(im)};
+    });
+    return ptrs[dev].part ? &ptrs[dev] : nullptr;
 }
 
 // QUARTZ_HIP_MMQ_MODE=m forces the image mode (0 streamed, 1 resident, 2

@@ -854,18 +854,16 @@ hipError_t qh_glue_attention_decode(float* out, const float* q, const float* kc,
 struct QaScratch { float* part; unsigned int* cnt; };
 static const QaScratch* qa_scratch_ptrs() {
     static QaScratch ptrs[64] = {};
+    static std::once_flag once[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    QaScratch& p = ptrs[dev];
-    if (!p.part) {
+    std::call_once(once[dev], [&] {
         void *a = nullptr, *b = nullptr;
-        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qa_part)) != hipSuccess ||
-            hipGetSymbolAddress(&b, HIP_SYMBOL(qa_cnt)) != hipSuccess)
-            return nullptr;
-        p.cnt = static_cast<unsigned int*>(b);
-        p.part = static_cast<float*>(a);
-    }
-    return &p;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(qa_part)) == hipSuccess &&
+            hipGetSymbolAddress(&b, HIP_SYMBOL(qa_cnt)) == hipSuccess)
+            ptrs[dev] = QaScratch{static_cast<float*>(a), static_cast<unsigned int*>(b)};
+    });
+    return ptrs[dev].part ? &ptrs[dev] : nullptr;
 }
 
 hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,

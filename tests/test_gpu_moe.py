@@ -258,7 +258,8 @@ def test_gemm_moe_dev_vs_oracle(qh, oracle, t, sets, swiglu, acc, counts):
     X, XU = dev(xg), (dev(xu) if swiglu else None)
     sl = type_size(t, in_dim * out_dim)
     assert sl == len(blobs[0][0])
-    gemm_moe_dev_async(qh, t, [w.data_ptr() for w in W], [y.data_ptr() for y in Y], E, dev(off).data_ptr(),
+    doff = dev(off)  # held until the launch has run
+    gemm_moe_dev_async(qh, t, [w.data_ptr() for w in W], [y.data_ptr() for y in Y], E, doff.data_ptr(),
                        max(counts), X.data_ptr(), in_dim, out_dim, torch.cuda.current_stream().cuda_stream,
                        x_up_ptr=XU.data_ptr() if swiglu else None, accumulate=acc)
     torch.cuda.synchronize()
@@ -278,6 +279,30 @@ def test_gemm_moe_dev_vs_oracle(qh, oracle, t, sets, swiglu, acc, counts):
             for r in range(b - a):
                 err = np.linalg.norm(got[a + r] - ref[r]) / np.linalg.norm(ref[r])
                 assert err < 1e-3, (s, e, r, err)
+
+
+def test_gemm_moe_dev_max_tokens_bound(qh, oracle):
+    """An expert holding more rows than max_tokens covers: its first
+    ceil(max_tokens / 16) x 16 rows are computed, the rest of its rows of y are
+    left untouched (the documented contract), and other experts are complete."""
+    from saient_quartz_amd.host import gemm_moe_dev_async
+    t, in_dim, out_dim, counts, max_tokens = 12, 512, 64, [5, 40], 16
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    blobs = [synth.weights(t, out_dim, in_dim, seed=90 + e) for e in range(2)]
+    W = dev(np.concatenate(blobs))
+    xg = synth.activations(45, in_dim, seed=91)
+    Y = torch.full((45, out_dim), np.nan, device="cuda")
+    doff, X = dev(off), dev(xg)  # held until the launch has run
+    gemm_moe_dev_async(qh, t, [W.data_ptr()], [Y.data_ptr()], 2, doff.data_ptr(), max_tokens, X.data_ptr(), in_dim,
+                       out_dim, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = Y.cpu().numpy()
+    for e, rows in ((0, 5), (1, 16)):
+        a = int(off[e])
+        ref = oracle.gemm(t, xg[a:a + rows], blobs[e], in_dim, out_dim, rows)
+        for r in range(rows):
+            assert np.linalg.norm(got[a + r] - ref[r]) / np.linalg.norm(ref[r]) < 1e-3, (e, r)
+    assert np.all(np.isnan(got[5 + 16:]))
 
 
 def test_gemm_moe_dev_rejects_other_types(qh):
