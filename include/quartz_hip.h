@@ -22,7 +22,8 @@
  * threads on distinct streams, with one exception: hip_gemm / hip_gemm_grouped /
  * hip_gemm_moe (and their _async forms) with n >= 2 on Q4_K, Q5_K, Q6_K, IQ3_S
  * or IQ2_XXS stage the digitised activations and split-K partials in static
- * device arrays (about 50 MB, one set per device), so such calls that overlap on
+ * device arrays (104.25 MiB: 64 MiB of split-K partials, 40 MiB of x images and
+ * 256 KiB of counters, one set per device), so such calls that overlap on
  * one device must be serialised by the caller (e.g. one stream per device).
  */
 #ifndef QUARTZ_HIP_H

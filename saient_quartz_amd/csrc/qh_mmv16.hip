@@ -957,7 +957,7 @@ static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int 
 // Measured on MI355X: 16 x 1 is fastest when K fits one chunk (in_dim <= 4096);
 // above that 8 x 1, except Q4_K, which stays at 16 x 1 (4096 x 11008 / 14336,
 // 8192 x 28672: 2-15% faster, while Q6_K and the IQ formats lose at 16 x 1).
-// QUARTZ_HIP_MMV16=4|10|2 forces 16x1 | 8x1 | 8x2 (tuning).
+// QUARTZ_HIP_MMV16=4|10|2|14 forces 16x1 | 8x1 | 8x2 | 14x1 (tuning).
 static int qh_mmv16_variant_env() {
     static const int v = [] {
         const char* e = getenv("QUARTZ_HIP_MMV16");
@@ -970,9 +970,17 @@ constexpr bool qh_mmv16_wide() {  // 16 x 1 also when K spans several chunks
     return std::is_same<F, M16Q4K>::value || std::is_same<F, M16Q4K16>::value;
 }
 template <class F>
+constexpr bool qh_mmv16_k5() {  // Q4_K / Q5_K: 14 x 1 when K is a multiple of 14 groups
+    return qh_mmv16_wide<F>() || std::is_same<F, M16Q5K>::value || std::is_same<F, M16Q5K16>::value;
+}
+template <class F>
 static int qh_mmv16_variant(int in_dim) {
     const int v = qh_mmv16_variant_env();
     if (v >= 0) return v;
+    // 14 waves when K splits into whole chunks of 14 groups (in_dim 14336: 4
+    // chunks, none idle): Q4_K 4096x14336 9.95 -> 9.41 us, Q5_K 11.63 -> 10.84;
+    // Q6_K loses (12.21 -> 14.47) and keeps 8 x 1
+    if (in_dim > 4096 && qh_mmv16_k5<F>() && (in_dim / 256) % 14 == 0) return 14;
     return in_dim <= 4096 || qh_mmv16_wide<F>() ? 4 : 10;
 }
 
@@ -984,6 +992,7 @@ static hipError_t dispatch_mmv16(const uint8_t* W, const float* x, float* y, int
         case 2: return launch_mmv16<F, 8, 2>(W, x, y, in_dim, out_dim, row_bytes, st);
         case 4: return launch_mmv16<F, 16, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
         case 10: return launch_mmv16<F, 8, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case 14: return launch_mmv16<F, 14, 1>(W, x, y, in_dim, out_dim, row_bytes, st);
         default: return hipErrorInvalidValue;
     }
 }
