@@ -6,8 +6,8 @@ Workload: Q4_K GEMV, W 14336 x 4096 in GGUF Q4_K
 superblocks, f32 x ~ N(0,1), batch 1.  A step is one hip_gemv_async call over
 one of ROT weight copies (>= 768 MB in total, so the 256 MB MALL cannot serve
 repeats); weights and x are resident in HBM before the timed region.  The W
-warm-up steps and the K timed steps are captured into one HIP graph with a
-device timestamp on each side of the K; one replay is timed.
+warm-up steps and the K timed steps go out back to back on one stream, with a
+device timestamp on each side of the K.
 Prints ONE JSON line.  `value` = algorithmic bytes (weights + x + y) per step x K
 / GPU time of the K steps (device wall-clock stamps around them).
 """
@@ -101,57 +101,48 @@ def main():
         check("hip_gemv_async", L.hip_gemv_async(Q4K, Ws[i % rot].data_ptr(), x.data_ptr(), y.data_ptr(),
                                                  in_dim, out_dim, sp))
 
-    def step_on(sp_, i):
-        check("hip_gemv_async", L.hip_gemv_async(Q4K, Ws[i % rot].data_ptr(), x.data_ptr(), y.data_ptr(),
-                                                 in_dim, out_dim, sp_))
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # The K steps are captured into one HIP graph (the same C-ABI calls, on
-    # torch's capture stream) so the timing is the GPU's, not Python's launch
-    # rate.  Step i uses weight copy i % rot.
-    # One HIP graph holds W untimed warm-up steps, a device timestamp, the K
-    # timed steps and a second timestamp (the same C-ABI calls, captured on
-    # torch's capture stream).  The timed steps run back to back behind steps
-    # already streaming, and the stamps (written by one-thread kernels when the
-    # preceding step has completed) bracket exactly the K steps: no graph
-    # submission or first-launch ramp inside the timed region.  Step i uses
-    # weight copy i % rot.
     stamps = torch.zeros(2, dtype=torch.int64, device="cuda")
     khz = L.hip_wallclock_khz()
     if khz <= 0:
         raise SystemExit("hip_wallclock_khz failed")
-    graph = torch.cuda.CUDAGraph()
-    nw_graph = max(args.warmup, 1)
-    with torch.cuda.graph(graph):
-        cs = torch.cuda.current_stream().cuda_stream
-        for i in range(nw_graph):
-            step_on(cs, i)
-        check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr(), cs))
-        for i in range(args.steps):
-            step_on(cs, nw_graph + i)
-        check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr() + 8, cs))
-    graph.replay()  # warm replay
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
-    y_graph = y.clone()
-    step(nw_graph + args.steps - 1)  # the graph's last step, launched eagerly
+    y_ref = y.clone()
+    step(args.warmup + args.steps - 1)  # the timed region's last step, on its own
     torch.cuda.synchronize()
-    if not torch.equal(y, y_graph):
-        raise SystemExit("graph replay result differs from the eager launch")
+    y_ref.copy_(y)
 
-    # Timed region: the K steps of one replay, between the graph's stamps.
-    graph.replay()
+    # Timed region: the launches go out eagerly on one stream behind a spin
+    # kernel that keeps the GPU busy while the host enqueues them (a HIP graph
+    # replay of the same launches measured 0.27 us slower per launch on this
+    # image).  W warm-up steps, a device timestamp, the K timed steps and a
+    # second timestamp; each stamp is a one-thread kernel writing
+    # s_memrealtime once the step before it has completed, so the stamps
+    # bracket exactly the K steps.  Step i uses weight copy i % rot.
+    lead_ms = 1.0 + 0.006 * (args.warmup + args.steps)  # host enqueue time, with margin
+    torch.cuda._sleep(int(lead_ms * 2.0e6))
+    for i in range(args.warmup):
+        step(i)
+    check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr(), sp))
+    h0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    h1 = time.perf_counter()
+    check("hip_timestamp_async", L.hip_timestamp_async(stamps.data_ptr() + 8, sp))
     torch.cuda.synchronize()
+    if not torch.equal(y, y_ref):
+        raise SystemExit("the timed region's last result differs from the same step launched on its own")
     t0, t1 = (int(v) for v in stamps.tolist())
     total_ms = (t1 - t0) / khz
     ms_per_step = total_ms / args.steps
+    if (h1 - h0) * 1e3 > total_ms + lead_ms:
+        print(f"warning: host enqueue ({(h1 - h0) * 1e3:.2f} ms) may have trailed the GPU", file=sys.stderr)
 
-    # Kernel duration: the K kernels run back to back inside the graph, so the
-    # per-step average is the kernel's duration plus the dispatch gap between
-    # launches (an upper bound on the kernel alone).  The rocprofv3 kernel-trace
-    # average of the same kernel is committed beside it (rocprof_kernel_us).
+    # Kernel duration: the K kernels run back to back, so the per-step average
+    # is the interval between consecutive completions.  The rocprofv3
+    # kernel-trace average of the same command's timed launches is committed
+    # beside it (rocprof_kernel_us).
     kern_ms = ms_per_step
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
@@ -186,7 +177,7 @@ def main():
                      "kernel": "qh_mmv16<M16Q4K, 16, 1, true, false, false, 1>",
                      "kernel_us": round(kern_ms * 1e3, 3),
                      "kernel_us_source": "device wall-clock stamps around the K back-to-back launches of the timed "
-                                         "replay, per launch (dispatch gaps included: an upper bound on the kernel)",
+                                         "region, per launch (the time between consecutive completions)",
                      "rocprof_kernel_us": profiled_kernel_us(ROOT / "profiles" / "mmv16_q4k_14336x4096_kernel_stats.md")},
         "cpu_baseline": cpu,
         "decode": decode,
@@ -269,12 +260,16 @@ def decode_leg(torch, reps):
 
 
 def forward_leg(torch, reps, wbytes, ns=(1, 4, 16, 32)):
-    """End-to-end Llama-3-8B-shaped decode steps generating tokens: one HIP
-    graph per N, captured once with the tokens and the position read on the
-    device (issue(dev=True, greedy=True): the step ends with the greedy pick,
-    which writes the next tokens and advances the position), then `reps`
-    consecutive replays from KV position 0 and from 511, i.e. positions
-    p0 .. p0 + reps - 1, each step feeding the next:
+    """End-to-end Llama-3-8B-shaped decode steps generating tokens, with the
+    tokens and the position in device memory (issue(dev=True, greedy=True):
+    each step ends with the greedy pick, which writes the next tokens and
+    advances the position), `reps` consecutive steps from KV position 0 and
+    from 511, i.e. positions p0 .. p0 + reps - 1, each step feeding the next:
+      n*_full_pos*: the steps issued eagerly on one stream (no host sync, no
+             host read between steps; events around them, a spin kernel ahead
+             so the host's enqueue is not timed; issue_ms_per_step is the
+             host's own time to enqueue a step);
+      n*_graph_pos*: the same step captured once in a HIP graph and replayed.
       N = 1: ForwardStep (embedding lookup, 32 x [fused norm + q/k/v, RoPE + KV
              append + attention, o + residual, fused norm + gate/up + SwiGLU,
              down + residual], fused final norm + head, greedy pick; 5
@@ -282,46 +277,67 @@ def forward_leg(torch, reps, wbytes, ns=(1, 4, 16, 32)):
       N = 4, 16, 32: BatchStep, N sequences in lockstep with their own K/V
              caches (batched matrix-core GEMMs, one weight pass per 16 tokens,
              or per 32 on two image halves, and batched glue).
-    n1_eager_pos0: the same N = 1 steps issued eagerly (host token and position
-    arguments, one C-ABI call per launch from Python, as a host without graphs
-    would), events around `reps` steps; issue_ms_per_step is the host's own
-    time to issue one step."""
+    n1_eager_hostargs_pos0: N = 1 with host token and position arguments (the
+    reference's calling convention), issued eagerly."""
     from saient_quartz_amd.decode import BatchStep, ForwardStep, ModelConfig
 
     cfg = ModelConfig(max_seq=1024)
     weights = ForwardStep.random_weights(cfg)
     out = {}
+
+    def rec_of(ms, n, pos):
+        return {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
+                "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+                "positions": [pos, pos + reps - 1]}
+
     for n in ns:
         step = ForwardStep(cfg, weights) if n == 1 else BatchStep(cfg, weights, n)
         tokens = [(7 * i + 3) % 1000 for i in range(n)]
         set_state = (lambda pos: step.set_state(tokens[0], pos)) if n == 1 else (lambda pos: step.set_state(tokens, pos))
         set_state(0)
-        step.issue(dev=True, greedy=True)  # eager warm-up (first-call device queries happen outside capture)
+        step.issue(dev=True, greedy=True)  # warm-up (first-call device queries happen outside capture)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             step.issue(dev=True, greedy=True)
         for pos in (0, 511):
-            set_state(pos)
-            g.replay()
+            # eager
             set_state(pos)
             torch.cuda.synchronize()
-            ms = timed_replay(torch, g, reps) / reps
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(int(2.0e6 * (1.0 + 3.0 * reps)))  # ~3 ms of lead per step
+            t0.record()
+            h0 = time.perf_counter()
+            for _ in range(reps):
+                step.issue(dev=True, greedy=True)
+            h1 = time.perf_counter()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / reps
             st = step.state.cpu().tolist()
             if st[-1] != pos + reps:
                 raise SystemExit(f"decode state did not advance: {st[-1]} != {pos + reps}")
             if not torch.isfinite(step.logits).all():
                 raise SystemExit("decode step produced non-finite logits")
-            rec = {"ms_per_step": round(ms, 4), "tok_s": round(n * 1e3 / ms, 1),
-                   "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
-                   "frac_of_weight_roofline": round(wbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-                   "positions": [pos, pos + reps - 1]}
+            r = rec_of(ms, n, pos)
+            r["issue_ms_per_step"] = round((h1 - h0) * 1e3 / reps, 4)
             if n == 1:
-                rec["launches"] = 1 + 5 * cfg.layers + 2
-            out[f"n{n}_full_pos{pos}"] = rec
+                r["launches"] = 1 + 5 * cfg.layers + 2
+            out[f"n{n}_full_pos{pos}"] = r
+            # graph
+            set_state(pos)
+            g.replay()
+            set_state(pos)
+            torch.cuda.synchronize()
+            ms = timed_replay(torch, g, reps) / reps
+            if step.state.cpu().tolist()[-1] != pos + reps:
+                raise SystemExit("decode state did not advance in the graph replays")
+            out[f"n{n}_graph_pos{pos}"] = rec_of(ms, n, pos)
         del g
         if n == 1:
-            out["n1_eager_pos0"] = eager_steps(torch, step, reps)
+            out["n1_eager_hostargs_pos0"] = eager_steps(torch, step, reps)
         del step
         torch.cuda.empty_cache()
     del weights

@@ -338,19 +338,25 @@ __host__ __device__ inline int qa_nch(int pos, int n_seq, int n_kv, int n_heads,
 // The attention of kv head g for one workgroup, slices c, c + nch, ... (the
 // body of qg_attention_step).  Returns true in the workgroup that wrote the
 // group's output rows (the only one when nch == 1, else the last to arrive,
-// which merges the partials).  PUB: those rows are stored for other workgroups
-// of the same launch to read (agent-scope stores).
-template <int HD, int GW, bool PUB>
+// which merges the partials).
+template <int HD, int GW>
 QH_DEV bool qg_attn_group(float* out, const float* q, const float* k, const float* v, float* kc, float* vc,
                           const float* sinks, int n_heads, int n_kv, int hd, int kv_dim, int pos, float theta,
                           float yarn_scale, int orig_ctx, int neox, float scale, float* part, unsigned int* cnt,
-                          const int g, const int c, const int nch, float* kl, float* vl, float* qr, float* kr,
-                          float* vr, int& last_flag) {
+                          const int g, const int c, int nch, float* kl, float* vl, float* qr, float* kr,
+                          float* vr, int& last_flag, const int* pos_dev, int per_force, int n_seq, size_t z) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int h0 = (g * n_heads + n_kv - 1) / n_kv, h1 = ((g + 1) * n_heads + n_kv - 1) / n_kv, ng = h1 - h0;
-    const int seq = pos + 1, half = hd >> 1;
+    // pos_dev: the position comes from device memory (a step replayed from one
+    // graph at consecutive positions) and `pos` is the launch's bound; the
+    // reference clamps to the cache (src/cuda.rs:517-520).  Its load is issued
+    // first and the first slice's K/V loads go out before it returns: they are
+    // clamped to the bound, and rows past the position are either replaced by
+    // row pos (the owner's slice) or never read.
+    const int bound = pos;
+    const int pos_ld = pos_dev ? *pos_dev : pos;
+    const int half = hd >> 1;
     constexpr int kp = HD + 4;  // LDS row strides of K (padded) and V: the template capacity
-    const bool owner = ((pos / QA_ROWS) % nch) == c;
     const float* kh = k + (size_t)g * hd;
     const float* vh = v + (size_t)g * hd;
     const int t_l = lane & 31, hsel = lane >> 5;
@@ -368,12 +374,21 @@ QH_DEV bool qg_attn_group(float* out, const float* q, const float* k, const floa
 #pragma unroll
         for (int u = 0; u < IT; u++) {
             const int i = threadIdx.x + 256 * u, r = i / (HD / 4), c4 = min(i % (HD / 4), q4 - 1);
-            const int t = min(sl * QA_ROWS + r, pos);
+            const int t = min(sl * QA_ROWS + r, bound);
             kk[u] = *reinterpret_cast<const f4*>(kc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
             vv[u] = *reinterpret_cast<const f4*>(vc + (size_t)t * kv_dim + (size_t)g * hd + 4 * c4);
         }
     };
     fetch(c);
+    if (pos_dev) {
+        // workgroups past this position's split exit at once
+        pos = min(max(pos_ld, 0), bound);
+        nch = qa_nch(pos, n_seq, n_kv, n_heads, hd, per_force);
+        if (c >= nch) return false;
+    }
+    part += z * (size_t)n_heads * nch * (hd + 2);
+    const int seq = pos + 1;
+    const bool owner = ((pos / QA_ROWS) % nch) == c;
     // q rows at stride HD, zero past hd: the score dot runs over HD (a constant)
     if (hd < HD)
         for (int p = threadIdx.x; p < ng * HD; p += 256)
@@ -488,13 +503,7 @@ QH_DEV bool qg_attn_group(float* out, const float* q, const float* k, const floa
 #pragma unroll
         for (int d = 0; d < HD / 64; d++) {
             const int dd = lane + 64 * d;
-            if (dd < hd) {
-                if constexpr (PUB)  // read by other workgroups of this launch
-                    __hip_atomic_store(out + (size_t)h * hd + dd, oo[d] * f, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                else
-                    out[(size_t)h * hd + dd] = oo[d] * f;
-            }
+            if (dd < hd) out[(size_t)h * hd + dd] = oo[d] * f;
         }
     };
     if (nch == 1) {
@@ -588,31 +597,19 @@ __global__ __launch_bounds__(256) void qg_attention_step(float* out, const float
     __shared__ __align__(16) float vr[HD];
     __shared__ int last_flag;
     const int g = blockIdx.x, c = blockIdx.y;
-    int nch = gridDim.y;
-    if (pos_dev) {
-        // the position comes from device memory (a step replayed from one graph
-        // at consecutive positions): `pos` is the launch's bound, and the
-        // reference clamps to the cache (src/cuda.rs:517-520); workgroups past
-        // this position's split exit at once
-        pos = min(max(*pos_dev, 0), pos);
-        nch = qa_nch(pos, gridDim.z, n_kv, n_heads, hd, per_force);
-        if (c >= nch) return;
-    }
     // sequence blockIdx.z of a batch: its q/k/v/out rows and its own K/V cache
-    {
-        const size_t z = blockIdx.z;
-        q += z * (size_t)n_heads * hd;
-        out += z * (size_t)n_heads * hd;
-        k += z * (size_t)kv_dim;
-        v += z * (size_t)kv_dim;
-        kc += z * cache_stride;
-        vc += z * cache_stride;
-        part += z * (size_t)n_heads * nch * (hd + 2);
-        cnt += z * (size_t)n_kv;
-    }
-    return (void)qg_attn_group<HD, GW, false>(out, q, k, v, kc, vc, sinks, n_heads, n_kv, hd, kv_dim, pos, theta,
-                                              yarn_scale, orig_ctx, neox, scale, part, cnt, g, c, nch, kl, vl, qr,
-                                              kr, vr, last_flag);
+    // (its partials: offset once the split is known)
+    const size_t z = blockIdx.z;
+    q += z * (size_t)n_heads * hd;
+    out += z * (size_t)n_heads * hd;
+    k += z * (size_t)kv_dim;
+    v += z * (size_t)kv_dim;
+    kc += z * cache_stride;
+    vc += z * cache_stride;
+    cnt += z * (size_t)n_kv;
+    return (void)qg_attn_group<HD, GW>(out, q, k, v, kc, vc, sinks, n_heads, n_kv, hd, kv_dim, pos, theta,
+                                              yarn_scale, orig_ctx, neox, scale, part, cnt, g, c, (int)gridDim.y, kl,
+                                              vl, qr, kr, vr, last_flag, pos_dev, per_force, (int)gridDim.z, z);
 }
 
 // silu(gate) * up (swiglu_f32, :670-676) and the clamped gpt-oss form

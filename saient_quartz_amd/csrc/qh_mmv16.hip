@@ -1068,6 +1068,8 @@ static hipError_t multi_mmv16(const uint8_t* const* Ws, float* const* ys, const 
         case 2:
             return in_dim <= 256 * 16 ? launch_mmv16_mats<F, 8, 2, true>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
                                       : launch_mmv16_mats<F, 8, 2, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case 14:  // in_dim > 4096 only (K in whole chunks of 14 groups)
+            return launch_mmv16_mats<F, 14, 1, false>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1158,6 +1160,10 @@ static hipError_t tok_mmv16(int nm, const uint8_t* const* Ws, float* const* ys, 
     if (tiles == 0) return hipSuccess;
     const bool x1 = in_dim <= 256 * 16;
     // the GEMV's launch shape, so that each token's result is bit-identical to it
+    if constexpr (qh_mmv16_k5<F>())
+        if (!x1 && (in_dim / 256) % 14 == 0 && qh_mmv16_variant_env() < 0)
+            return ntok <= 2 ? launch_mmv16_tok<F, 14, false, 2>(mm, x, in_dim, row_bytes, st)
+                             : launch_mmv16_tok<F, 14, false, 4>(mm, x, in_dim, row_bytes, st);
     if constexpr (qh_mmv16_wide<F>())
         if (!x1)
             return ntok <= 2 ? launch_mmv16_tok<F, 16, false, 2>(mm, x, in_dim, row_bytes, st)
