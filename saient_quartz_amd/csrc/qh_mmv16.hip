@@ -41,11 +41,22 @@ typedef int32_t qh_i32x4 __attribute__((ext_vector_type(4)));
 #define QH_RING 4   // finished tiles per workgroup barrier (launches with few tiles)
 
 QH_DEV uint32_t qh_lo4(uint32_t q) { return q & 0x0F0F0F0Fu; }
+// Formats whose blocks sit at 2-byte alignment set HALF: a 16-byte load at an
+// address that is not a multiple of 4 costs the address units far more than
+// one at a multiple of 4 (measured on MI355X: the Q6_K head 86 against 73 us),
+// so their slices are loaded from the dword at or below the slice and shifted
+// into place when staged, the two bytes past them taken from the next lane's
+// load (the next slice of the row).  The last slice starts at a multiple of 4
+// from the block (LAST), so its two missing bytes lie past the block.
+template <class F, class = void>
+struct QhHalf : std::false_type {};
+template <class F>
+struct QhHalf<F, std::void_t<decltype(F::HALF)>> : std::bool_constant<F::HALF> {};
 QH_DEV uint32_t qh_hi4(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
 
 // ---------------------------------------------------------------- formats
 // Each format gives: BYTES (per superblock), CH (16-byte slices loaded per row and
-// superblock; slice c starts at block byte 16c, the last at LAST <= BYTES - 16),
+// superblock; slice c starts at block byte 16c, the last at LAST <= BYTES - 14),
 // ROWS, a header decoded once per group (hdr), the four B operands of lane kg
 // (bops), and per MFMA s: the x piece of lane kg (piece), its integer scale (scl)
 // and the integer weight of the piece's f32 x-sum (mn).  Group result:
@@ -134,16 +145,17 @@ struct M16Q5K {
 // scales word s.  Weight = d*sc*(q - 32): the -32 goes through the x sums.
 struct M16Q6K {
     static constexpr int BYTES = 210, CH = 14, ROWS = 16;
-    // The 14th slice is loaded from block bytes 194-209 (not 208-223), so no load
-    // leaves the block: the LDS line then holds bytes 0-207 at 0-207 and d at 222.
-    static constexpr int LAST = 194, RS = QH_RS;
-    static constexpr bool FLOAT_D = false, MINS = true;
+    // The 14th slice is block bytes 196-211 (a multiple of 4 from the block, as
+    // HALF needs; the last two bytes are past the block and unused): the LDS
+    // line holds bytes 0-207 at 0-207 and d at 220.
+    static constexpr int LAST = 196, RS = QH_RS;
+    static constexpr bool FLOAT_D = false, MINS = true, HALF = true;
     static constexpr int GRID = 0;
     struct H { qh_u32x4 s; float d, dm; };
     static QH_DEV H hdr(const unsigned char* r, int) {
         H o;
         o.s = *reinterpret_cast<const qh_u32x4*>(r + 192);
-        o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 222));
+        o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 208 + (BYTES - 2 - LAST)));
         o.dm = 32.0f * o.d;
         return o;
     }
@@ -168,6 +180,22 @@ struct M16Q6K {
     static QH_DEV int scl(const H& h, int kg) { return ((int)(h.s[S] >> (8 * kg)) << 24) >> 24; }
     template <int S>
     static QH_DEV int mn(const H& h, int kg) { return scl<S>(h, kg); }
+};
+
+// Q6_K for K past one chunk (in_dim > 4096): plain 2-byte aligned loads, the
+// last slice from block bytes 194-209 (d at line 222).  With many chunks per
+// wavefront the shifts of HALF cost more than they save (4096x14336: 12.2 us
+// plain, 13.0 with HALF).
+struct M16Q6KW : M16Q6K {
+    static constexpr int LAST = 194;
+    static constexpr bool HALF = false;
+    static QH_DEV H hdr(const unsigned char* r, int) {
+        H o;
+        o.s = *reinterpret_cast<const qh_u32x4*>(r + 192);
+        o.d = qh_h2f(*reinterpret_cast<const uint16_t*>(r + 208 + (BYTES - 2 - LAST)));
+        o.dm = 32.0f * o.d;
+        return o;
+    }
 };
 
 // Q8_0: blocks of [d f16][32 x int8] (src/dequant.rs:1450-1463); a group is 8
@@ -471,11 +499,12 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     // Slices of this lane in a tile: row rr[h], byte offset goff[h] from the
     // tile's first row, LDS offset soff[h].
     uint32_t goff[NH], soff[NH];
-    int rr[NH];
+    int rr[NH], chs[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) {
         const int q = 64 * h + lane, r = q / CH, c = q - CH * r;
         rr[h] = q < ROWS * CH ? r : 1 << 30;
+        chs[h] = c;
         goff[h] = (uint32_t)r * row_bytes + (c == CH - 1 ? F::LAST : 16u * c);
         // Lanes past ROWS * CH store into the spare bytes after the tile's last line.
         soff[h] = q < ROWS * CH ? (uint32_t)(r * RS + 16 * c) : (uint32_t)(ROWS * RS);
@@ -499,6 +528,9 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     // Weight loads of item (tile, ch).  Rows past out_dim and groups past in_dim
     // get offsets beyond the buffer range and read as zeros, so the load stream
     // has no branches.
+    constexpr bool HALF = QhHalf<F>::value;
+    // HALF: the byte shift of each slice load
+    uint32_t wsa[HALF ? GPW * NH : 1];
     auto load_w = [&](int tile, int ch, qh_u32x4* wo) {
         const int g0 = ch * (W * GPW) + w * GPW;
         const int m = mat_of(tile);
@@ -511,7 +543,13 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
 #pragma unroll
             for (int h = 0; h < NH; h++) {
                 const bool ok = tile * ROWS + rr[h] < out_dim && g0 + t < ngroups;
-                wo[t * NH + h] = qh_ld128(wb, (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)(g0 + t));
+                const uint32_t a = (ok ? base + goff[h] : 0x80000000u) + (uint32_t)F::BYTES * (uint32_t)(g0 + t);
+                if constexpr (HALF) {
+                    wo[t * NH + h] = qh_ld128(wb, a & ~3u);
+                    wsa[t * NH + h] = a & 3u;
+                } else {
+                    wo[t * NH + h] = qh_ld128(wb, a);
+                }
             }
     };
     // x of group t, token k -> xo[t NT + k]; tokens past ntok read as zeros.
@@ -627,8 +665,30 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
 #pragma unroll
         for (int t = 0; t < GPW; t++)
 #pragma unroll
-            for (int h = 0; h < NH; h++)
-                *reinterpret_cast<qh_u32x4*>(wl + t * TILE + soff[h]) = wr[t * NH + h];
+            for (int h = 0; h < NH; h++) {
+                qh_u32x4 v = wr[t * NH + h];
+                if constexpr (HALF) {
+                    // the next slice's first dword: the next lane's, lane 63's from
+                    // lane 0 of the next load (past the last real slice: unused)
+                    // (the slice before the last: the last starts 16 (CH - 1) - LAST bytes early,
+                    // so the dword needed is its dword (16 (CH - 1) - LAST) / 4)
+                    static_assert((16 * (CH - 1) - F::LAST) % 4 == 0 && 16 * (CH - 1) - F::LAST < 16, "LAST");
+                    constexpr int LD = (16 * (CH - 1) - F::LAST) / 4;
+                    const bool pen = chs[h] == CH - 2;
+                    // DPP wave_shl:1: lane i reads lane i + 1
+                    uint32_t xa = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v.x, 0x130, 0xF, 0xF, false);
+                    uint32_t xb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[LD], 0x130, 0xF, 0xF, false);
+                    if (h + 1 < NH && lane == 63) {
+                        xa = (uint32_t)__builtin_amdgcn_readlane((int)wr[t * NH + h + 1].x, 0);
+                        xb = (uint32_t)__builtin_amdgcn_readlane((int)wr[t * NH + h + 1][LD], 0);
+                    }
+                    const uint32_t x4 = pen ? xb : xa;
+                    const uint32_t sh = wsa[t * NH + h];
+                    v = qh_u32x4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                                 __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(x4, v.w, sh)};
+                }
+                *reinterpret_cast<qh_u32x4*>(wl + t * TILE + soff[h]) = v;
+            }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1031,7 +1091,9 @@ hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, floa
             return qh_rows16_better(M16Q5K::ROWS, out_dim)
                        ? dispatch_mmv16<M16Q5K16>(W, x, y, in_dim, out_dim, row_bytes, st)
                        : dispatch_mmv16<M16Q5K>(W, x, y, in_dim, out_dim, row_bytes, st);
-        case QT_Q6_K: return dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st);
+        case QT_Q6_K:
+            return in_dim <= 4096 ? dispatch_mmv16<M16Q6K>(W, x, y, in_dim, out_dim, row_bytes, st)
+                                  : dispatch_mmv16<M16Q6KW>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_IQ3_S: return dispatch_mmv16<M16IQ3S>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q4_1: return dispatch_mmv16<M16Blk<1>>(W, x, y, in_dim, out_dim, row_bytes, st);
         case QT_Q5_1: return dispatch_mmv16<M16Blk<3>>(W, x, y, in_dim, out_dim, row_bytes, st);
@@ -1090,7 +1152,9 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
             return qh_rows16_better(M16Q5K::ROWS, total)
                        ? multi_mmv16<M16Q5K16>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
                        : multi_mmv16<M16Q5K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
-        case QT_Q6_K: return multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
+        case QT_Q6_K:
+            return in_dim <= 4096 ? multi_mmv16<M16Q6K>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair)
+                                  : multi_mmv16<M16Q6KW>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_IQ3_S: return multi_mmv16<M16IQ3S>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q4_1: return multi_mmv16<M16Blk<1>>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
         case QT_Q5_1: return multi_mmv16<M16Blk<3>>(Ws, ys, outs, nm, x, in_dim, row_bytes, st, nw, accum, pair);
@@ -1198,7 +1262,10 @@ hipError_t qh_launch_mmv16_tokens(uint32_t type, int nm, const uint8_t* const* W
                        ? tok_mmv16<M16Q4K16>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st)
                        : tok_mmv16<M16Q4K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_Q5_K: return tok_mmv16<M16Q5K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
-        case QT_Q6_K: return tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
+        case QT_Q6_K:
+            return in_dim <= 4096 ? tok_mmv16<M16Q6K>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st)
+                                  : tok_mmv16<M16Q6KW>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw,
+                                                       st);
         case QT_Q8_0: return tok_mmv16<M16Q80>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_IQ3_S: return tok_mmv16<M16IQ3S>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
         case QT_Q4_1: return tok_mmv16<M16Blk<1>>(nm, Ws, ys, outs, ldys, x, ldx, ntok, in_dim, row_bytes, accum, nw, st);
