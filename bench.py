@@ -33,6 +33,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--lead-ms", type=float, default=0.0,
+                    help="spin ahead of the headline's launches (0: sized for the launch count)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the 8B-shape decode-step leg")
     ap.add_argument("--decode-reps", type=int, default=20)
@@ -120,7 +122,8 @@ def main():
     # second timestamp; each stamp is a one-thread kernel writing
     # s_memrealtime once the step before it has completed, so the stamps
     # bracket exactly the K steps.  Step i uses weight copy i % rot.
-    lead_ms = 1.0 + 0.006 * (args.warmup + args.steps)  # host enqueue time, with margin
+    # host enqueue time (about 6 us per launch), with margin
+    lead_ms = args.lead_ms if args.lead_ms > 0 else 1.0 + 0.006 * (args.warmup + args.steps)
     torch.cuda._sleep(int(lead_ms * 2.0e6))
     for i in range(args.warmup):
         step(i)
