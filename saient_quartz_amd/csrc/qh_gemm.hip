@@ -918,8 +918,8 @@ static const QgScratch* qh_mmq_scratch_ptrs() {
 // resident and digitised in the kernel) where it applies (tuning).
 static int qh_mmq_mode_env() {
     static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMQ_MODE");
-        return e ? atoi(e) : -1;
+        const int m = qh_env_int("QUARTZ_HIP_MMQ_MODE", -1);
+        return m >= 0 && m <= 2 ? m : -1;
     }();
     return v;
 }
@@ -927,8 +927,8 @@ static int qh_mmq_mode_env() {
 // QUARTZ_HIP_MMQ_SPLITS=k forces the K splits per row block (tuning).
 static int qh_mmq_splits_env() {
     static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMQ_SPLITS");
-        return e ? atoi(e) : 0;
+        const int k = qh_env_int("QUARTZ_HIP_MMQ_SPLITS", 0);
+        return k > 0 ? k : 0;
     }();
     return v;
 }

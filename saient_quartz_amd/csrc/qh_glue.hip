@@ -877,8 +877,8 @@ hipError_t qh_glue_attention_step(float* out, const float* q, const float* k, co
     if (!sc) return hipErrorInvalidDevice;
     // QUARTZ_HIP_ATTN_SLICES=k forces k slices per workgroup
     static const int env_per = [] {
-        const char* e = getenv("QUARTZ_HIP_ATTN_SLICES");
-        return e && atoi(e) > 0 ? atoi(e) : 0;
+        const int k = qh_env_int("QUARTZ_HIP_ATTN_SLICES", 0);
+        return k > 0 ? k : 0;
     }();
     // pos_dev: the grid covers the largest split of any position up to pos
     int nch = 0;

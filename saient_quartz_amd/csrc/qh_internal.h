@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 // Block geometry, src/gguf.rs:172-191 (Q4_0/Q4_1 from the GGUF layout).
 __host__ __device__ inline int qh_block_elems(uint32_t t) {
@@ -124,3 +125,13 @@ hipError_t qh_glue_embed(float* out, size_t out_stride, const uint8_t* data, uin
                          int n_tok, int embed_dim, hipStream_t st, const int* tok_dev = nullptr,
                          int vocab = 0);
 hipError_t qh_launch_dequant(uint32_t type, const uint8_t* W, float* out, size_t n_elems, hipStream_t st);
+
+// Integer value of a tuning variable: dflt when it is unset, empty or not a
+// whole decimal number.
+static inline int qh_env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    if (!e || !*e) return dflt;
+    char* end = nullptr;
+    const long v = strtol(e, &end, 10);
+    return (*end == '\0' && v >= -(1L << 30) && v <= (1L << 30)) ? (int)v : dflt;
+}

@@ -1020,8 +1020,8 @@ static hipError_t launch_mmv16(const uint8_t* Wt, const float* x, float* y, int 
 // QUARTZ_HIP_MMV16=4|10|2|14 forces 16x1 | 8x1 | 8x2 | 14x1 (tuning).
 static int qh_mmv16_variant_env() {
     static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_MMV16");
-        return e ? atoi(e) : -1;
+        const int k = qh_env_int("QUARTZ_HIP_MMV16", -1);
+        return k == 4 || k == 10 || k == 2 || k == 14 ? k : -1;
     }();
     return v;
 }
@@ -1061,8 +1061,8 @@ static hipError_t dispatch_mmv16(const uint8_t* W, const float* x, float* y, int
 // rows-per-tile x tiles-per-CU (QUARTZ_HIP_MMV16_ROWS=16|0 forces it, tuning).
 static bool qh_rows16_better(int rows, int out_dim) {
     static const int env = [] {
-        const char* e = getenv("QUARTZ_HIP_MMV16_ROWS");
-        return e ? atoi(e) : -1;
+        const int k = qh_env_int("QUARTZ_HIP_MMV16_ROWS", -1);
+        return k == 16 || k == 0 ? k : -1;
     }();
     if (env >= 0) return env == 16;
     static int cus = 0;
@@ -1173,8 +1173,7 @@ hipError_t qh_launch_mmv16_multi(uint32_t type, const uint8_t* const* Ws, float*
 // third token runs in a 4-token launch with the fourth masked).
 static bool qh_tokens_enabled() {
     static const int v = [] {
-        const char* e = getenv("QUARTZ_HIP_TOKENS");
-        return e ? atoi(e) : 1;
+        return qh_env_int("QUARTZ_HIP_TOKENS", 1);
     }();
     return v != 0;
 }
