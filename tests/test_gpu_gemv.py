@@ -52,7 +52,11 @@ def test_dequant_f16_all_patterns(qh, oracle):
     assert np.array_equal(out.download(np.uint32), oracle.dequant(1, bits, 65536).view(np.uint32))
 
 
-SHAPES = [(64, 4096), (37, 4096), (5, 256), (130, 512), (19, 14336), (3, 8192), (2, 12288), (1, 28672)]
+# (21, 768) and (9, 3840): an odd number of 256-weight groups, so with 2-byte
+# aligned blocks (Q6_K: 210 bytes) both rows and groups alternate their 4-byte
+# alignment within one K chunk
+SHAPES = [(64, 4096), (37, 4096), (5, 256), (130, 512), (21, 768), (9, 3840), (19, 14336), (3, 8192), (2, 12288),
+          (1, 28672)]
 
 
 @pytest.mark.parametrize("t", ALL_TYPES)
