@@ -76,3 +76,34 @@ def test_set_ksigns_checks_closed_form():
     bad[5] ^= 0x80
     assert L.hip_set_ksigns(bad.ctypes.data) == -5
     assert L.hip_set_ksigns(None) == -3
+
+
+def test_device_state_and_graph_argument_errors():
+    """The device-state, graph and stream entry points reject bad arguments
+    before touching the GPU (this runs without one)."""
+    L = lib()
+    nul = None
+    # hip_greedy_next_async(logits, row_stride, rows, n, d_tokens, d_pos, stream)
+    assert L.hip_greedy_next_async(nul, 0, 1, 10, nul, nul, nul) == -3
+    assert L.hip_greedy_next_async(nul, 5, 2, 10, nul, nul, nul) == -2   # rows overlap
+    assert L.hip_greedy_next_async(nul, 0, -1, 10, nul, nul, nul) == -2
+    assert L.hip_greedy_next_async(nul, 0, 1, -1, nul, nul, nul) == -2
+    assert L.hip_greedy_next_async(nul, 0, 0, 10, nul, nul, nul) == 0   # nothing to pick
+    assert L.hip_greedy_next_async(nul, 0, 1, 0, nul, nul, nul) == 0
+    # hip_embed_lookup_dev_async(out, out_stride, data, type, d_tokens, n_tok, n_vocab, embed_dim, stream)
+    assert L.hip_embed_lookup_dev_async(nul, 0, nul, 99, nul, 1, 100, 4096, nul) == -1
+    assert L.hip_embed_lookup_dev_async(nul, 0, nul, 12, nul, 1, 100, 100, nul) == -2   # not whole blocks
+    assert L.hip_embed_lookup_dev_async(nul, 10, nul, 12, nul, 2, 100, 256, nul) == -2  # rows overlap
+    assert L.hip_embed_lookup_dev_async(nul, 0, nul, 12, nul, 0, 100, 256, nul) == 0
+    assert L.hip_embed_lookup_dev_async(nul, 0, nul, 12, nul, 1, 100, 256, nul) == -3
+    # hip_attention_step_dev_async: the position pointer is required
+    args = [nul] * 7 + [1, 0, 32, 8, 128, 1024, nul, 0, 5e5, 1.0, 0, 0, 0.088, nul]
+    assert L.hip_attention_step_dev_async(*args) == -3
+    # graphs and streams
+    assert L.hip_graph_begin(nul) == -3          # the null stream cannot be captured
+    assert L.hip_graph_end(nul, nul) == -3
+    assert L.hip_graph_launch(nul, nul) == -3
+    assert L.hip_stream_create(nul) == -3
+    assert L.hip_timestamp_async(nul, nul) == -3
+    L.hip_graph_destroy(nul)                     # no-ops
+    L.hip_stream_destroy(nul)
