@@ -751,12 +751,15 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
         for (int k = 0; k < NT; k++) out[k] = fmaf(acc[k], rs[k], -accm[k]);
     };
 
+    float ypre = 0.f;  // y of row threadIdx.x of the first tile (residual launches)
     auto put = [&](int d, int c, float r, int k) {  // y of row c of this workgroup's tile d, token k
         const int tile = wg_tile(d), m = mat_of(tile);
         const int row = local_tile(tile, m) * ROWS + c;
         if (c < ROWS && row < (MULTI ? mm.rows[m] : one.rows) && k < ntok) {
             float* yp = (MULTI ? mm.y[m] : one.y) + (NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row;
-            *yp = (MULTI ? mm.accum : one.accum) ? *yp + r : r;
+            // tile 0's rows are stored by threads 0-15, which loaded them at the start
+            const bool pre = NT == 1 && !PAIR && d == 0;
+            *yp = (MULTI ? mm.accum : one.accum) ? (pre ? ypre : *yp) + r : r;
         }
     };
     // Sum the wavefront partials of tiles d0 .. d0+cnt-1 (one set of the ring)
@@ -803,6 +806,15 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     load_x(0, xva);
     load_nw(nv);
     load_w(tile, 0, wra);
+    // Residual launches (y += W x) read the y they add to.  Threads 0-15 store
+    // the rows of this workgroup's first tile, so they load those now, behind the
+    // first weights, and the read costs no round trip at the end.
+    if constexpr (NT == 1 && !PAIR) {
+        const int m = mat_of(tile);
+        const int row = local_tile(tile, m) * ROWS + (int)threadIdx.x;
+        if ((MULTI ? mm.accum : one.accum) && threadIdx.x < (unsigned)ROWS && row < (MULTI ? mm.rows[m] : one.rows))
+            ypre = (MULTI ? mm.y[m] : one.y)[row];
+    }
     if constexpr (F::GRID == 0) {
         __builtin_amdgcn_sched_barrier(0);
         set_offsets();
