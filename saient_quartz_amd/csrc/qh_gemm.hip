@@ -843,6 +843,16 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
     float a[NS];
 #pragma unroll
     for (int i = 0; i < NS; i++) a[i] = 0.f;
+    // A residual launch's y values go out with the first round of partial loads
+    // (one round trip for both, not one more at the end).
+    float yv[NS];
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+        for (int i = 0; i < NSL; i++) {
+            const int t = stok(i), row = (tile0 + tt) * 32 + R;
+            yv[tt * NSL + i] = gs.accum && t < n && row < out_dim ? y[(size_t)t * ldy + row] : 0.f;
+        }
     for (int k0 = 0; k0 < splits; k0 += 4) {
         uint32_t v[NS][4];
 #pragma unroll
@@ -865,7 +875,10 @@ __device__ __forceinline__ void qh_mmq_body(const QgGroups& gs, const QgXs& xs, 
 #pragma unroll
     for (int tt = 0; tt < TPW; tt++)
 #pragma unroll
-        for (int i = 0; i < NSL; i++) put(stok(i), (tile0 + tt) * 32 + R, a[tt * NSL + i]);
+        for (int i = 0; i < NSL; i++) {
+            const int t = stok(i), row = (tile0 + tt) * 32 + R;
+            if (t < n && row < out_dim) y[(size_t)t * ldy + row] = gs.accum ? yv[tt * NSL + i] + a[tt * NSL + i] : a[tt * NSL + i];
+        }
     if (lane == 0) __hip_atomic_store(&cnt[wslot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
