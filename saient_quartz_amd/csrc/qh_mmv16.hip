@@ -757,8 +757,8 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
         const int row = local_tile(tile, m) * ROWS + c;
         if (c < ROWS && row < (MULTI ? mm.rows[m] : one.rows) && k < ntok) {
             float* yp = (MULTI ? mm.y[m] : one.y) + (NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row;
-            // tile 0's rows are stored by threads 0-15, which loaded them at the start
-            const bool pre = NT == 1 && !PAIR && d == 0;
+            // the thread that loaded this value at the start
+            const bool pre = !PAIR && d == 0 && c == (int)(threadIdx.x & 15) && k == (int)(threadIdx.x >> 4);
             *yp = (MULTI ? mm.accum : one.accum) ? (pre ? ypre : *yp) + r : r;
         }
     };
@@ -806,14 +806,15 @@ __device__ __forceinline__ void qh_mmv16_body(const QhMats& mm, const QhOne& one
     load_x(0, xva);
     load_nw(nv);
     load_w(tile, 0, wra);
-    // Residual launches (y += W x) read the y they add to.  Threads 0-15 store
-    // the rows of this workgroup's first tile, so they load those now, behind the
-    // first weights, and the read costs no round trip at the end.
-    if constexpr (NT == 1 && !PAIR) {
-        const int m = mat_of(tile);
-        const int row = local_tile(tile, m) * ROWS + (int)threadIdx.x;
-        if ((MULTI ? mm.accum : one.accum) && threadIdx.x < (unsigned)ROWS && row < (MULTI ? mm.rows[m] : one.rows))
-            ypre = (MULTI ? mm.y[m] : one.y)[row];
+    // Residual launches (y += W x) read the y they add to.  Thread 16k + c stores
+    // row c of token k of this workgroup's first tile when the workgroup has one
+    // tile, so it loads that value now, behind the first weights, and the read
+    // costs no round trip at the end.
+    if constexpr (!PAIR) {
+        const int m = mat_of(tile), c = threadIdx.x & 15, k = (int)threadIdx.x >> 4;
+        const int row = local_tile(tile, m) * ROWS + c;
+        if ((MULTI ? mm.accum : one.accum) && k < ntok && c < ROWS && row < (MULTI ? mm.rows[m] : one.rows))
+            ypre = (MULTI ? mm.y[m] : one.y)[(NT > 1 ? (size_t)k * (size_t)mm.ldy[m] : 0) + row];
     }
     if constexpr (F::GRID == 0) {
         __builtin_amdgcn_sched_barrier(0);
