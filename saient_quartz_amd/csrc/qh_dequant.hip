@@ -256,6 +256,35 @@ __device__ void qh_decode_block(uint32_t t, const uint8_t* b, float* o) {
     }
 }
 
+// Elements 16u .. 16u + 15 of a Q4_K or Q6_K block (u < 16), with the same f32
+// operations as qh_decode_block, so 16 threads decode a block bit-identically
+// to one thread decoding all of it.  False for other types.
+__device__ bool qh_decode_part16(uint32_t t, const uint8_t* b, int u, float* o) {
+    if (t == QT_Q4_K) {  // sub-block j = u / 2, positions 16 (u % 2) ..
+        const int j = u >> 1, l0 = 16 * (u & 1);
+        const float d = qh_f16(qh_rd16(b)), dmin = qh_f16(qh_rd16(b + 2));
+        uint32_t s, mb;
+        qh_gsm_k4(j, b + 4, s, mb);
+        const float d1 = d * (float)s, m1 = dmin * (float)mb;
+        const uint8_t* qs = b + 16 + 32 * (j >> 1) + l0;
+        for (int l = 0; l < 16; l++) o[l] = d1 * (float)((j & 1) ? (qs[l] >> 4) : (qs[l] & 0x0F)) - m1;
+        return true;
+    }
+    if (t == QT_Q6_K) {  // half h = u / 8, quarter r = (u / 2) % 4, positions 16 (u % 2) ..
+        const int h = u >> 3, r = (u >> 1) & 3, l0 = 16 * (u & 1), is = l0 / 16;
+        const float d = qh_f16(qh_rd16(b + 208));
+        const uint8_t* ql = b + 64 * h + (r & 1) * 32;
+        const uint8_t* qh = b + 128 + 32 * h;
+        const int8_t* sc = (const int8_t*)(b + 192 + 8 * h);
+        for (int l = l0; l < l0 + 16; l++) {
+            const int q = (int)(((r < 2) ? (ql[l] & 0x0F) : (ql[l] >> 4)) | (((qh[l] >> (2 * r)) & 3) << 4)) - 32;
+            o[l - l0] = d * (float)sc[is + 2 * r] * (float)q;
+        }
+        return true;
+    }
+    return false;
+}
+
 #pragma clang fp contract(on)
 
 // One thread per block.

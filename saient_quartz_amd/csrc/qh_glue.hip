@@ -657,6 +657,25 @@ __global__ __launch_bounds__(256) void qg_embed_lookup(float* out, const uint8_t
         }
     }
     const uint8_t* src = data + ((size_t)token * nb + b0) * bb;
+    if ((type == QT_Q4_K || type == QT_Q6_K) && nbw <= 16) {
+        // 16 threads per block, each decoding 16 values straight from memory:
+        // one round trip and no serial decode of whole blocks
+        const int blk = threadIdx.x >> 4, u = threadIdx.x & 15;
+        if (blk < nbw) {
+            float v[16];
+            (void)qh_decode_part16(type, src + (size_t)blk * bb, u, v);
+            float* o = out + (size_t)(b0 + blk) * qk + 16 * u;
+            if ((reinterpret_cast<uintptr_t>(o) & 15u) == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; i += 4)
+                    *reinterpret_cast<float4*>(o + i) = float4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[i] = v[i];
+            }
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < nbw * (int)bb; i += 256) raw[i] = src[i];
     __syncthreads();
     if ((int)threadIdx.x < nbw) qh_decode_block(type, raw + threadIdx.x * bb, dec + threadIdx.x * qk);

@@ -42,6 +42,7 @@ __host__ __device__ inline size_t qh_type_size(uint32_t t, size_t n) {
 
 // Bit-exact decode of one block (qk elements) -- qh_dequant.hip.
 __device__ void qh_decode_block(uint32_t type, const uint8_t* blk, float* out);
+__device__ bool qh_decode_part16(uint32_t type, const uint8_t* blk, int part, float* out);
 
 hipError_t qh_launch_mmv16(uint32_t type, const uint8_t* W, const float* x, float* y, int in_dim, int out_dim,
                            hipStream_t st);
