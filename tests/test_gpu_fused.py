@@ -128,3 +128,25 @@ def test_gemv_group(qh, oracle, types, dims, in_dim, norm, acc):
         ref = w @ xin + (y0[k] if acc else 0.0)
         got = ys[k].download(np.float32)[:o]
         assert cf.rel_l2(got, ref) < 1e-3, (k, t, cf.rel_l2(got, ref))
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("out_dim, in_dim", [(14336, 4096), (40000, 1024), (4097, 14336)], ids=str)
+def test_residual_gemv_many_tiles(qh, oracle, t, out_dim, in_dim):
+    """y += W x with several row tiles per workgroup: a workgroup's first tile
+    takes the y values its threads loaded at the start, the later tiles read y
+    at the end; every row against the oracle."""
+    rng = np.random.default_rng(out_dim + t)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    data = synth.weights(t, out_dim, in_dim, seed=44 + t)
+    y0 = (10 * rng.standard_normal(out_dim)).astype(np.float32)
+    w, y, dx = GpuBuf.upload(data), GpuBuf.upload_f32(y0), GpuBuf.upload_f32(x)
+    scratch = GpuBuf.alloc_f32(in_dim + out_dim)
+    gemv_fused_async(qh, t, [w.ptr], [y.ptr], [out_dim], dx.ptr, in_dim, None, norm_ptr=None, accumulate=True,
+                     scratch_ptr=scratch.ptr)
+    check("hip_sync", qh.hip_sync())
+    ref = oracle.gemv(t, x, data, in_dim, out_dim).astype(np.float64) + y0
+    got = y.download(np.float32)[:out_dim]
+    assert cf.rel_l2(got, ref) < 1e-3, cf.rel_l2(got, ref)
+    # row by row: a lost or doubled residual shows as an error of |y0| on its row
+    assert np.max(np.abs(got - ref)) < 1e-2 * np.max(np.abs(ref))

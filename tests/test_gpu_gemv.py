@@ -518,3 +518,28 @@ def test_non_finite_x_flags_rows(qh, oracle, t, n):
     assert np.array_equal(np.isfinite(got[0]), np.isfinite(ref[0]))
     for k in range(1, n):
         assert cf.rel_l2(got[k], ref[k]) < TOL
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("n", [2, 3, 4])
+def test_gemm_residual_tokens_many_tiles(qh, oracle, t, n):
+    """y += W x for 2-4 tokens through the GEMV kernel with several row tiles per
+    workgroup (9000 rows): each token's rows against the oracle, so a residual
+    value taken from the wrong token or tile would show."""
+    from saient_quartz_amd.host import gemm_grouped_ex_async
+    in_dim, o = 1024, 9000
+    rng = np.random.default_rng(7 * n + t)
+    x = rng.standard_normal((n, in_dim)).astype(np.float32)
+    data = synth.weights(t, o, in_dim, seed=300 + t)
+    y0 = (10 * rng.standard_normal((n, o))).astype(np.float32)
+    w, y, dx = GpuBuf.upload(data), GpuBuf.upload_f32(y0.reshape(-1)), GpuBuf.upload_f32(x.reshape(-1))
+    scratch = GpuBuf.alloc_f32(n * in_dim + n * o)
+    gemm_grouped_ex_async(qh, t, [w.ptr], [dx.ptr], [y.ptr], [n], [o], in_dim, None, accumulate=True,
+                          scratch_ptr=scratch.ptr)
+    check("hip_sync", qh.hip_sync())
+    got = y.download(np.float32)[:n * o].reshape(n, o)
+    wd = oracle.dequant(t, data, o * in_dim).astype(np.float64).reshape(o, in_dim)
+    for i in range(n):
+        ref = wd @ x[i].astype(np.float64) + y0[i]
+        assert cf.rel_l2(got[i], ref) < TOL, (i, cf.rel_l2(got[i], ref))
+        assert np.max(np.abs(got[i] - ref)) < 1e-2 * np.max(np.abs(ref)), i
