@@ -180,6 +180,25 @@ def test_embed_lookup_batched_bit_exact(qh, oracle, t, n):
         assert np.all(got[i, dim:].view(np.float32) == 7.0), i
 
 
+@pytest.mark.parametrize("t", [12, 14])
+def test_embed_lookup_odd_stride_bit_exact(qh, oracle, t):
+    """Rows at an odd float stride (not 16-byte aligned): the 16-values-per-thread
+    decode stores them one float at a time, still bit-exact."""
+    vocab, dim, stride, n = 9, 1024, 1027, 3
+    data = synth.weights(t, vocab, dim, seed=5 + t)
+    dd = GpuBuf.upload(data)
+    toks = [4, 0, 8]
+    out = GpuBuf.upload_f32(np.full(n * stride, 7.0, np.float32))
+    check("embed_batched", qh.hip_embed_lookup_batched_async(out.ptr, stride, dd.ptr, t, (C.c_int * n)(*toks), n,
+                                                             dim, None))
+    sync(qh)
+    ref = oracle.dequant(t, data, vocab * dim).reshape(vocab, dim)
+    got = out.download(np.uint32)[:n * stride].reshape(n, stride)
+    for i in range(n):
+        assert np.array_equal(got[i, :dim], ref[toks[i]].view(np.uint32)), i
+        assert np.all(got[i, dim:].view(np.float32) == 7.0), i
+
+
 def test_embed_lookup_batched_rejects(qh):
     """Negative tokens and a row stride below embed_dim are rejected before any
     launch."""
